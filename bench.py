@@ -1,0 +1,250 @@
+#!/usr/bin/env python3
+"""MoE-layer throughput of the quantized MoE hot path on one MI355X.
+
+Workload: continuous-batching decode over all 36 GPT-OSS-120B MoE layers
+(hidden 2880, 128 experts, top-4, MXFP4 gate/up/down 2880x2880 per expert,
+~60.9 GB of expert weights resident in HBM).  One step = B tokens (one per
+sequence) through the 36 layers; routing is independent per token (router
+N(0,0.02) over RMS-normalised N(0,1) tokens, logits ~N(0,1)).
+
+Timed region: K steps bracketed by torch.cuda.synchronize(); value =
+MoE-layer tokens/s = B * 36 / step time.  A second, event-instrumented pass
+of the same steps measures the average duration of each kernel launch on the
+library's stream; the roofline object is computed for the dominant kernel
+(grouped gate/up GEMV) from its algorithmic bytes per launch.  The CPU
+baseline is the reference-algorithm layer (fp32 activations, AVX2/FMA lane
+order, row-parallel threads) timed on this host on a bounded sample.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for p in (os.path.join(ROOT, "stream-pt_amd"), ROOT):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+HBM_PEAK_GBPS = 8000.0
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--batch", type=int, default=64, help="tokens per decode step (headline)")
+    ap.add_argument("--extra-batches", default="1,8", help="other batch sizes reported beside it")
+    ap.add_argument("--layers", type=int, default=36)
+    ap.add_argument("--seed", type=int, default=3)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    return ap.parse_args()
+
+
+def gate_up_bytes(shp, batch, n_distinct, n_valid):
+    """Algorithmic HBM bytes of one grouped gate/up launch: both matrices and
+    biases of every distinct expert once, the Q8_0 token rows in, the SwiGLU
+    rows out."""
+    H, D = shp.hidden, shp.expert_dim
+    w = n_distinct * (2 * shp.gate_bytes + (2 * D * 4 if shp.biases else 0))
+    return w + batch * (H + H // 32 * 4) + n_valid * D * 4
+
+
+def down_bytes(shp, n_distinct, n_valid):
+    H, D = shp.hidden, shp.expert_dim
+    w = n_distinct * (shp.down_bytes + (H * 4 if shp.biases else 0))
+    return w + n_valid * (D + D // 32 * 4) + n_valid * H * 4
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (got --gpus {args.gpus}); the expert-parallel "
+              "sharding across GPUs is described in DESIGN.md and is not built.", file=sys.stderr)
+        sys.exit(2)
+    import numpy as np
+    import torch
+
+    import spt
+    from spt import workloads as W
+
+    torch.cuda.set_device(0)
+    stream = torch.cuda.current_stream()
+    ctx = spt.Context(0, stream.cuda_stream)
+    shp = W.MoEShape()
+    L = args.layers
+    t0 = time.time()
+    layers = [W.device_layer(ctx, args.seed, l, shp) for l in range(L)]
+    torch.cuda.synchronize()
+    resident = sum(t.numel() * t.element_size() for dl in layers for t in dl.tensors.values())
+    log(f"{L} layers resident: {resident / 1e9:.2f} GB in {time.time() - t0:.1f}s")
+
+    results = {}
+    batches = [args.batch] + [int(b) for b in args.extra_batches.split(",") if b and int(b) != args.batch]
+    for B in batches:
+        xs = [torch.from_numpy(W.x_tokens(args.seed, l, B, shp.hidden)).cuda() for l in range(L)]
+        outs = [torch.empty(B * shp.hidden, dtype=torch.float32, device="cuda") for _ in range(L)]
+
+        def step():
+            for l in range(L):
+                ctx.forward_moe_batch(layers[l].config, layers[l].layer, xs[l], outs[l], B)
+
+        # routing statistics per layer (deterministic: same tokens every step)
+        n_active = torch.zeros(1, dtype=torch.int32, device="cuda")
+        weights = torch.zeros(B * shp.topk, dtype=torch.float32, device="cuda")
+        distinct, valid = [], []
+        for l in range(L):
+            taps = spt.make_taps(n_active=n_active, weights=weights)
+            ctx.forward_moe_batch(layers[l].config, layers[l].layer, xs[l], outs[l], B, taps)
+            torch.cuda.synchronize()
+            distinct.append(int(n_active.item()))
+            valid.append(int((weights > 0).sum().item()))
+        for _ in range(args.warmup):
+            step()
+        torch.cuda.synchronize()
+        log(f"B={B}: warmup done; distinct experts/layer mean {np.mean(distinct):.1f}")
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        wall0 = time.perf_counter()
+        start.record(stream)
+        for _ in range(args.steps):
+            step()
+        end.record(stream)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - wall0
+        ms_step = start.elapsed_time(end) / args.steps
+        # instrumented pass: per-kernel durations from HIP events
+        ctx.enable_timing(True)
+        ctx.read_timing()
+        for _ in range(args.steps):
+            step()
+        kt = ctx.read_timing()
+        ctx.enable_timing(False)
+        gu_ms, gu_n = kt["gate_up"]
+        dn_ms, dn_n = kt["down"]
+        gu_bytes = np.mean([gate_up_bytes(shp, B, d, v) for d, v in zip(distinct, valid)])
+        dn_bytes = np.mean([down_bytes(shp, d, v) for d, v in zip(distinct, valid)])
+        layer_bytes = np.mean([W.moe_algorithmic_bytes(shp, B, d) for d in distinct])
+        res = {
+            "batch": B,
+            "ms_per_step": ms_step,
+            "wall_ms_per_step": wall * 1e3 / args.steps,
+            "moe_layer_tokens_per_s": B * L / (ms_step / 1e3),
+            "decode_tokens_per_s": B / (ms_step / 1e3),
+            "distinct_experts_per_layer": float(np.mean(distinct)),
+            "step_algorithmic_gb": float(layer_bytes * L / 1e9),
+            "step_gbps": float(layer_bytes * L / (ms_step / 1e3) / 1e9),
+            "gate_up_avg_us": gu_ms / gu_n * 1e3,
+            "gate_up_gbps": float(gu_bytes / (gu_ms / gu_n / 1e3) / 1e9),
+            "gate_up_bytes_per_launch": float(gu_bytes),
+            "down_avg_us": dn_ms / dn_n * 1e3,
+            "down_gbps": float(dn_bytes / (dn_ms / dn_n / 1e3) / 1e9),
+            "kernel_ms_per_step": {k: v[0] / args.steps for k, v in kt.items() if v[1]},
+        }
+        results[B] = res
+        log(f"B={B}: {json.dumps(res)}")
+        del xs, outs
+
+    head = results[args.batch]
+    roofline = {
+        "kernel": "grouped MXFP4xQ8_0 gate/up GEMV + SwiGLU (k_mx_gemv<gate_up>)",
+        "bound": "hbm",
+        "achieved": round(head["gate_up_gbps"], 1),
+        "peak": HBM_PEAK_GBPS,
+        "unit": "GB/s",
+        "frac": round(head["gate_up_gbps"] / HBM_PEAK_GBPS, 4),
+        "traffic": None,
+        "bytes_per_launch": head["gate_up_bytes_per_launch"],
+        "avg_launch_us": round(head["gate_up_avg_us"], 2),
+    }
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(args, shp, W)
+    line = {
+        "metric": "MoE-layer tokens/s; decode HBM GB/s vs peak; prefill int8 MFMA util",
+        "value": round(head["moe_layer_tokens_per_s"], 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (seeded MXFP4 experts generated in HBM, N(0,0.02) router/biases, N(0,1) tokens)",
+        "config": {
+            "workload": f"continuous-batching decode step: B={args.batch} tokens through {L} GPT-OSS-120B MoE "
+                        f"layers (hidden 2880, 128 experts, top-4, MXFP4 experts resident in HBM)",
+            "batch": args.batch, "layers": L, "hidden": shp.hidden, "expert_dim": shp.expert_dim,
+            "experts": shp.experts, "topk": shp.topk, "activations": "Q8_0 (int8 dot, fp32 accumulate)",
+            "resident_gb": round(resident / 1e9, 2),
+        },
+        "decode_tokens_per_s": round(head["decode_tokens_per_s"], 1),
+        "step_gbps": round(head["step_gbps"], 1),
+        "by_batch": {str(b): {k: (round(v, 3) if isinstance(v, float) else v) for k, v in r.items()
+                              if k != "kernel_ms_per_step"} for b, r in results.items()},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    ctx.close()
+
+
+def cpu_baseline(args, shp, W):
+    """Reference-algorithm layer on the host: fp32 activations in the
+    reference's AVX2/FMA order, rows split over all cores (the Go worker
+    pool's partition), weights pre-faulted in RAM."""
+    import numpy as np
+
+    from oracle import oracle as O
+
+    B = args.batch
+    threads = os.cpu_count() or 1
+    x = W.x_tokens(args.seed, 0, B, shp.hidden)
+    small = W.host_small_tensors(args.seed, 0, shp)
+    logits = O.route(small["router"], small.get("router_bias"), x, B, shp.hidden, shp.experts)
+    ids = np.concatenate([O.select(logits[t * shp.experts:(t + 1) * shp.experts], shp.topk)[0] for t in range(B)])
+    t0 = time.time()
+    lay = W.host_layer(args.seed, 0, shp, experts=np.unique(ids))
+    log(f"cpu baseline: layer 0 weights for {len(np.unique(ids))} experts generated in {time.time() - t0:.1f}s")
+    O.forward_moe_batch(lay, x, B, q8=False, threads=threads)  # warm (page in)
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        O.forward_moe_batch(lay, x, B, q8=False, threads=threads)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= args.cpu_seconds or reps >= 200:
+            break
+    per_layer = el / reps
+    return {
+        "value": round(B / per_layer, 2),
+        "unit": "tokens/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"layer 0 of the same workload, B={B} tokens, {len(np.unique(ids))} distinct experts, "
+                  f"{reps} repetitions in {el:.1f}s ({per_layer * 1e3:.1f} ms/layer); MoE-layer tokens/s",
+        "cpu": _cpu_model(),
+    }
+
+
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+if __name__ == "__main__":
+    main()

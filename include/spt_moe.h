@@ -1,0 +1,233 @@
+/*
+ * spt_moe.h -- C ABI of libspt_moe.so, the MI355X (gfx950) quantized-MoE
+ * hot path of Stream-PT.
+ *
+ * The entry points are what the reference's forward package would bind over
+ * cgo in place of its Go operators.  Quantized weights live in HBM with the
+ * ggufindex tensor layout unchanged (one spt_tensor per ggufindex.Tensor,
+ * data = device address of the bytes [Range.Start, Range.End)).  Activations
+ * are quantized to GGML Q8_0 on the device and every dot product uses exact
+ * int32 per-block sums with fp32 cross-block accumulation.
+ *
+ * Conventions
+ *   - Every function returns SPT_OK or an SPT_ERR_* code; spt_last_error()
+ *     returns the calling thread's message for the last failure.
+ *   - Arguments are validated before any device work, with the reference's
+ *     rules (shape, type, byte range, overflow, overlap); nothing is launched
+ *     on a validation error.
+ *   - Pointers named *_dev are device pointers; *_host are host pointers.
+ *     Work is enqueued on the context's stream; *_host entry points
+ *     synchronise before returning, the others do not.
+ *   - A context is not safe for concurrent calls (forward/prefill.go:15);
+ *     contexts on different threads are independent.
+ *   - Kernels are not interruptible.  A cancellation flag registered with
+ *     spt_ctx_set_cancel_flag() is checked before each launch of a
+ *     multi-launch entry point (the reference's ctx.Err() checks,
+ *     forward/moe_batch.go:84,146,167); outputs may then be partial, as in the
+ *     reference (forward/q40.go:34,45).
+ */
+#ifndef SPT_MOE_H
+#define SPT_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    SPT_OK = 0,
+    SPT_ERR_INVALID = 1,  /* validation failed; nothing was launched       */
+    SPT_ERR_DEVICE = 2,   /* HIP runtime error, or a context without device */
+    SPT_ERR_NOMEM = 3,    /* device allocation failed                       */
+    SPT_ERR_CANCELED = 4  /* cancellation flag was set                      */
+};
+
+/* GGML type ids used on this path (ggufindex/index.go:540-551). */
+enum {
+    SPT_TYPE_F32 = 0,
+    SPT_TYPE_F16 = 1,
+    SPT_TYPE_Q4_0 = 2,
+    SPT_TYPE_Q8_0 = 8,
+    SPT_TYPE_BF16 = 30,
+    SPT_TYPE_MXFP4 = 39
+};
+
+/* ggufindex.Tensor (ggufindex/index.go:15-26) with the file byte range
+ * replaced by its HBM-resident copy.  shape[0] is the contiguous (input)
+ * dimension, as in GGUF.  An absent optional tensor (bias) has name NULL or
+ * "" and nbytes 0, like the reference's unnamed ggufindex.Tensor{}. */
+typedef struct spt_tensor {
+    const char *name;
+    uint32_t type;
+    uint32_t n_dims;
+    uint64_t shape[4];
+    uint64_t nbytes;
+    const void *data;
+} spt_tensor;
+
+/* The MoE fields of forward.Config (forward/config.go:14-35). */
+typedef struct spt_moe_config {
+    int32_t hidden_dim;
+    int32_t expert_hidden_dim;
+    int32_t num_experts;
+    int32_t num_experts_used;
+} spt_moe_config;
+
+/* The MoE fields of forward.LayerWeights (forward/layer.go:17-37). */
+typedef struct spt_moe_layer {
+    spt_tensor ffn_gate_inp;      /* F32 router [hidden, experts]          */
+    spt_tensor ffn_gate_inp_bias; /* optional [experts]                    */
+    spt_tensor ffn_gate_exps;     /* MXFP4 [hidden, expert_dim, experts]   */
+    spt_tensor ffn_gate_exps_bias;/* optional [expert_dim, experts]        */
+    spt_tensor ffn_up_exps;
+    spt_tensor ffn_up_exps_bias;
+    spt_tensor ffn_down_exps;     /* MXFP4 [expert_dim, hidden, experts]   */
+    spt_tensor ffn_down_exps_bias;/* optional [hidden, experts]            */
+} spt_moe_layer;
+
+/* Optional device buffers a forward call fills with its intermediate stages
+ * (parity taps), and optional injected router logits.  Any pointer may be
+ * NULL.  B = batch, k = experts used, E = experts, H = hidden,
+ * D = expert hidden dim. */
+typedef struct spt_moe_taps {
+    const float *logits_in; /* [B][E]: if set, skip the router and select
+                               from these logits                            */
+    float *logits;          /* [B][E]                                        */
+    int32_t *ids;           /* [B][k]  expert of each selection              */
+    float *weights;         /* [B][k]  softmax weight of each selection      */
+    int32_t *counts;        /* [E]     selections per expert                 */
+    int32_t *offsets;       /* [E+1]   exclusive scan of counts              */
+    int32_t *list;          /* [B*k]   idx = token*k+rank, grouped by expert
+                                       ascending, descending idx inside     */
+    int32_t *active;        /* [E]     experts with a non-empty list         */
+    int32_t *n_active;      /* [1]                                           */
+    void *xq;               /* [B][H/32] Q8_0 blocks (34 B) of x             */
+    float *gate;            /* [B*k][D] gate projection + bias               */
+    float *up;              /* [B*k][D] up projection + bias                 */
+    float *act;             /* [B*k][D] clamped SwiGLU                       */
+    void *actq;             /* [B*k][D/32] Q8_0 blocks of act                */
+    float *results;         /* [B*k][H] down projection + bias               */
+} spt_moe_taps;
+
+/* ---- context ----------------------------------------------------------- */
+
+/* Thread-local message of the last failed call on this thread. */
+const char *spt_last_error(void);
+
+/* Create a context on HIP device `device`, enqueueing on `hip_stream`
+ * (a hipStream_t; NULL creates a stream owned by the context).  device = -1
+ * creates a validation-only context: every entry point validates its
+ * arguments and then fails with SPT_ERR_DEVICE. */
+int spt_ctx_create(int device, void *hip_stream, struct spt_ctx **out);
+int spt_ctx_destroy(struct spt_ctx *ctx);
+int spt_ctx_synchronize(struct spt_ctx *ctx);
+/* Register a host flag polled before each launch; NULL clears it. */
+int spt_ctx_set_cancel_flag(struct spt_ctx *ctx, const volatile int32_t *flag);
+
+/* Per-kernel timing with HIP events recorded on the context's stream around
+ * each launch (measurement instrumentation, off by default).  Kernel kinds: */
+enum {
+    SPT_KERNEL_QUANTIZE = 0, /* activation -> Q8_0                           */
+    SPT_KERNEL_ROUTE = 1,    /* router logits + top-k + per-expert packing   */
+    SPT_KERNEL_GATE_UP = 2,  /* grouped gate/up GEMV + bias + SwiGLU        */
+    SPT_KERNEL_DOWN = 3,     /* grouped down GEMV + bias                      */
+    SPT_KERNEL_COMBINE = 4,  /* weighted combine                              */
+    SPT_KERNEL_Q40 = 5,      /* Q4_0 GEMV / small GEMM                        */
+    SPT_KERNEL_KINDS = 6
+};
+int spt_ctx_enable_timing(struct spt_ctx *ctx, int enable);
+/* Synchronise, then write the summed milliseconds and launch counts of each
+ * kind since the last read (arrays of SPT_KERNEL_KINDS) and reset them. */
+int spt_ctx_read_timing(struct spt_ctx *ctx, double *total_ms, int64_t *launches);
+
+/* ---- device memory and weight residency -------------------------------- */
+
+int spt_alloc(struct spt_ctx *ctx, uint64_t nbytes, void **out_dev);
+int spt_free(struct spt_ctx *ctx, void *dev);
+int spt_copy_h2d(struct spt_ctx *ctx, void *dst_dev, const void *src_host, uint64_t nbytes);
+int spt_copy_d2h(struct spt_ctx *ctx, void *dst_host, const void *src_dev, uint64_t nbytes);
+
+/* Copy a tensor's bytes to HBM unchanged and set t->data; replaces the
+ * ggufmap mmap windows (ggufmap/mmap_linux.go:210-291,391-555).  Free with
+ * spt_free(ctx, (void *)t->data). */
+int spt_tensor_upload(struct spt_ctx *ctx, spt_tensor *t, const void *src_host);
+
+/* ---- operators ----------------------------------------------------------- */
+
+/* x[n] f32 -> n/32 GGML Q8_0 blocks (fp16 d, 32 int8), n % 32 == 0.
+ * No reference counterpart: the activation quantizer of this path. */
+int spt_quantize_q8_0(struct spt_ctx *ctx, const float *x_dev, int64_t n, void *out_dev);
+
+/* forward.MulQ40Into (forward/q40.go:128-133): y = W x for a Q4_0 [in, out]
+ * matrix.  x_len/y_len are element counts (len(x), len(y)). */
+int spt_mul_q40_into(struct spt_ctx *ctx, const spt_tensor *w, const float *x_dev,
+                     int64_t x_len, float *y_dev, int64_t y_len);
+
+/* forward.MulQ40BatchInto (forward/q40.go:135-198): batch consecutive
+ * vectors, y[b*out + row]. */
+int spt_mul_q40_batch_into(struct spt_ctx *ctx, const spt_tensor *w, const float *x_dev,
+                           int64_t x_len, float *y_dev, int64_t y_len, int64_t batch);
+
+/* Host-slice form of MulQ40BatchInto for a cgo caller holding Go slices. */
+int spt_mul_q40_batch_into_host(struct spt_ctx *ctx, const spt_tensor *w, const float *x_host,
+                                int64_t x_len, float *y_host, int64_t y_len, int64_t batch);
+
+/* forward.mulMoEBatchExpert (forward/mxfp4_batch.go:29-53) for one expert of
+ * an MXFP4 [in, out, experts] tensor with consecutive (not gathered) rows:
+ * y[t*out + row] = dot(W_e[row], x[t*in:]) + bias_e[row], t < batch.
+ * bias is an optional [out, experts] tensor. */
+int spt_mul_mxfp4_expert(struct spt_ctx *ctx, const spt_tensor *w, const spt_tensor *bias,
+                         int32_t expert, const float *x_dev, int64_t x_len, float *y_dev,
+                         int64_t y_len, int64_t batch);
+
+/* forward.routeMoEBatch (forward/moe_batch.go:221-303, vector_amd64.go:11-56):
+ * logits[t*E + e] = router_e . x_t + bias[e], in the reference's fp32
+ * accumulation order. */
+int spt_route_moe_batch(struct spt_ctx *ctx, const spt_tensor *router, const spt_tensor *bias,
+                        const float *x_dev, int64_t batch, float *logits_dev);
+
+/* forward.forwardMoE (forward/moe.go:28-64): one token. */
+int spt_forward_moe(struct spt_ctx *ctx, const spt_moe_config *cfg, const spt_moe_layer *lw,
+                    const float *x_dev, int64_t x_len, float *out_dev, int64_t out_len);
+
+/* forward.forwardMoEBatch (forward/moe_batch.go:76-194): router, top-k
+ * softmax, per-expert grouping, gate/up, clamped SwiGLU, down and the
+ * weighted combine for batch tokens of x [batch][hidden] into out.
+ * x and out must not overlap. */
+int spt_forward_moe_batch(struct spt_ctx *ctx, const spt_moe_config *cfg,
+                          const spt_moe_layer *lw, const float *x_dev, int64_t x_len,
+                          float *out_dev, int64_t out_len, int64_t batch);
+
+/* forwardMoEBatch with parity taps / injected logits (taps may be NULL). */
+int spt_forward_moe_batch_ex(struct spt_ctx *ctx, const spt_moe_config *cfg,
+                             const spt_moe_layer *lw, const float *x_dev, int64_t x_len,
+                             float *out_dev, int64_t out_len, int64_t batch,
+                             const spt_moe_taps *taps);
+
+/* Host-slice form of forwardMoEBatch for a cgo caller holding Go slices. */
+int spt_forward_moe_batch_host(struct spt_ctx *ctx, const spt_moe_config *cfg,
+                               const spt_moe_layer *lw, const float *x_host, int64_t x_len,
+                               float *out_host, int64_t out_len, int64_t batch);
+
+/* Parity tap: exact int32 per-block sums of rows [0, rows) of one weight
+ * matrix against one Q8_0 activation vector, computed by the same device
+ * decode as the GEMV kernels.  w is MXFP4 [in, out, experts] (expert used) or
+ * Q4_0 [in, out] (expert must be 0); xq_dev holds in/32 Q8_0 blocks;
+ * sums_dev is [rows][in/32] int32. */
+int spt_block_sums(struct spt_ctx *ctx, const spt_tensor *w, int32_t expert,
+                   const void *xq_dev, int64_t rows, int32_t *sums_dev);
+
+/* Synthetic MXFP4 bytes for blocks [first_block, first_block + nblocks) of a
+ * tensor, written at dst_dev (block g at dst + (g - first_block)*17): E8M0 =
+ * scale_lo + h(3g) mod (scale_hi - scale_lo + 1), nibbles = bytes of h(3g+1),
+ * h(3g+2), h = SplitMix64 finaliser over key + i*0x9E3779B97F4A7C15.  Used to
+ * fill HBM with benchmark weights without a host round trip. */
+int spt_synth_mxfp4(struct spt_ctx *ctx, void *dst_dev, uint64_t key, uint64_t first_block,
+                    uint64_t nblocks, int32_t scale_lo, int32_t scale_hi);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,210 @@
+// spt_device.h -- gfx950 device helpers shared by the quantized-MoE kernels.
+//
+// Block formats (GGUF layout, unchanged in HBM):
+//   MXFP4 (type 39, 17 B): byte 0 = E8M0 exponent e, bytes 1..16 = 32 E2M1
+//     codes; element i = low nibble of byte 1+i, element i+16 = high nibble
+//     (forward/mxfp4.go:52-59).
+//   Q4_0 (type 2, 18 B): fp16 d, then 16 bytes of nibbles n, w = (n-8)*d,
+//     same element order (forward/quant_portable.go:66-72).
+//   Q8_0 (type 8, 34 B): fp16 d, then 32 int8 (forward/q80.go:15-18).
+//
+// Activations are held on device as split Q8_0: int8 codes [rows][K] and
+// fp32 scales [rows][K/32] (the fp16 d widened exactly), so the 32 codes of a
+// block are 8 aligned dwords that feed v_dot4_i32_i8 directly.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace spt {
+
+constexpr int kMxBlock = 17;
+constexpr int kQ40Block = 18;
+constexpr int kQ80Block = 34;
+
+// gfx9 raw buffer descriptor word 3 (DATA_FORMAT=32, no swizzle).
+constexpr int kRsrcWord3 = 0x00020000;
+
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+
+// A bounds-checked view of `nbytes` bytes at `p`: the descriptor base is p
+// rounded down to 4 bytes and `lead` (0..3) is p's offset inside it, so every
+// dword load stays aligned; dwords wholly past the end read as zero.
+struct ByteView {
+    rsrc_t r;
+    uint32_t lead;
+};
+
+__device__ inline ByteView make_view(const void *p, uint64_t nbytes) {
+    uintptr_t a = reinterpret_cast<uintptr_t>(p);
+    uint32_t lead = static_cast<uint32_t>(a & 3u);
+    uint64_t nrec = (nbytes + lead + 3u) & ~uint64_t(3);
+    ByteView v;
+    v.r = __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void *>(a - lead), (short)0,
+                                            (int)(uint32_t)nrec, kRsrcWord3);
+    v.lead = lead;
+    return v;
+}
+
+// Five consecutive aligned dwords covering bytes [pos, pos+17) of the view;
+// *o = pos & 3 is the offset of byte `pos` inside the first dword.
+__device__ inline void load_block5(const ByteView &v, uint32_t pos, uint32_t d[5], uint32_t *o) {
+    uint32_t p = pos + v.lead;
+    uint32_t base = p & ~3u;
+    *o = p & 3u;
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    u32x4 q = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(v.r, base, 0, 0));
+    d[0] = q.x;
+    d[1] = q.y;
+    d[2] = q.z;
+    d[3] = q.w;
+    d[4] = __builtin_amdgcn_raw_buffer_load_b32(v.r, base + 16, 0, 0);
+}
+
+// ---- fp16 -----------------------------------------------------------------
+__device__ inline float f16_bits_to_f32(uint32_t h) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h)));
+}
+
+// Round-to-nearest-even fp32 -> fp16 bits; NaN becomes 0x7e00 | sign.
+__device__ inline uint16_t f32_to_f16_bits(float f) {
+    if (f != f) return static_cast<uint16_t>(((__float_as_uint(f) >> 16) & 0x8000u) | 0x7e00u);
+    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+}
+
+// forward/layer.go:279-303 (readFloatVector) element decode: F32, F16, BF16.
+__device__ inline float bias_at(const void *p, int type, uint64_t i) {
+    if (!p) return 0.0f;
+    if (type == 1) return f16_bits_to_f32(reinterpret_cast<const uint16_t *>(p)[i]);
+    if (type == 30) return __uint_as_float(uint32_t(reinterpret_cast<const uint16_t *>(p)[i]) << 16);
+    return reinterpret_cast<const float *>(p)[i];
+}
+
+// ---- MXFP4 block decode ------------------------------------------------------
+// LUT2 = 2*E2M1 = {0,1,2,3,4,6,8,12} and their negatives: exact int8 values,
+// so sdot4 against Q8_0 codes gives the exact block sum; the block scale of
+// the integer form is 2^(e-128) (half the reference's 2^(e-127)).
+constexpr uint32_t kPosLo = 0x03020100u, kPosHi = 0x0C080604u;
+constexpr uint32_t kNegLo = 0xFDFEFF00u, kNegHi = 0xF4F8FAFCu;
+
+struct MxDecoded {
+    uint32_t lo[4];  // int8x4: elements 4k..4k+3
+    uint32_t hi[4];  // int8x4: elements 16+4k..16+4k+3
+    uint32_t e;      // E8M0 byte
+};
+
+// Eight nibbles of one dword -> two int8x4 words through v_perm_b32 lookups:
+// magnitude from the positive and negative tables by (nibble & 7), then a
+// byte select by the sign bit (bit 3 of the nibble).
+__device__ inline void mx_lut(uint32_t w, uint32_t *lo, uint32_t *hi) {
+    uint32_t il = w & 0x07070707u;
+    uint32_t ih = (w >> 4) & 0x07070707u;
+    uint32_t pl = __builtin_amdgcn_perm(kPosHi, kPosLo, il);
+    uint32_t nl = __builtin_amdgcn_perm(kNegHi, kNegLo, il);
+    uint32_t ph = __builtin_amdgcn_perm(kPosHi, kPosLo, ih);
+    uint32_t nh = __builtin_amdgcn_perm(kNegHi, kNegLo, ih);
+    uint32_t sl = ((w >> 1) & 0x04040404u) | 0x03020100u;
+    uint32_t sh = ((w >> 5) & 0x04040404u) | 0x03020100u;
+    *lo = __builtin_amdgcn_perm(nl, pl, sl);
+    *hi = __builtin_amdgcn_perm(nh, ph, sh);
+}
+
+// d[0..4] from load_block5 at the block's first byte, o = its offset.
+__device__ inline void mx_decode(const uint32_t d[5], uint32_t o, MxDecoded &m) {
+    uint32_t sel = 0x04030201u + o * 0x01010101u;  // bytes o+1..o+4
+    m.e = __builtin_amdgcn_ubfe(d[0], o * 8u, 8u);
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        uint32_t w = __builtin_amdgcn_perm(d[k + 1], d[k], sel);
+        mx_lut(w, &m.lo[k], &m.hi[k]);
+    }
+}
+
+// Exact int32 block sum of a decoded MXFP4 block against 8 code dwords.
+__device__ inline int32_t mx_isum(const MxDecoded &m, const uint32_t q[8]) {
+    int32_t s = 0;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        s = __builtin_amdgcn_sdot4((int)m.lo[k], (int)q[k], s, false);
+        s = __builtin_amdgcn_sdot4((int)m.hi[k], (int)q[k + 4], s, false);
+    }
+    return s;
+}
+
+// d_x * 2^(e-128); e = 255 keeps the reference's +Inf block scale
+// (forward/mxfp4.go:23: float32(math.Ldexp(1, 128)) = +Inf).
+__device__ inline float mx_block_scale(float dx, uint32_t e) {
+    return e == 255u ? dx * __builtin_inff() : __builtin_ldexpf(dx, (int)e - 128);
+}
+
+// ---- Q4_0 block decode ---------------------------------------------------------
+struct Q40Decoded {
+    uint32_t lo[4];  // nibbles 0..15 (unsigned) of elements 4k..4k+3
+    uint32_t hi[4];  // nibbles of elements 16+4k..
+    float d;         // fp16 scale widened
+};
+
+// o is 0 or 2 (Q4_0 rows are 2-byte aligned).
+__device__ inline void q40_decode(const uint32_t d[5], uint32_t o, Q40Decoded &m) {
+    uint32_t sel = 0x05040302u + o * 0x01010101u;  // bytes o+2..o+5
+    m.d = f16_bits_to_f32(__builtin_amdgcn_ubfe(d[0], o * 8u, 16u));
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        uint32_t w = __builtin_amdgcn_perm(d[k + 1], d[k], sel);
+        m.lo[k] = w & 0x0F0F0F0Fu;
+        m.hi[k] = (w >> 4) & 0x0F0F0F0Fu;
+    }
+}
+
+// sum (n-8)*q = sum n*q - 8*sum q (n in 0..15 is a non-negative int8).
+__device__ inline int32_t q40_isum(const Q40Decoded &m, const uint32_t q[8], int32_t sumq) {
+    int32_t s = 0;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        s = __builtin_amdgcn_sdot4((int)m.lo[k], (int)q[k], s, false);
+        s = __builtin_amdgcn_sdot4((int)m.hi[k], (int)q[k + 4], s, false);
+    }
+    return s - 8 * sumq;
+}
+
+// ---- Q8_0 quantization of one block of 32 ---------------------------------------
+// GGML quantize_row_q8_0 reference rule: d = amax/127 (IEEE division),
+// id = d ? 1/d : 0, q = roundf(x*id) half away from zero; a NaN element makes
+// d NaN; a NaN product gives code 0; codes clamp to [-127, 127].
+__device__ inline void q8_quantize32(const float v[32], uint32_t codes[8], uint16_t *dbits) {
+    float amax = 0.0f;
+    bool nan = false;
+#pragma unroll
+    for (int i = 0; i < 32; i++) {
+        float a = __builtin_fabsf(v[i]);
+        nan |= (a != a);
+        amax = a > amax ? a : amax;
+    }
+    float d = nan ? __builtin_nanf("") : amax / 127.0f;
+    float id = (d != 0.0f) ? 1.0f / d : 0.0f;
+    *dbits = f32_to_f16_bits(d);
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            float r = __builtin_roundf(v[4 * k + i] * id);
+            int q = (r != r) ? 0 : (r > 127.0f ? 127 : (r < -127.0f ? -127 : (int)r));
+            word |= (uint32_t)(q & 0xff) << (8 * i);
+        }
+        codes[k] = word;
+    }
+}
+
+// ---- clamped SwiGLU (forward/moe.go:195-199) ------------------------------------
+// Go's min/max return NaN when either operand is NaN; the comparisons below
+// keep that (a NaN gate or up propagates).
+__device__ inline float swiglu(float gate, float up) {
+    float g = (gate > 7.0f) ? 7.0f : gate;
+    float u = (up > 7.0f) ? 7.0f : up;
+    u = (u < -7.0f) ? -7.0f : u;
+    float e = static_cast<float>(exp(static_cast<double>(-1.702f * g)));
+    return g / (1.0f + e) * (u + 1.0f);
+}
+
+}  // namespace spt

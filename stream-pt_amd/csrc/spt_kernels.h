@@ -1,0 +1,75 @@
+// spt_kernels.h -- host-side launchers of the gfx950 kernels (internal).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace spt {
+
+constexpr int kMaxTopK = 16;
+constexpr int kMaxExperts = 1024;
+constexpr int kMaxSelections = 4096;
+
+struct SelectOut {
+    int32_t *ids;
+    float *weights;
+    int32_t *counts;
+    int32_t *offsets;
+    int32_t *list;
+    int32_t *active;
+    int32_t *n_active;
+};
+
+enum GemvMode { kGateUp = 0, kDown = 1, kRows = 2 };
+
+struct MxGemvArgs {
+    const uint8_t *w[2];     // MXFP4 expert tensors (gate, up) or (down) or (w)
+    uint64_t expert_bytes;   // bytes of one expert matrix
+    int rows;                // output rows per expert (= bias dim)
+    int nb;                  // input blocks of 32 per row
+    const void *bias[2];     // optional [rows][experts] biases
+    int bias_type[2];
+    const int8_t *codes;     // activation Q8_0 codes [*][nb*32]
+    const float *scales;     // activation Q8_0 scales [*][nb]
+    const int32_t *active;   // grouped modes: packed expert lists
+    const int32_t *n_active;
+    const int32_t *offsets;
+    const int32_t *list;
+    int topk;
+    int expert;              // kRows: the expert
+    int ntok;                // kRows: tokens 0..ntok-1
+    float *out;
+    float *tap[2];
+};
+
+struct Q40Args {
+    const uint8_t *w;
+    uint64_t nbytes;
+    int rows;
+    int nb;
+    const int8_t *codes;
+    const float *scales;
+    const int32_t *sumq;
+    int ntok;
+    float *y;
+};
+
+hipError_t launch_quantize(hipStream_t s, const float *x, int64_t nblocks, int8_t *codes,
+                           float *scales, int32_t *sumq, uint8_t *blocks34);
+hipError_t launch_route(hipStream_t s, const float *router, const void *bias, int bias_type,
+                        const float *x, int batch, int hidden, int experts, float *logits,
+                        int topk, bool select, const SelectOut &o, uint32_t *counter);
+hipError_t launch_select(hipStream_t s, const float *logits, int batch, int experts, int topk,
+                         const SelectOut &o);
+hipError_t launch_mx_gemv(hipStream_t s, GemvMode mode, const MxGemvArgs &a, int slots);
+hipError_t launch_q40_gemv(hipStream_t s, const Q40Args &a);
+hipError_t launch_combine(hipStream_t s, const float *results, const float *weights, int batch,
+                          int topk, int hidden, float *out);
+hipError_t launch_block_sums_mx(hipStream_t s, const uint8_t *w, uint64_t nbytes, int rows, int nb,
+                                const uint8_t *xq34, int32_t *sums);
+hipError_t launch_block_sums_q40(hipStream_t s, const uint8_t *w, uint64_t nbytes, int rows,
+                                 int nb, const uint8_t *xq34, int32_t *sums);
+hipError_t launch_synth_mxfp4(hipStream_t s, uint8_t *dst, uint64_t key, uint64_t first_block,
+                              uint64_t nblocks, int scale_lo, int scale_hi);
+
+}  // namespace spt

@@ -1,0 +1,260 @@
+"""spt -- Python binding of libspt_moe.so (include/spt_moe.h).
+
+The operator names and argument meanings follow Stream-PT's forward package
+(MulQ40Into, MulQ40BatchInto, forwardMoE, forwardMoEBatch, routeMoEBatch,
+mulMoEBatchExpert); tensors are passed as device memory (torch tensors on a
+ROCm device) plus ggufindex-style descriptors.  Errors raise SptError with
+the library's message.  There is no fallback: if the HIP library is missing
+the import fails.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+__all__ = ["SptError", "Tensor", "MoEConfig", "MoELayer", "MoETaps", "Context", "lib", "LIB_PATH",
+           "TYPE_F32", "TYPE_F16", "TYPE_Q4_0", "TYPE_Q8_0", "TYPE_BF16", "TYPE_MXFP4",
+           "OK", "ERR_INVALID", "ERR_DEVICE", "ERR_NOMEM", "ERR_CANCELED"]
+
+_PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.path.join(_PKG_DIR, "libspt_moe.so")
+
+OK, ERR_INVALID, ERR_DEVICE, ERR_NOMEM, ERR_CANCELED = 0, 1, 2, 3, 4
+TYPE_F32, TYPE_F16, TYPE_Q4_0, TYPE_Q8_0, TYPE_BF16, TYPE_MXFP4 = 0, 1, 2, 8, 30, 39
+
+EXPORTED = (
+    "spt_last_error", "spt_ctx_create", "spt_ctx_destroy", "spt_ctx_synchronize",
+    "spt_ctx_set_cancel_flag", "spt_alloc", "spt_free", "spt_copy_h2d", "spt_copy_d2h",
+    "spt_tensor_upload", "spt_quantize_q8_0", "spt_mul_q40_into", "spt_mul_q40_batch_into",
+    "spt_mul_q40_batch_into_host", "spt_mul_mxfp4_expert", "spt_route_moe_batch",
+    "spt_forward_moe", "spt_forward_moe_batch", "spt_forward_moe_batch_ex",
+    "spt_forward_moe_batch_host", "spt_block_sums", "spt_synth_mxfp4",
+    "spt_ctx_enable_timing", "spt_ctx_read_timing",
+)
+KERNEL_KINDS = ("quantize", "route", "gate_up", "down", "combine", "q40")
+
+
+class SptError(RuntimeError):
+    def __init__(self, code: int, message: str):
+        super().__init__(f"spt error {code}: {message}")
+        self.code = code
+        self.message = message
+
+
+class Tensor(C.Structure):
+    """spt_tensor: ggufindex.Tensor with its HBM-resident bytes."""
+    _fields_ = [("name", C.c_char_p), ("type", C.c_uint32), ("n_dims", C.c_uint32),
+                ("shape", C.c_uint64 * 4), ("nbytes", C.c_uint64), ("data", C.c_void_p)]
+
+    @classmethod
+    def make(cls, name, typ, shape, data_ptr, nbytes):
+        t = cls()
+        t.name = name.encode() if name else None
+        t.type = typ
+        t.n_dims = len(shape)
+        for i, s in enumerate(shape):
+            t.shape[i] = int(s)
+        t.nbytes = int(nbytes)
+        t.data = int(data_ptr) if data_ptr else None
+        return t
+
+    @classmethod
+    def absent(cls):
+        return cls()
+
+
+class MoEConfig(C.Structure):
+    _fields_ = [("hidden_dim", C.c_int32), ("expert_hidden_dim", C.c_int32),
+                ("num_experts", C.c_int32), ("num_experts_used", C.c_int32)]
+
+
+class MoELayer(C.Structure):
+    _fields_ = [(n, Tensor) for n in (
+        "ffn_gate_inp", "ffn_gate_inp_bias", "ffn_gate_exps", "ffn_gate_exps_bias",
+        "ffn_up_exps", "ffn_up_exps_bias", "ffn_down_exps", "ffn_down_exps_bias")]
+
+
+class MoETaps(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in (
+        "logits_in", "logits", "ids", "weights", "counts", "offsets", "list", "active",
+        "n_active", "xq", "gate", "up", "act", "actq", "results")]
+
+
+_lib = None
+
+
+def lib():
+    """Load libspt_moe.so; raise if it was not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(f"{LIB_PATH} is missing: run __graft_entry__.build() first")
+    L = C.CDLL(LIB_PATH)
+    vp, i64, i32, u64 = C.c_void_p, C.c_int64, C.c_int32, C.c_uint64
+    T = C.POINTER(Tensor)
+    sig = {
+        "spt_last_error": ([], C.c_char_p),
+        "spt_ctx_create": ([C.c_int, vp, C.POINTER(vp)], C.c_int),
+        "spt_ctx_destroy": ([vp], C.c_int),
+        "spt_ctx_synchronize": ([vp], C.c_int),
+        "spt_ctx_set_cancel_flag": ([vp, vp], C.c_int),
+        "spt_alloc": ([vp, u64, C.POINTER(vp)], C.c_int),
+        "spt_free": ([vp, vp], C.c_int),
+        "spt_copy_h2d": ([vp, vp, vp, u64], C.c_int),
+        "spt_copy_d2h": ([vp, vp, vp, u64], C.c_int),
+        "spt_tensor_upload": ([vp, T, vp], C.c_int),
+        "spt_quantize_q8_0": ([vp, vp, i64, vp], C.c_int),
+        "spt_mul_q40_into": ([vp, T, vp, i64, vp, i64], C.c_int),
+        "spt_mul_q40_batch_into": ([vp, T, vp, i64, vp, i64, i64], C.c_int),
+        "spt_mul_q40_batch_into_host": ([vp, T, vp, i64, vp, i64, i64], C.c_int),
+        "spt_mul_mxfp4_expert": ([vp, T, T, i32, vp, i64, vp, i64, i64], C.c_int),
+        "spt_route_moe_batch": ([vp, T, T, vp, i64, vp], C.c_int),
+        "spt_forward_moe": ([vp, C.POINTER(MoEConfig), C.POINTER(MoELayer), vp, i64, vp, i64], C.c_int),
+        "spt_forward_moe_batch": ([vp, C.POINTER(MoEConfig), C.POINTER(MoELayer), vp, i64, vp, i64, i64],
+                                  C.c_int),
+        "spt_forward_moe_batch_ex": ([vp, C.POINTER(MoEConfig), C.POINTER(MoELayer), vp, i64, vp, i64, i64,
+                                      C.POINTER(MoETaps)], C.c_int),
+        "spt_forward_moe_batch_host": ([vp, C.POINTER(MoEConfig), C.POINTER(MoELayer), vp, i64, vp, i64,
+                                        i64], C.c_int),
+        "spt_block_sums": ([vp, T, i32, vp, i64, vp], C.c_int),
+        "spt_synth_mxfp4": ([vp, vp, u64, u64, u64, i32, i32], C.c_int),
+        "spt_ctx_enable_timing": ([vp, C.c_int], C.c_int),
+        "spt_ctx_read_timing": ([vp, C.POINTER(C.c_double), C.POINTER(C.c_int64)], C.c_int),
+    }
+    for name, (args, res) in sig.items():
+        f = getattr(L, name)
+        f.argtypes = args
+        f.restype = res
+    _lib = L
+    return L
+
+
+def _ptr(t):
+    """Device or host address of a torch tensor / numpy array / int / None."""
+    if t is None:
+        return None
+    if isinstance(t, int):
+        return t
+    if hasattr(t, "data_ptr"):
+        return t.data_ptr()
+    if hasattr(t, "ctypes"):
+        return t.ctypes.data
+    raise TypeError(f"cannot take the address of {type(t)}")
+
+
+def _numel(t):
+    if hasattr(t, "numel") and callable(t.numel):
+        return int(t.numel())
+    return int(t.size)
+
+
+def _check(rc):
+    if rc != OK:
+        raise SptError(rc, lib().spt_last_error().decode(errors="replace"))
+
+
+def _ref(t):
+    return C.byref(t) if t is not None else None
+
+
+class Context:
+    """An spt_ctx: one HIP stream, one scratch arena (device=-1: validation
+    only)."""
+
+    def __init__(self, device: int = 0, stream=None):
+        h = C.c_void_p()
+        _check(lib().spt_ctx_create(device, stream, C.byref(h)))
+        self.handle = h
+        self.device = device
+        self._cancel = None
+
+    def close(self):
+        if self.handle:
+            lib().spt_ctx_destroy(self.handle)
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def synchronize(self):
+        _check(lib().spt_ctx_synchronize(self.handle))
+
+    def enable_timing(self, enable: bool = True):
+        _check(lib().spt_ctx_enable_timing(self.handle, 1 if enable else 0))
+
+    def read_timing(self) -> dict:
+        """{kind: (total_ms, launches)} since the last read."""
+        ms = (C.c_double * len(KERNEL_KINDS))()
+        n = (C.c_int64 * len(KERNEL_KINDS))()
+        _check(lib().spt_ctx_read_timing(self.handle, ms, n))
+        return {k: (ms[i], n[i]) for i, k in enumerate(KERNEL_KINDS)}
+
+    def set_cancel_flag(self, flag_array):
+        """flag_array: a host int32 numpy array of one element, or None."""
+        self._cancel = flag_array
+        _check(lib().spt_ctx_set_cancel_flag(self.handle, _ptr(flag_array)))
+
+    # -- operators -----------------------------------------------------------
+    def quantize_q8_0(self, x, out):
+        _check(lib().spt_quantize_q8_0(self.handle, _ptr(x), _numel(x), _ptr(out)))
+
+    def mul_q40_into(self, w: Tensor, x, y):
+        _check(lib().spt_mul_q40_into(self.handle, C.byref(w), _ptr(x), _numel(x), _ptr(y), _numel(y)))
+
+    def mul_q40_batch_into(self, w: Tensor, x, y, batch: int):
+        _check(lib().spt_mul_q40_batch_into(self.handle, C.byref(w), _ptr(x), _numel(x), _ptr(y),
+                                            _numel(y), batch))
+
+    def mul_q40_batch_into_host(self, w: Tensor, x, y, batch: int):
+        _check(lib().spt_mul_q40_batch_into_host(self.handle, C.byref(w), _ptr(x), _numel(x), _ptr(y),
+                                                 _numel(y), batch))
+
+    def mul_mxfp4_expert(self, w: Tensor, bias, expert: int, x, y, batch: int):
+        b = bias if bias is not None else Tensor.absent()
+        _check(lib().spt_mul_mxfp4_expert(self.handle, C.byref(w), C.byref(b), expert, _ptr(x), _numel(x),
+                                          _ptr(y), _numel(y), batch))
+
+    def route_moe_batch(self, router: Tensor, bias, x, batch: int, logits):
+        b = bias if bias is not None else Tensor.absent()
+        _check(lib().spt_route_moe_batch(self.handle, C.byref(router), C.byref(b), _ptr(x), batch,
+                                         _ptr(logits)))
+
+    def forward_moe(self, cfg: MoEConfig, lw: MoELayer, x, out):
+        _check(lib().spt_forward_moe(self.handle, _ref(cfg), _ref(lw), _ptr(x), _numel(x), _ptr(out),
+                                     _numel(out)))
+
+    def forward_moe_batch(self, cfg: MoEConfig, lw: MoELayer, x, out, batch: int, taps: MoETaps = None):
+        if taps is None:
+            rc = lib().spt_forward_moe_batch(self.handle, _ref(cfg), _ref(lw), _ptr(x), _numel(x), _ptr(out),
+                                             _numel(out), batch)
+        else:
+            rc = lib().spt_forward_moe_batch_ex(self.handle, _ref(cfg), _ref(lw), _ptr(x), _numel(x),
+                                                _ptr(out), _numel(out), batch, C.byref(taps))
+        _check(rc)
+
+    def forward_moe_batch_host(self, cfg: MoEConfig, lw: MoELayer, x, out, batch: int):
+        _check(lib().spt_forward_moe_batch_host(self.handle, _ref(cfg), _ref(lw), _ptr(x), _numel(x),
+                                                _ptr(out), _numel(out), batch))
+
+    def block_sums(self, w: Tensor, expert: int, xq, rows: int, sums):
+        _check(lib().spt_block_sums(self.handle, C.byref(w), expert, _ptr(xq), rows, _ptr(sums)))
+
+    def synth_mxfp4(self, dst, key: int, first_block: int, nblocks: int, scale_lo=118, scale_hi=124):
+        _check(lib().spt_synth_mxfp4(self.handle, _ptr(dst), key, first_block, nblocks, scale_lo, scale_hi))
+
+
+def make_taps(**bufs) -> MoETaps:
+    taps = MoETaps()
+    for name, t in bufs.items():
+        setattr(taps, name, _ptr(t))
+    return taps

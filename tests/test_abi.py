@@ -1,0 +1,159 @@
+"""CPU tests of the C ABI: every symbol include/spt_moe.h declares is
+exported, and argument validation follows the reference's rules (a
+validation-only context, device -1, runs every check without a GPU).
+
+Validation cases: tests/testdata/forward/moe_batch_test.go:170-237
+(TestForwardMoEBatchValidation) and q40_stream_test.go:107-151."""
+import ctypes as C
+import os
+import re
+
+import numpy as np
+import pytest
+
+import spt
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared():
+    text = open(os.path.join(ROOT, "include", "spt_moe.h")).read()
+    return sorted(set(re.findall(r"\b(spt_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_symbols_exported():
+    L = spt.lib()
+    declared = _declared()
+    assert len(declared) >= 20
+    for name in declared:
+        assert hasattr(L, name), f"{name} not exported"
+    assert set(declared) == set(spt.EXPORTED)
+
+
+@pytest.fixture()
+def vctx():
+    ctx = spt.Context(-1)
+    yield ctx
+    ctx.close()
+
+
+def _moe_descriptors(H=32, D=64, E=4, k=2, biases=True):
+    """Descriptors with fake (never dereferenced) device addresses."""
+    base = 0x10000000
+    lw = spt.MoELayer()
+    lw.ffn_gate_inp = spt.Tensor.make("router", spt.TYPE_F32, [H, E], base, H * E * 4)
+    lw.ffn_gate_exps = spt.Tensor.make("gate", spt.TYPE_MXFP4, [H, D, E], base, H // 32 * 17 * D * E)
+    lw.ffn_up_exps = spt.Tensor.make("up", spt.TYPE_MXFP4, [H, D, E], base, H // 32 * 17 * D * E)
+    lw.ffn_down_exps = spt.Tensor.make("down", spt.TYPE_MXFP4, [D, H, E], base, D // 32 * 17 * H * E)
+    if biases:
+        lw.ffn_gate_inp_bias = spt.Tensor.make("router.bias", spt.TYPE_F32, [E], base, E * 4)
+        lw.ffn_gate_exps_bias = spt.Tensor.make("gate.bias", spt.TYPE_F32, [D, E], base, D * E * 4)
+        lw.ffn_up_exps_bias = spt.Tensor.make("up.bias", spt.TYPE_F32, [D, E], base, D * E * 4)
+        lw.ffn_down_exps_bias = spt.Tensor.make("down.bias", spt.TYPE_F32, [H, E], base, H * E * 4)
+    cfg = spt.MoEConfig()
+    cfg.hidden_dim, cfg.expert_hidden_dim, cfg.num_experts, cfg.num_experts_used = H, D, E, k
+    return cfg, lw
+
+
+def _call_moe(ctx, cfg, lw, x_ptr, x_len, out_ptr, out_len, batch):
+    return spt.lib().spt_forward_moe_batch(ctx.handle if ctx else None, C.byref(cfg) if cfg else None,
+                                           C.byref(lw) if lw else None, x_ptr, x_len, out_ptr, out_len, batch)
+
+
+X, OUT = 0x20000000, 0x30000000
+
+
+def test_moe_valid_arguments_reach_the_device(vctx):
+    cfg, lw = _moe_descriptors()
+    rc = _call_moe(vctx, cfg, lw, X, 64, OUT, 64, 2)
+    assert rc == spt.ERR_DEVICE and b"validation-only" in spt.lib().spt_last_error()
+
+
+CASES = {
+    "zero hidden": lambda c, w: setattr(c, "hidden_dim", 0),
+    "negative expert dimension": lambda c, w: setattr(c, "expert_hidden_dim", -1),
+    "unaligned expert dimension": lambda c, w: setattr(c, "expert_hidden_dim", 63),
+    "invalid topk": lambda c, w: setattr(c, "num_experts_used", 5),
+    "overflow": lambda c, w: setattr(c, "hidden_dim", 2**31 - 1),
+    "router type": lambda c, w: setattr(w.ffn_gate_inp, "type", 1),
+    "router shape": lambda c, w: setattr(w.ffn_gate_inp, "n_dims", 0),
+    "router range": lambda c, w: setattr(w.ffn_gate_inp, "nbytes", w.ffn_gate_inp.nbytes - 1),
+    "expert type": lambda c, w: setattr(w.ffn_up_exps, "type", 0),
+    "expert shape": lambda c, w: w.ffn_gate_exps.shape.__setitem__(2, 5),
+    "expert range": lambda c, w: setattr(w.ffn_down_exps, "nbytes", 0),
+    "expert range overflow": lambda c, w: setattr(w.ffn_gate_exps, "nbytes", 2**64 - 8),
+    "bias type": lambda c, w: setattr(w.ffn_up_exps_bias, "type", 39),
+    "bias shape": lambda c, w: setattr(w.ffn_gate_exps_bias, "n_dims", 0),
+    "bias range": lambda c, w: setattr(w.ffn_gate_inp_bias, "nbytes", w.ffn_gate_inp_bias.nbytes - 1),
+    "unnamed bias with bytes": lambda c, w: setattr(w.ffn_down_exps_bias, "name", None),
+}
+
+
+@pytest.mark.parametrize("case", sorted(CASES))
+def test_moe_validation(vctx, case):
+    cfg, lw = _moe_descriptors()
+    CASES[case](cfg, lw)
+    rc = _call_moe(vctx, cfg, lw, X, 64, OUT, 64, 2)
+    assert rc == spt.ERR_INVALID, (case, spt.lib().spt_last_error())
+
+
+@pytest.mark.parametrize("batch", [-1, 0, 1, 2**63 - 1])
+def test_moe_batch_validation(vctx, batch):
+    cfg, lw = _moe_descriptors()
+    assert _call_moe(vctx, cfg, lw, X, 64, OUT, 64, batch) == spt.ERR_INVALID
+
+
+def test_moe_nil_and_overlap(vctx):
+    cfg, lw = _moe_descriptors()
+    assert _call_moe(None, cfg, lw, X, 64, OUT, 64, 2) == spt.ERR_INVALID
+    assert _call_moe(vctx, None, lw, X, 64, OUT, 64, 2) == spt.ERR_INVALID
+    assert _call_moe(vctx, cfg, None, X, 64, OUT, 64, 2) == spt.ERR_INVALID
+    assert _call_moe(vctx, cfg, lw, X, 64, OUT, 63, 2) == spt.ERR_INVALID
+    assert _call_moe(vctx, cfg, lw, X, 64, X, 64, 2) == spt.ERR_INVALID
+    for xp, op in ((X, X + 4), (X + 4, X)):  # partial overlap either way
+        assert _call_moe(vctx, cfg, lw, xp, 64, op, 64, 2) == spt.ERR_INVALID
+        assert b"overlap" in spt.lib().spt_last_error()
+
+
+def test_moe_cancellation_before_launch(vctx):
+    cfg, lw = _moe_descriptors()
+    flag = np.ones(1, np.int32)
+    vctx.set_cancel_flag(flag)
+    assert _call_moe(vctx, cfg, lw, X, 64, OUT, 64, 2) == spt.ERR_CANCELED
+    flag[0] = 0
+    assert _call_moe(vctx, cfg, lw, X, 64, OUT, 64, 2) == spt.ERR_DEVICE
+    vctx.set_cancel_flag(None)
+
+
+def _q40(inp=64, out=3, nbytes=None):
+    return spt.Tensor.make("q", spt.TYPE_Q4_0, [inp, out], 0x40000000,
+                           inp // 32 * 18 * out if nbytes is None else nbytes)
+
+
+def _call_q40(ctx, w, x_len, y_len, batch, x=X, y=OUT):
+    return spt.lib().spt_mul_q40_batch_into(ctx.handle, C.byref(w), x, x_len, y, y_len, batch)
+
+
+def test_q40_validation(vctx):
+    assert _call_q40(vctx, _q40(), 64, 3, 1) == spt.ERR_DEVICE
+    bad = [
+        (spt.Tensor.make("q", spt.TYPE_Q8_0, [64, 3], 0x40000000, 2 * 34 * 3), 64, 3, 1, b"instead of Q4_0"),
+        (spt.Tensor.make("q", spt.TYPE_Q4_0, [64], 0x40000000, 36), 64, 3, 1, b"two-dimensional"),
+        (spt.Tensor.make("q", spt.TYPE_Q4_0, [48, 3], 0x40000000, 36), 48, 3, 1, b"invalid Q4_0 matrix shape"),
+        (_q40(nbytes=107), 64, 3, 1, b"byte range"),
+        (_q40(), 63, 3, 1, b"expected 64 input and 3 output"),
+        (_q40(), 64, 3, 0, b"invalid or oversized batch"),
+        (_q40(), 128, 6, -2, b"invalid or oversized batch"),
+    ]
+    for w, xl, yl, b, msg in bad:
+        assert _call_q40(vctx, w, xl, yl, b) == spt.ERR_INVALID
+        assert msg in spt.lib().spt_last_error(), spt.lib().spt_last_error()
+    assert _call_q40(vctx, _q40(), 64, 3, 1, x=X, y=X + 8) == spt.ERR_INVALID
+    assert b"overlap" in spt.lib().spt_last_error()
+
+
+def test_quantize_validation(vctx):
+    L = spt.lib()
+    assert L.spt_quantize_q8_0(vctx.handle, X, 33, OUT) == spt.ERR_INVALID
+    assert L.spt_quantize_q8_0(vctx.handle, X, 64, X + 4) == spt.ERR_INVALID
+    assert L.spt_quantize_q8_0(vctx.handle, X, 64, OUT) == spt.ERR_DEVICE

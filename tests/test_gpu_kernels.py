@@ -1,0 +1,196 @@
+"""GPU parity of the individual kernels against the CPU oracle, through the
+C ABI.  Integer and byte outputs are compared bit-exactly; fp32 dot products
+within helpers.REL_TOL."""
+import numpy as np
+import pytest
+
+from helpers import assert_close
+
+pytestmark = pytest.mark.gpu
+
+
+def _dev(a):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def _mx_tensor(buf, input_dim, output_dim, experts, name="w"):
+    import spt
+
+    return spt.Tensor.make(name, spt.TYPE_MXFP4, [input_dim, output_dim, experts], buf.data_ptr(),
+                           buf.numel())
+
+
+def test_synth_matches_host(gpu_ctx):
+    import torch
+
+    from spt import synth
+
+    key = synth.stream_key(7, 3)
+    first, n = 12345, 4099
+    d = torch.zeros(n * 17, dtype=torch.uint8, device="cuda")
+    gpu_ctx.synth_mxfp4(d, key, first, n)
+    torch.cuda.synchronize()
+    assert np.array_equal(d.cpu().numpy(), synth.mxfp4_expert_bytes(key, first, n))
+
+
+@pytest.mark.parametrize("case", ["normal", "edge"])
+def test_quantize_q8_0_bit_exact(gpu_ctx, O, case):
+    import torch
+
+    from spt import synth
+
+    n = 32 * 1024
+    x = synth.normal(synth.stream_key(1, 2), n) * 3.0
+    if case == "edge":
+        x = x.reshape(-1, 32)
+        x[0] = 0.0                         # all-zero block: d = 0, id = 0
+        x[1, 5] = np.nan                   # NaN block
+        x[2, 7] = np.inf                   # Inf block
+        x[3] = np.float32(1e-30)           # subnormal fp16 scale
+        x[4] = np.float32(6e4) * np.sign(x[4])   # scale overflows fp16
+        x[5] = np.arange(32, dtype=np.float32) - 15.5   # exact .5 ties after scaling
+        x[6] = -0.0
+        x[7, :] = np.float32(127.0) * np.arange(32) / 31  # integer codes
+        x = x.reshape(-1)
+    xd = _dev(x.astype(np.float32))
+    out = torch.zeros(n // 32 * 34, dtype=torch.uint8, device="cuda")
+    gpu_ctx.quantize_q8_0(xd, out)
+    torch.cuda.synchronize()
+    want = O.quantize_q8_0(x)
+    got = out.cpu().numpy()
+    assert np.array_equal(got, want), np.nonzero(got != want)[0][:10]
+
+
+def _q8_of(O, x):
+    return O.quantize_q8_0(np.ascontiguousarray(x, np.float32))
+
+
+@pytest.mark.parametrize("input_dim", [32, 96, 2880])
+def test_mxfp4_block_sums_exact(gpu_ctx, O, input_dim):
+    import torch
+
+    from spt import synth
+
+    rows, E = 64, 3
+    nb = input_dim // 32
+    w = synth.mxfp4_expert_bytes(synth.stream_key(3, input_dim), 0, rows * nb * E)
+    x = synth.normal(synth.stream_key(4, input_dim), input_dim)
+    xq = _q8_of(O, x)
+    wd = _dev(w)
+    t = _mx_tensor(wd, input_dim, rows, E)
+    sums = torch.zeros(rows * nb, dtype=torch.int32, device="cuda")
+    for expert in range(E):
+        gpu_ctx.block_sums(t, expert, _dev(xq), rows, sums)
+        torch.cuda.synchronize()
+        got = sums.cpu().numpy().reshape(rows, nb)
+        base = expert * rows * nb * 17
+        for r in range(rows):
+            for b in range(nb):
+                blk = w[base + (r * nb + b) * 17: base + (r * nb + b + 1) * 17]
+                q = xq[b * 34 + 2: b * 34 + 34].view(np.int8)
+                assert got[r, b] == O.isum_mxfp4_q8(blk, q), (expert, r, b)
+
+
+def test_mxfp4_block_sums_all_encodings(gpu_ctx, O):
+    """Every nibble byte with every sign/magnitude against all-ones and
+    signed ramp activations (TestSIMDKernelMXFP4DecodeAllEncodings shape)."""
+    import torch
+
+    nb = 256
+    w = np.zeros((nb, 17), np.uint8)
+    w[:, 0] = 127
+    w[:, 1:] = np.arange(256, dtype=np.uint8)[:, None]
+    w = w.reshape(-1)
+    wd = _dev(w)  # keep the device copy alive while the descriptor is used
+    t = _mx_tensor(wd, 32 * nb, 1, 1)
+    for x in (np.ones(32 * nb, np.float32), (np.arange(32 * nb) % 64 - 31.5).astype(np.float32)):
+        xq = _q8_of(O, x)
+        sums = torch.zeros(nb, dtype=torch.int32, device="cuda")
+        gpu_ctx.block_sums(t, 0, _dev(xq), 1, sums)
+        torch.cuda.synchronize()
+        got = sums.cpu().numpy()
+        want = [O.isum_mxfp4_q8(w[b * 17:(b + 1) * 17], xq[b * 34 + 2:b * 34 + 34].view(np.int8))
+                for b in range(nb)]
+        assert np.array_equal(got, np.array(want, np.int32))
+
+
+@pytest.mark.parametrize("input_dim,output_dim,batch", [(2880, 2880, 1), (2880, 2880, 3), (96, 64, 5),
+                                                       (32, 257, 1)])
+def test_mxfp4_expert_gemv(gpu_ctx, O, input_dim, output_dim, batch):
+    import torch
+
+    import spt
+    from spt import synth
+
+    E, expert = 2, 1
+    nb = input_dim // 32
+    w = synth.mxfp4_expert_bytes(synth.stream_key(5, input_dim + output_dim), 0, E * output_dim * nb)
+    bias = synth.normal(synth.stream_key(6, 1), E * output_dim, 0.0, 0.02)
+    x = synth.normal(synth.stream_key(7, batch), batch * input_dim)
+    wd, bd, xd = _dev(w), _dev(bias), _dev(x)
+    y = torch.zeros(batch * output_dim, dtype=torch.float32, device="cuda")
+    bt = spt.Tensor.make("b", spt.TYPE_F32, [output_dim, E], bd.data_ptr(), bd.numel() * 4)
+    gpu_ctx.mul_mxfp4_expert(_mx_tensor(wd, input_dim, output_dim, E), bt, expert, xd, y, batch)
+    torch.cuda.synchronize()
+    got = y.cpu().numpy().reshape(batch, output_dim)
+    ew = w[expert * output_dim * nb * 17:(expert + 1) * output_dim * nb * 17]
+    for t in range(batch):
+        xq = _q8_of(O, x[t * input_dim:(t + 1) * input_dim])
+        want = O.mul_mxfp4_q8(ew, xq, bias[expert * output_dim:(expert + 1) * output_dim], input_dim,
+                              output_dim)
+        assert_close(got[t], want, what=f"token {t}")
+
+
+@pytest.mark.parametrize("input_dim,output_dim", [(2880, 4096), (2880, 512), (4096, 2880), (32, 17)])
+@pytest.mark.parametrize("batch", [1, 32])
+def test_q40_gemv(gpu_ctx, O, input_dim, output_dim, batch):
+    import torch
+
+    import spt
+    from spt import synth
+
+    w = synth.q40_bytes(synth.stream_key(8, output_dim), output_dim, input_dim)
+    x = synth.normal(synth.stream_key(9, batch), batch * input_dim)
+    wd, xd = _dev(w), _dev(x)
+    y = torch.zeros(batch * output_dim, dtype=torch.float32, device="cuda")
+    t = spt.Tensor.make("attn", spt.TYPE_Q4_0, [input_dim, output_dim], wd.data_ptr(), w.size)
+    gpu_ctx.mul_q40_batch_into(t, xd, y, batch)
+    torch.cuda.synchronize()
+    want = O.mul_q40_q8(w, x, input_dim, output_dim, batch)
+    assert_close(y.cpu().numpy(), want, what="q40")
+    # exact int32 block sums of the first rows against token 0
+    nb = input_dim // 32
+    xq = _q8_of(O, x[:input_dim])
+    rows = min(output_dim, 16)
+    sums = torch.zeros(rows * nb, dtype=torch.int32, device="cuda")
+    gpu_ctx.block_sums(t, 0, _dev(xq), rows, sums)
+    torch.cuda.synchronize()
+    got = sums.cpu().numpy().reshape(rows, nb)
+    for r in range(rows):
+        for b in range(nb):
+            blk = w[(r * nb + b) * 18:(r * nb + b + 1) * 18]
+            assert got[r, b] == O.isum_q40_q8(blk, xq[b * 34 + 2:b * 34 + 34].view(np.int8))
+
+
+@pytest.mark.parametrize("hidden,batch", [(2880, 1), (2880, 19), (96, 3), (32, 2)])
+def test_router_logits_bit_exact(gpu_ctx, O, hidden, batch):
+    import torch
+
+    import spt
+    from spt import synth
+
+    E = 128 if hidden == 2880 else 5
+    W = synth.normal(synth.stream_key(10, hidden), E * hidden, 0.0, 0.02)
+    b = synth.normal(synth.stream_key(11, hidden), E, 0.0, 0.02)
+    x = synth.normal(synth.stream_key(12, batch), batch * hidden)
+    Wd, bd, xd = _dev(W), _dev(b), _dev(x)
+    logits = torch.zeros(batch * E, dtype=torch.float32, device="cuda")
+    rt = spt.Tensor.make("router", spt.TYPE_F32, [hidden, E], Wd.data_ptr(), W.size * 4)
+    bt = spt.Tensor.make("router.bias", spt.TYPE_F32, [E], bd.data_ptr(), E * 4)
+    gpu_ctx.route_moe_batch(rt, bt, xd, batch, logits)
+    torch.cuda.synchronize()
+    want = O.route(W, b, x, batch, hidden, E)
+    got = logits.cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), np.nonzero(got != want)[0][:8]

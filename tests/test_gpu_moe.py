@@ -1,0 +1,180 @@
+"""GPU parity of the full MoE layer (forwardMoEBatch) against the CPU oracle.
+
+Stage-wise: every stage of the GPU path is checked against the oracle fed
+the GPU's own upstream bits, so integer stages (Q8_0 codes/scales, expert
+ids, packing) and fp32 stages with a fixed operation order (router logits,
+softmax weights, SwiGLU, combine) must match bit-for-bit, and the two GEMV
+stages within helpers.REL_TOL.  End-to-end the output is then compared with
+the oracle's own run of the whole Q8_0 layer."""
+import numpy as np
+import pytest
+
+from fixtures import ROUTER_MODES, device_moe_layer, moe_batch_fixture, moe_batch_x
+from helpers import assert_close, bits
+
+pytestmark = pytest.mark.gpu
+
+
+def _zeros(n, dtype):
+    import torch
+
+    return torch.zeros(n, dtype=dtype, device="cuda")
+
+
+def _taps(B, H, D, E, k):
+    import torch
+
+    n = B * k
+    t = {
+        "logits": _zeros(B * E, torch.float32), "ids": _zeros(n, torch.int32), "weights": _zeros(n, torch.float32),
+        "counts": _zeros(E, torch.int32), "offsets": _zeros(E + 1, torch.int32), "list": _zeros(n, torch.int32),
+        "active": _zeros(E, torch.int32), "n_active": _zeros(1, torch.int32),
+        "xq": _zeros(B * H // 32 * 34, torch.uint8), "gate": _zeros(n * D, torch.float32),
+        "up": _zeros(n * D, torch.float32), "act": _zeros(n * D, torch.float32),
+        "actq": _zeros(n * D // 32 * 34, torch.uint8), "results": _zeros(n * H, torch.float32),
+    }
+    return t
+
+
+def _host(t):
+    return {k: v.cpu().numpy() for k, v in t.items()}
+
+
+def _run(ctx, cfg, lw, x, B, logits_in=None):
+    import torch
+
+    import spt
+
+    H, D, E, k = cfg.hidden_dim, cfg.expert_hidden_dim, cfg.num_experts, cfg.num_experts_used
+    t = _taps(B, H, D, E, k)
+    extra = {}
+    if logits_in is not None:
+        extra["logits_in"] = torch.from_numpy(logits_in).cuda()
+    taps = spt.make_taps(**t, **extra)
+    xd = torch.from_numpy(x).cuda()
+    out = torch.full((B * H,), 999.0, dtype=torch.float32, device="cuda")
+    ctx.forward_moe_batch(cfg, lw, xd, out, B, taps)
+    torch.cuda.synchronize()
+    g = _host(t)
+    g["out"] = out.cpu().numpy()
+    assert np.array_equal(x, xd.cpu().numpy()), "input modified"
+    return g
+
+
+def _bias_vec(lay, name, e, dim, O):
+    b = lay.get(name)
+    if b is None:
+        return np.zeros(dim, np.float32)
+    arr, typ = b
+    seg = arr[e * dim:(e + 1) * dim]
+    if typ == 0:
+        return seg.astype(np.float32)
+    if typ == 30:
+        return (seg.astype(np.uint32) << 16).view(np.float32)
+    return np.array([O.fp16_to_f32(int(h)) for h in seg], np.float32)
+
+
+def check_stagewise(O, lay, x, B, g, logits_in=None):
+    """Check every GPU stage against the oracle fed the GPU's inputs."""
+    H, D, E, k = lay["hidden"], lay["expert_dim"], lay["experts"], lay["topk"]
+    n = B * k
+    nbh, nbd = H // 32, D // 32
+    # Q8_0 of x: bit-exact
+    assert np.array_equal(g["xq"], O.quantize_q8_0(x)), "x Q8_0 codes/scales"
+    # router logits: bit-exact (the reference's AVX2 accumulation order)
+    if logits_in is None:
+        rb = _bias_vec(lay, "router_bias", 0, E, O) if lay.get("router_bias") else None
+        want_logits = O.route(lay["router"], rb if rb is not None else np.zeros(E, np.float32), x, B, H, E)
+        assert np.array_equal(bits(g["logits"]), bits(want_logits)), "router logits"
+    logits = g["logits"].reshape(B, E)
+    # top-k + softmax: ids and weights bit-exact
+    for t in range(B):
+        ids, w = O.select(logits[t], k)
+        assert np.array_equal(g["ids"][t * k:(t + 1) * k], ids), f"ids token {t}"
+        assert np.array_equal(bits(g["weights"][t * k:(t + 1) * k]), bits(w)), f"weights token {t}"
+    # grouping: bit-exact lists
+    counts, offsets, lst, active = O.group(g["ids"], g["weights"], B, k, E)
+    assert np.array_equal(g["counts"], counts) and np.array_equal(g["offsets"], offsets)
+    assert np.array_equal(g["list"][:offsets[-1]], lst), "per-expert packing"
+    assert g["n_active"][0] == active.size and np.array_equal(g["active"][:active.size], active)
+    valid = [i for i in range(n) if not (g["weights"][i] <= 0)]
+    xq = g["xq"].reshape(B, nbh * 34)
+    gate, up = g["gate"].reshape(n, D), g["up"].reshape(n, D)
+    act, actq, res = g["act"].reshape(n, D), g["actq"].reshape(n, nbd * 34), g["results"].reshape(n, H)
+    gb = H // 32 * 17 * D
+    db = D // 32 * 17 * H
+    errs = []
+    for idx in valid:
+        e, t = int(g["ids"][idx]), idx // k
+        G = lay["gate"][e * gb:(e + 1) * gb]
+        U = lay["up"][e * gb:(e + 1) * gb]
+        wg = O.mul_mxfp4_q8(G, xq[t], _bias_vec(lay, "gate_bias", e, D, O), H, D)
+        wu = O.mul_mxfp4_q8(U, xq[t], _bias_vec(lay, "up_bias", e, D, O), H, D)
+        errs.append(assert_close(gate[idx], wg, what=f"gate idx {idx}"))
+        errs.append(assert_close(up[idx], wu, what=f"up idx {idx}"))
+        wa = np.array([O.swiglu(a, b) for a, b in zip(gate[idx], up[idx])], np.float32)
+        assert np.array_equal(bits(act[idx]), bits(wa)), f"SwiGLU idx {idx}"
+        assert np.array_equal(actq[idx], O.quantize_q8_0(act[idx])), f"act Q8_0 idx {idx}"
+        Dn = lay["down"][e * db:(e + 1) * db]
+        wr = O.mul_mxfp4_q8(Dn, actq[idx], _bias_vec(lay, "down_bias", e, H, O), D, H)
+        errs.append(assert_close(res[idx], wr, what=f"down idx {idx}"))
+    # combine: bit-exact given the GPU results and weights
+    want = O.combine(g["results"], g["weights"], B, k, H)
+    assert _nan_equal(g["out"], want), "combine"
+    return max(errs) if errs else 0.0
+
+
+def _nan_equal(a, b):
+    a = np.asarray(a).ravel()
+    b = np.asarray(b).ravel()
+    return np.array_equal(np.isnan(a), np.isnan(b)) and np.array_equal(a[~np.isnan(a)], b[~np.isnan(b)])
+
+
+def test_moe_decode_gpt_oss_layer(gpu_ctx, O):
+    """One GPT-OSS-120B MoE layer, decode of 1 token (128 experts, top-4,
+    MXFP4 experts with E8M0 in [118,124], N(0,0.02) router and biases)."""
+    from spt import workloads as W
+
+    shp = W.MoEShape()
+    dl = W.device_layer(gpu_ctx, seed=0, layer=0, shp=shp)
+    x = W.x_tokens(0, 0, 1, shp.hidden)
+    g = _run(gpu_ctx, dl.config, dl.layer, x, 1)
+    lay = W.host_layer(0, 0, shp, experts=g["ids"])
+    err = check_stagewise(O, lay, x, 1, g)
+    want = O.forward_moe_batch(lay, x, 1, q8=True, threads=8)
+    e2e = assert_close(g["out"], want, what="end-to-end")
+    ref = O.forward_moe_batch(lay, x, 1, q8=False, threads=8)
+    print(f"gemv max rel err {err:.2e}; end-to-end vs Q8 oracle {e2e:.2e}; "
+          f"vs fp32-activation reference {np.max(np.abs(g['out'] - ref)) / np.max(np.abs(ref)):.2e}")
+
+
+@pytest.mark.parametrize("batch", [32])
+def test_moe_prefill_zipf(gpu_ctx, O, batch):
+    """32 positions per weight pass, router logits injected so expert
+    popularity follows Zipf(1.1): ragged groups of 0..32 rows."""
+    from spt import synth
+    from spt import workloads as W
+
+    shp = W.MoEShape()
+    dl = W.device_layer(gpu_ctx, seed=2, layer=0, shp=shp)
+    x = W.x_tokens(2, 0, batch, shp.hidden)
+    logits = synth.zipf_logits(synth.stream_key(2, 99), batch, shp.experts, 1.1)
+    g = _run(gpu_ctx, dl.config, dl.layer, x, batch, logits_in=logits)
+    lay = W.host_layer(2, 0, shp, experts=np.unique(g["ids"]))
+    check_stagewise(O, lay, x, batch, g, logits_in=logits)
+
+
+@pytest.mark.parametrize("experts,topk", [(1, 1), (4, 2), (7, 7), (8, 2)])
+@pytest.mark.parametrize("bias_type", [-1, 0, 1, 30])
+@pytest.mark.parametrize("mode", ROUTER_MODES)
+def test_moe_reference_fixture(gpu_ctx, O, experts, topk, bias_type, mode):
+    """moeBatchFixture (hidden 96, expert dim 64) in every router mode, bias
+    type and batch of the reference's batch==sequential test."""
+    lay = moe_batch_fixture(96, 64, experts, topk, bias_type, mode)
+    keep, cfg, lw = device_moe_layer(lay)
+    for batch in (1, 5, 37):
+        x = moe_batch_x(batch, 96, mode)
+        g = _run(gpu_ctx, cfg, lw, x, batch)
+        check_stagewise(O, lay, x, batch, g)
+        want = O.forward_moe_batch(lay, x, batch, q8=True)
+        assert_close(g["out"], want, what=f"{mode} batch {batch}")
