@@ -117,7 +117,7 @@ typedef struct spt_moe_taps {
 const char *spt_last_error(void);
 
 /* Create a context on HIP device `device`, enqueueing on `hip_stream`
- * (a hipStream_t; NULL creates a stream owned by the context).  device = -1
+ * (a hipStream_t; NULL is the device's default stream).  device = -1
  * creates a validation-only context: every entry point validates its
  * arguments and then fails with SPT_ERR_DEVICE. */
 int spt_ctx_create(int device, void *hip_stream, struct spt_ctx **out);

@@ -267,16 +267,18 @@ int run_moe(spt_ctx *ctx, const spt_moe_layer *lw, const float *x, float *out, c
     const int64_t h = m.h, d = m.d, E = m.E, k = m.k, B = m.batch, n = B * k;
     const int64_t nbh = h / 32, nbd = d / 32;
     Carve c;
-    size_t o_xc = c.take(B * h), o_xs = c.take(B * nbh * 4), o_logits = c.take(B * E * 4);
+    size_t o_xc = c.take(B * h), o_xs = c.take(B * nbh * 4), o_xm = c.take(B * nbh * 64);
+    size_t o_logits = c.take(B * E * 4);
     size_t o_ids = c.take(n * 4), o_w = c.take(n * 4), o_cnt = c.take(E * 4), o_off = c.take((E + 1) * 4);
     size_t o_list = c.take(n * 4), o_act_list = c.take(E * 4), o_na = c.take(4);
-    size_t o_act = c.take(n * d * 4), o_ac = c.take(n * d), o_as = c.take(n * nbd * 4);
+    size_t o_act = c.take(n * d * 4), o_ac = c.take(n * d), o_as = c.take(n * nbd * 4), o_am = c.take(n * nbd * 64);
     size_t o_res = c.take(n * h * 4);
     char *S;
     int rc;
     if ((rc = scratch(ctx, c.off, &S))) return rc;
     int8_t *xc = (int8_t *)(S + o_xc), *ac = (int8_t *)(S + o_ac);
     float *xs = (float *)(S + o_xs), *logits = (float *)(S + o_logits), *act = (float *)(S + o_act);
+    uint8_t *xm = (uint8_t *)(S + o_xm), *am = (uint8_t *)(S + o_am);
     float *as = (float *)(S + o_as), *res = (float *)(S + o_res);
     spt::SelectOut so{(int32_t *)(S + o_ids), (float *)(S + o_w), (int32_t *)(S + o_cnt),
                       (int32_t *)(S + o_off), (int32_t *)(S + o_list), (int32_t *)(S + o_act_list),
@@ -284,7 +286,9 @@ int run_moe(spt_ctx *ctx, const spt_moe_layer *lw, const float *x, float *out, c
     hipStream_t s = ctx->stream;
 
     if ((rc = check_cancel(ctx))) return rc;
-    SPT_HIP(timed(ctx, SPT_KERNEL_QUANTIZE, [&] { return spt::launch_quantize(s, x, B * nbh, xc, xs, nullptr, taps ? (uint8_t *)taps->xq : nullptr); }));
+    SPT_HIP(timed(ctx, SPT_KERNEL_QUANTIZE, [&] {
+        return spt::launch_quantize(s, x, B * nbh, xc, xs, nullptr, xm, taps ? (uint8_t *)taps->xq : nullptr);
+    }));
     if ((rc = check_cancel(ctx))) return rc;
     if (taps && taps->logits_in) {
         SPT_HIP(timed(ctx, SPT_KERNEL_ROUTE, [&] { return spt::launch_select(s, taps->logits_in, (int)B, (int)E, (int)k, so); }));
@@ -298,7 +302,7 @@ int run_moe(spt_ctx *ctx, const spt_moe_layer *lw, const float *x, float *out, c
         if (taps && (rc = copy_tap(ctx, taps->logits, logits, B * E * 4))) return rc;
     }
     const int slots = (int)(n < E ? n : E);
-    spt::MxGemvArgs ga{};
+    spt::MxMfmaArgs ga{};
     ga.w[0] = (const uint8_t *)lw->ffn_gate_exps.data;
     ga.w[1] = (const uint8_t *)lw->ffn_up_exps.data;
     ga.expert_bytes = (uint64_t)nbh * 17 * d;
@@ -308,8 +312,9 @@ int run_moe(spt_ctx *ctx, const spt_moe_layer *lw, const float *x, float *out, c
     ga.bias_type[0] = bias_type(lw->ffn_gate_exps_bias);
     ga.bias[1] = bias_ptr(lw->ffn_up_exps_bias);
     ga.bias_type[1] = bias_type(lw->ffn_up_exps_bias);
-    ga.codes = xc;
+    ga.mxtab = xm;
     ga.scales = xs;
+    ga.codes = xc;
     ga.active = so.active;
     ga.n_active = so.n_active;
     ga.offsets = so.offsets;
@@ -318,19 +323,22 @@ int run_moe(spt_ctx *ctx, const spt_moe_layer *lw, const float *x, float *out, c
     ga.out = act;
     ga.tap[0] = taps ? taps->gate : nullptr;
     ga.tap[1] = taps ? taps->up : nullptr;
+    ga.act_codes = ac;
+    ga.act_scales = as;
+    ga.act_mxtab = am;
+    ga.act_blocks34 = taps ? (uint8_t *)taps->actq : nullptr;
     if ((rc = check_cancel(ctx))) return rc;
-    SPT_HIP(timed(ctx, SPT_KERNEL_GATE_UP, [&] { return spt::launch_mx_gemv(s, spt::kGateUp, ga, slots); }));
-    if ((rc = check_cancel(ctx))) return rc;
-    SPT_HIP(timed(ctx, SPT_KERNEL_QUANTIZE, [&] { return spt::launch_quantize(s, act, n * nbd, ac, as, nullptr, taps ? (uint8_t *)taps->actq : nullptr); }));
-    spt::MxGemvArgs da{};
+    SPT_HIP(timed(ctx, SPT_KERNEL_GATE_UP, [&] { return spt::launch_mx_mfma(s, spt::kGateUp, ga, slots); }));
+    spt::MxMfmaArgs da{};
     da.w[0] = (const uint8_t *)lw->ffn_down_exps.data;
     da.expert_bytes = (uint64_t)nbd * 17 * h;
     da.rows = (int)h;
     da.nb = (int)nbd;
     da.bias[0] = bias_ptr(lw->ffn_down_exps_bias);
     da.bias_type[0] = bias_type(lw->ffn_down_exps_bias);
-    da.codes = ac;
+    da.mxtab = am;
     da.scales = as;
+    da.codes = ac;
     da.active = so.active;
     da.n_active = so.n_active;
     da.offsets = so.offsets;
@@ -338,7 +346,7 @@ int run_moe(spt_ctx *ctx, const spt_moe_layer *lw, const float *x, float *out, c
     da.topk = (int)k;
     da.out = res;
     if ((rc = check_cancel(ctx))) return rc;
-    SPT_HIP(timed(ctx, SPT_KERNEL_DOWN, [&] { return spt::launch_mx_gemv(s, spt::kDown, da, slots); }));
+    SPT_HIP(timed(ctx, SPT_KERNEL_DOWN, [&] { return spt::launch_mx_mfma(s, spt::kDown, da, slots); }));
     if ((rc = check_cancel(ctx))) return rc;
     SPT_HIP(timed(ctx, SPT_KERNEL_COMBINE, [&] { return spt::launch_combine(s, res, so.weights, (int)B, (int)k, (int)h, out); }));
     if (taps) {
@@ -355,16 +363,21 @@ int run_moe(spt_ctx *ctx, const spt_moe_layer *lw, const float *x, float *out, c
     return SPT_OK;
 }
 
+// Quantize `rows` activation rows of nb blocks into the scratch arena: Q8_0
+// codes, scales, per-block code sums (Q4_0) and the E4M3 digit table (MXFP4).
 int quantize_into_scratch(spt_ctx *ctx, const float *x, int64_t rows, int64_t nb, Carve &c, char **S,
-                          size_t extra, int8_t **codes, float **scales, int32_t **sumq, size_t *o_extra) {
+                          int8_t **codes, float **scales, int32_t **sumq, uint8_t **mxtab) {
     size_t o_c = c.take(rows * nb * 32), o_s = c.take(rows * nb * 4), o_q = c.take(rows * nb * 4);
-    *o_extra = c.take(extra);
+    size_t o_m = c.take(mxtab ? rows * nb * 64 : 0);
     int rc;
     if ((rc = scratch(ctx, c.off, S))) return rc;
     *codes = (int8_t *)(*S + o_c);
     *scales = (float *)(*S + o_s);
     *sumq = (int32_t *)(*S + o_q);
-    SPT_HIP(spt::launch_quantize(ctx->stream, x, rows * nb, *codes, *scales, *sumq, nullptr));
+    if (mxtab) *mxtab = (uint8_t *)(*S + o_m);
+    SPT_HIP(timed(ctx, SPT_KERNEL_QUANTIZE, [&] {
+        return spt::launch_quantize(ctx->stream, x, rows * nb, *codes, *scales, *sumq, mxtab ? *mxtab : nullptr, nullptr);
+    }));
     return SPT_OK;
 }
 
@@ -406,16 +419,7 @@ int spt_ctx_create(int device, void *hip_stream, spt_ctx **out) {
             delete ctx;
             return hip_fail(err, "hipSetDevice");
         }
-        if (hip_stream) {
-            ctx->stream = (hipStream_t)hip_stream;
-        } else {
-            err = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
-            if (err != hipSuccess) {
-                delete ctx;
-                return hip_fail(err, "hipStreamCreate");
-            }
-            ctx->own_stream = true;
-        }
+        ctx->stream = (hipStream_t)hip_stream;  // NULL: the device's default stream
         if ((err = hipMalloc(&ctx->counter, 256)) != hipSuccess ||
             (err = hipMemset(ctx->counter, 0, 256)) != hipSuccess) {
             if (ctx->own_stream) (void)hipStreamDestroy(ctx->stream);
@@ -553,7 +557,7 @@ int spt_quantize_q8_0(spt_ctx *ctx, const float *x_dev, int64_t n, void *out_dev
     if (ranges_overlap(x_dev, (uint64_t)n * 4, out_dev, (uint64_t)n / 32 * 34))
         return fail(SPT_ERR_INVALID, "input and output must not overlap");
     if ((rc = check_device(ctx)) || (rc = check_cancel(ctx))) return rc;
-    SPT_HIP(spt::launch_quantize(ctx->stream, x_dev, n / 32, nullptr, nullptr, nullptr, (uint8_t *)out_dev));
+    SPT_HIP(spt::launch_quantize(ctx->stream, x_dev, n / 32, nullptr, nullptr, nullptr, nullptr, (uint8_t *)out_dev));
     return SPT_OK;
 }
 
@@ -569,8 +573,7 @@ int spt_mul_q40_batch_into(spt_ctx *ctx, const spt_tensor *w, const float *x_dev
     int8_t *codes;
     float *scales;
     int32_t *sumq;
-    size_t o_extra;
-    if ((rc = quantize_into_scratch(ctx, x_dev, batch, nb, c, &S, 0, &codes, &scales, &sumq, &o_extra))) return rc;
+    if ((rc = quantize_into_scratch(ctx, x_dev, batch, nb, c, &S, &codes, &scales, &sumq, nullptr))) return rc;
     if ((rc = check_cancel(ctx))) return rc;
     spt::Q40Args a{(const uint8_t *)w->data, w->nbytes, (int)out, (int)nb, codes, scales, sumq, (int)batch, y_dev};
     SPT_HIP(timed(ctx, SPT_KERNEL_Q40, [&] { return spt::launch_q40_gemv(ctx->stream, a); }));
@@ -628,21 +631,22 @@ int spt_mul_mxfp4_expert(spt_ctx *ctx, const spt_tensor *w, const spt_tensor *bi
     int8_t *codes;
     float *scales;
     int32_t *sumq;
-    size_t o_extra;
-    if ((rc = quantize_into_scratch(ctx, x_dev, batch, nb, c, &S, 0, &codes, &scales, &sumq, &o_extra))) return rc;
-    spt::MxGemvArgs a{};
+    uint8_t *mxtab;
+    if ((rc = quantize_into_scratch(ctx, x_dev, batch, nb, c, &S, &codes, &scales, &sumq, &mxtab))) return rc;
+    spt::MxMfmaArgs a{};
     a.w[0] = (const uint8_t *)w->data;
     a.expert_bytes = (uint64_t)nb * 17 * out;
     a.rows = (int)out;
     a.nb = (int)nb;
     a.bias[0] = bias ? bias_ptr(*bias) : nullptr;
     a.bias_type[0] = bias ? bias_type(*bias) : 0;
+    a.mxtab = mxtab;
     a.codes = codes;
     a.scales = scales;
     a.expert = expert;
     a.ntok = (int)batch;
     a.out = y_dev;
-    SPT_HIP(spt::launch_mx_gemv(ctx->stream, spt::kRows, a, 1));
+    SPT_HIP(timed(ctx, SPT_KERNEL_DOWN, [&] { return spt::launch_mx_mfma(ctx->stream, spt::kRows, a, 1); }));
     return SPT_OK;
 }
 

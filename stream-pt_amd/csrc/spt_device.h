@@ -61,6 +61,18 @@ __device__ inline void load_block5(const ByteView &v, uint32_t pos, uint32_t d[5
     d[4] = __builtin_amdgcn_raw_buffer_load_b32(v.r, base + 16, 0, 0);
 }
 
+// The same five dwords when the caller already knows pos & 3.
+__device__ inline void load_block5_raw(const ByteView &v, uint32_t pos, uint32_t d[5]) {
+    uint32_t base = (pos + v.lead) & ~3u;
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    u32x4 q = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(v.r, base, 0, 0));
+    d[0] = q.x;
+    d[1] = q.y;
+    d[2] = q.z;
+    d[3] = q.w;
+    d[4] = __builtin_amdgcn_raw_buffer_load_b32(v.r, base + 16, 0, 0);
+}
+
 // ---- fp16 -----------------------------------------------------------------
 __device__ inline float f16_bits_to_f32(uint32_t h) {
     return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h)));
@@ -193,6 +205,107 @@ __device__ inline void q8_quantize32(const float v[32], uint32_t codes[8], uint1
             word |= (uint32_t)(q & 0xff) << (8 * i);
         }
         codes[k] = word;
+    }
+}
+
+// ---- Q8_0 digit table for the block-scaled MFMA -------------------------------
+// FP8 E4M3 encoding of a small integer, exact for |v| <= 15.
+__device__ inline uint32_t e4m3_small(int v) {
+    const uint32_t a = (uint32_t)(v < 0 ? -v : v);
+    if (a == 0) return 0u;
+    const uint32_t e = 31u - __builtin_clz(a);               // floor(log2 a), 0..3
+    const uint32_t code = ((e + 7u) << 3) | ((a << (3u - e)) & 7u);
+    return v < 0 ? (code | 0x80u) : code;
+}
+
+// Store one quantized block of 32 (codes w[8], fp16 scale bits dh) as block
+// `blk` of every requested layout:
+//   codes  : int8 [blk][32]
+//   scales : f32  [blk]          (fp16 d widened exactly)
+//   mxtab  : u8   [blk][64]      E4M3 digits of q = 16*h + l in MXFP4 nibble
+//                                 order (position p <-> element (p>>1) +
+//                                 16*(p&1)): h digits at [0,32), l at [32,64)
+//   blocks34: u8  [blk][34]      GGML Q8_0 block
+__device__ inline void write_q8_block(const uint32_t w[8], uint16_t dh, size_t blk, int8_t *codes,
+                                      float *scales, uint8_t *mxtab, uint8_t *blocks34) {
+    if (codes) {
+        uint32_t *c = reinterpret_cast<uint32_t *>(codes + blk * 32);
+#pragma unroll
+        for (int k = 0; k < 8; k++) c[k] = w[k];
+    }
+    if (scales) scales[blk] = f16_bits_to_f32(dh);
+    if (mxtab) {
+        uint32_t hw[8], lw[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            hw[k] = 0;
+            lw[k] = 0;
+        }
+#pragma unroll
+        for (int p = 0; p < 32; p++) {
+            const int el = (p >> 1) + 16 * (p & 1);
+            const int q = (int)(int8_t)(w[el >> 2] >> (8 * (el & 3)));
+            const int h = q >> 4, l = q & 15;
+            hw[p >> 2] |= e4m3_small(h) << (8 * (p & 3));
+            lw[p >> 2] |= e4m3_small(l) << (8 * (p & 3));
+        }
+        uint32_t *o = reinterpret_cast<uint32_t *>(mxtab + blk * 64);
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            o[k] = hw[k];
+            o[8 + k] = lw[k];
+        }
+    }
+    if (blocks34) {
+        uint8_t *o = blocks34 + blk * kQ80Block;
+        o[0] = (uint8_t)(dh & 0xff);
+        o[1] = (uint8_t)(dh >> 8);
+#pragma unroll
+        for (int k = 0; k < 8; k++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) o[2 + 4 * k + i] = (uint8_t)(w[k] >> (8 * i));
+    }
+}
+
+// The same rule with one element per lane (lanes 0..31 of a wavefront hold
+// the block; lanes 32..63 pass v = 0 and their results are unused).  amax
+// skips NaN elements exactly as the sequential form does, so codes and scale
+// are identical to q8_quantize32.
+__device__ inline int q8_quantize_lane(float v, int lane, uint16_t *dbits) {
+    const float a = __builtin_fabsf(v);
+    const bool in_block = lane < 32;
+    const bool nan_any = __any(in_block && (a != a));
+    float m = (in_block && a == a) ? a : 0.0f;
+#pragma unroll
+    for (int off = 16; off >= 1; off >>= 1) {
+        const float o = __shfl_xor(m, off, 32);
+        m = o > m ? o : m;
+    }
+    const float d = nan_any ? __builtin_nanf("") : m / 127.0f;
+    const float id = (d != 0.0f) ? 1.0f / d : 0.0f;
+    *dbits = f32_to_f16_bits(d);
+    const float r = __builtin_roundf(v * id);
+    return (r != r) ? 0 : (r > 127.0f ? 127 : (r < -127.0f ? -127 : (int)r));
+}
+
+// Lane i (< 32) of a wavefront stores element i of Q8_0 block `blk` (code q)
+// into every requested layout of write_q8_block; lane 0 also stores the scale.
+__device__ inline void write_q8_lane(int q, uint16_t dh, int lane, size_t blk, int8_t *codes,
+                                     float *scales, uint8_t *mxtab, uint8_t *blocks34) {
+    if (lane >= 32) return;
+    if (codes) codes[blk * 32 + lane] = (int8_t)q;
+    if (scales && lane == 0) scales[blk] = f16_bits_to_f32(dh);
+    if (mxtab) {
+        const int p = 2 * (lane & 15) + (lane >> 4);  // nibble position of element `lane`
+        mxtab[blk * 64 + p] = (uint8_t)e4m3_small(q >> 4);
+        mxtab[blk * 64 + 32 + p] = (uint8_t)e4m3_small(q & 15);
+    }
+    if (blocks34) {
+        if (lane == 0) {
+            blocks34[blk * kQ80Block] = (uint8_t)(dh & 0xff);
+            blocks34[blk * kQ80Block + 1] = (uint8_t)(dh >> 8);
+        }
+        blocks34[blk * kQ80Block + 2 + lane] = (uint8_t)q;
     }
 }
 

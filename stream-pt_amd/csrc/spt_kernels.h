@@ -22,15 +22,23 @@ struct SelectOut {
 
 enum GemvMode { kGateUp = 0, kDown = 1, kRows = 2 };
 
-struct MxGemvArgs {
+// Grouped MXFP4 x Q8_0 GEMV on the block-scaled MFMA (spt_mx_mfma.hip).
+//   kGateUp: per active expert, gate and up rows for the tokens of the
+//            expert's list, bias, clamped SwiGLU -> out = act[idx][row]; each
+//            32-row tile also writes the Q8_0 block of act it completes.
+//   kDown:   per active expert, down rows for every selection in the list,
+//            bias -> out = results[idx][row].
+//   kRows:   one expert, consecutive tokens -> out = y[t][row] (+ bias).
+struct MxMfmaArgs {
     const uint8_t *w[2];     // MXFP4 expert tensors (gate, up) or (down) or (w)
     uint64_t expert_bytes;   // bytes of one expert matrix
     int rows;                // output rows per expert (= bias dim)
     int nb;                  // input blocks of 32 per row
     const void *bias[2];     // optional [rows][experts] biases
     int bias_type[2];
-    const int8_t *codes;     // activation Q8_0 codes [*][nb*32]
+    const uint8_t *mxtab;    // activation E4M3 digit table [*][nb][64]
     const float *scales;     // activation Q8_0 scales [*][nb]
+    const int8_t *codes;     // activation Q8_0 codes [*][nb*32]
     const int32_t *active;   // grouped modes: packed expert lists
     const int32_t *n_active;
     const int32_t *offsets;
@@ -39,7 +47,11 @@ struct MxGemvArgs {
     int expert;              // kRows: the expert
     int ntok;                // kRows: tokens 0..ntok-1
     float *out;
-    float *tap[2];
+    float *tap[2];           // kGateUp: gate / up + bias
+    int8_t *act_codes;       // kGateUp: Q8_0 of act, all layouts (optional)
+    float *act_scales;
+    uint8_t *act_mxtab;
+    uint8_t *act_blocks34;
 };
 
 struct Q40Args {
@@ -55,13 +67,13 @@ struct Q40Args {
 };
 
 hipError_t launch_quantize(hipStream_t s, const float *x, int64_t nblocks, int8_t *codes,
-                           float *scales, int32_t *sumq, uint8_t *blocks34);
+                           float *scales, int32_t *sumq, uint8_t *mxtab, uint8_t *blocks34);
 hipError_t launch_route(hipStream_t s, const float *router, const void *bias, int bias_type,
                         const float *x, int batch, int hidden, int experts, float *logits,
                         int topk, bool select, const SelectOut &o, uint32_t *counter);
 hipError_t launch_select(hipStream_t s, const float *logits, int batch, int experts, int topk,
                          const SelectOut &o);
-hipError_t launch_mx_gemv(hipStream_t s, GemvMode mode, const MxGemvArgs &a, int slots);
+hipError_t launch_mx_mfma(hipStream_t s, GemvMode mode, const MxMfmaArgs &a, int slots);
 hipError_t launch_q40_gemv(hipStream_t s, const Q40Args &a);
 hipError_t launch_combine(hipStream_t s, const float *results, const float *weights, int batch,
                           int topk, int hidden, float *out);

@@ -1,12 +1,11 @@
 // spt_kernels.hip -- gfx950 kernels of the quantized MoE hot path.
 //
-// Work decomposition of every weight-streaming kernel: 16 lanes per weight
-// row (one DPP row of a 64-wide wavefront), 16 rows per 256-thread
-// workgroup.  Lane j of a row owns blocks j, j+16, j+32, ... so each group of
-// 16 lanes reads 16 consecutive 17/18-byte blocks (272/288 contiguous bytes)
-// per load, and every weight byte is fetched from HBM exactly once per
-// workgroup.  Activations (Q8_0 codes + scales of the workgroup's tokens) are
-// staged in LDS once and shared by the 16 rows.
+// The Q4_0 GEMV uses 16 lanes per weight row (one DPP row of a 64-wide
+// wavefront), 16 rows per 256-thread workgroup: lane j of a row owns blocks
+// j, j+16, j+32, ... so each group of 16 lanes reads 16 consecutive 18-byte
+// blocks (288 contiguous bytes) per load.  Activations (Q8_0 codes + scales
+// of the workgroup's tokens) are staged in LDS once and shared by the rows.
+// The MXFP4 GEMV lives in spt_mx_mfma.hip.
 #include "spt_device.h"
 #include "spt_kernels.h"
 
@@ -22,6 +21,7 @@ __global__ __launch_bounds__(kWG) void k_quantize(const float *__restrict__ x, i
                                                   int8_t *__restrict__ codes,
                                                   float *__restrict__ scales,
                                                   int32_t *__restrict__ sumq,
+                                                  uint8_t *__restrict__ mxtab,
                                                   uint8_t *__restrict__ blocks34) {
     int64_t b = (int64_t)blockIdx.x * kWG + threadIdx.x;
     if (b >= nblocks) return;
@@ -31,34 +31,20 @@ __global__ __launch_bounds__(kWG) void k_quantize(const float *__restrict__ x, i
     uint32_t w[8];
     uint16_t dh;
     q8_quantize32(v, w, &dh);
-    if (codes) {
-        uint32_t *c = reinterpret_cast<uint32_t *>(codes + b * 32);
-#pragma unroll
-        for (int k = 0; k < 8; k++) c[k] = w[k];
-    }
-    if (scales) scales[b] = f16_bits_to_f32(dh);
+    write_q8_block(w, dh, (size_t)b, codes, scales, mxtab, blocks34);
     if (sumq) {
         int32_t s = 0;
 #pragma unroll
         for (int k = 0; k < 8; k++) s = __builtin_amdgcn_sdot4((int)w[k], 0x01010101, s, false);
         sumq[b] = s;
     }
-    if (blocks34) {
-        uint8_t *o = blocks34 + b * kQ80Block;
-        o[0] = (uint8_t)(dh & 0xff);
-        o[1] = (uint8_t)(dh >> 8);
-#pragma unroll
-        for (int k = 0; k < 8; k++)
-#pragma unroll
-            for (int i = 0; i < 4; i++) o[2 + 4 * k + i] = (uint8_t)(w[k] >> (8 * i));
-    }
 }
 
 hipError_t launch_quantize(hipStream_t s, const float *x, int64_t nblocks, int8_t *codes,
-                           float *scales, int32_t *sumq, uint8_t *blocks34) {
+                           float *scales, int32_t *sumq, uint8_t *mxtab, uint8_t *blocks34) {
     if (nblocks <= 0) return hipSuccess;
     dim3 grid((unsigned)((nblocks + kWG - 1) / kWG));
-    hipLaunchKernelGGL(k_quantize, grid, dim3(kWG), 0, s, x, nblocks, codes, scales, sumq, blocks34);
+    hipLaunchKernelGGL(k_quantize, grid, dim3(kWG), 0, s, x, nblocks, codes, scales, sumq, mxtab, blocks34);
     return hipGetLastError();
 }
 
@@ -259,163 +245,6 @@ hipError_t launch_select(hipStream_t s, const float *logits, int batch, int expe
     hipLaunchKernelGGL(k_select, dim3(1), dim3(kWG), select_lds(batch, experts, topk), s, logits,
                        batch, experts, topk, o);
     return hipGetLastError();
-}
-
-// ---------------------------------------------------------------------------
-// Grouped MXFP4 x Q8_0 GEMV.
-//   kGateUp: per active expert, gate and up rows for every token in the
-//            expert's list, bias, clamped SwiGLU -> act[idx][row].
-//   kDown:   per active expert, down rows for every selection in the list,
-//            bias -> results[idx][row].
-//   kRows:   one expert, consecutive tokens -> y[t][row] (+ bias).
-// blockIdx.x = slot * tiles + tile; the workgroup's 16 rows are tile*16...
-// ---------------------------------------------------------------------------
-template <int MODE, int MAXP, int NT>
-__global__ __launch_bounds__(kWG) void k_mx_gemv(MxGemvArgs a) {
-    constexpr int NMAT = MODE == kGateUp ? 2 : 1;
-    extern __shared__ uint32_t smem_u[];
-    __shared__ int s_entry[NT];
-    __shared__ int s_arow[NT];
-    const int nb = a.nb, words = nb * 8;
-    uint32_t *s_codes = smem_u;
-    float *s_scales = reinterpret_cast<float *>(smem_u + NT * words);
-
-    const int tiles = (a.rows + kRowsPerWG - 1) / kRowsPerWG;
-    const int slot = blockIdx.x / tiles, tile = blockIdx.x - slot * tiles;
-    int e, begin, count;
-    if (MODE == kRows) {
-        e = a.expert;
-        begin = 0;
-        count = a.ntok;
-    } else {
-        if (slot >= *a.n_active) return;
-        e = a.active[slot];
-        begin = a.offsets[e];
-        count = a.offsets[e + 1] - begin;
-    }
-    const int tid = threadIdx.x, j = tid & 15, g = tid >> 4;
-    const int r = tile * kRowsPerWG + g;
-    const bool row_ok = r < a.rows;
-    const uint32_t row_pos = (uint32_t)(row_ok ? r : 0) * (uint32_t)(nb * kMxBlock);
-    ByteView view[NMAT];
-#pragma unroll
-    for (int m = 0; m < NMAT; m++) view[m] = make_view(a.w[m] + (uint64_t)e * a.expert_bytes, a.expert_bytes);
-
-    for (int c0 = 0; c0 < count; c0 += NT) {
-        const int nt = min(NT, count - c0);
-        if (tid < nt) {
-            int ent = MODE == kRows ? c0 + tid : a.list[begin + c0 + tid];
-            s_entry[tid] = ent;
-            s_arow[tid] = MODE == kGateUp ? ent / a.topk : ent;
-        }
-        __syncthreads();
-        for (int t = 0; t < nt; t++) {
-            const uint32_t *src = reinterpret_cast<const uint32_t *>(a.codes + (size_t)s_arow[t] * nb * 32);
-            for (int i = tid; i < words; i += kWG) s_codes[t * words + i] = src[i];
-            const float *ss = a.scales + (size_t)s_arow[t] * nb;
-            for (int i = tid; i < nb; i += kWG) s_scales[t * nb + i] = ss[i];
-        }
-        __syncthreads();
-
-        float acc[NMAT][NT];
-#pragma unroll
-        for (int m = 0; m < NMAT; m++)
-#pragma unroll
-            for (int t = 0; t < NT; t++) acc[m][t] = 0.0f;
-
-        for (int seg = 0; seg < nb; seg += 16 * MAXP) {
-            uint32_t raw[NMAT][MAXP][5];
-            uint32_t off[NMAT][MAXP];
-#pragma unroll
-            for (int p = 0; p < MAXP; p++) {
-                const int b = seg + j + 16 * p;
-                if (row_ok && b < nb) {
-#pragma unroll
-                    for (int m = 0; m < NMAT; m++)
-                        load_block5(view[m], row_pos + (uint32_t)b * kMxBlock, raw[m][p], &off[m][p]);
-                }
-            }
-#pragma unroll
-            for (int p = 0; p < MAXP; p++) {
-                const int b = seg + j + 16 * p;
-                if (row_ok && b < nb) {
-#pragma unroll
-                    for (int m = 0; m < NMAT; m++) {
-                        MxDecoded dec;
-                        mx_decode(raw[m][p], off[m][p], dec);
-#pragma unroll
-                        for (int t = 0; t < NT; t++) {
-                            if (t < nt) {
-                                const uint4 *q4 = reinterpret_cast<const uint4 *>(s_codes + t * words + b * 8);
-                                uint4 qa = q4[0], qb = q4[1];
-                                uint32_t q[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
-                                int32_t s = mx_isum(dec, q);
-                                float ds = mx_block_scale(s_scales[t * nb + b], dec.e);
-                                acc[m][t] = __builtin_fmaf((float)s, ds, acc[m][t]);
-                            }
-                        }
-                    }
-                }
-            }
-        }
-#pragma unroll
-        for (int m = 0; m < NMAT; m++)
-#pragma unroll
-            for (int t = 0; t < NT; t++) {
-                float v = acc[m][t];
-                v += __shfl_xor(v, 8, 16);
-                v += __shfl_xor(v, 4, 16);
-                v += __shfl_xor(v, 2, 16);
-                v += __shfl_xor(v, 1, 16);
-                acc[m][t] = v;
-            }
-        if (j == 0 && row_ok) {
-            const uint64_t brow = (uint64_t)e * a.rows + r;
-#pragma unroll
-            for (int t = 0; t < NT; t++) {
-                if (t >= nt) continue;
-                const int ent = s_entry[t];
-                const size_t o = (size_t)ent * a.rows + r;
-                if (MODE == kGateUp) {
-                    float gv = acc[0][t] + bias_at(a.bias[0], a.bias_type[0], brow);
-                    float uv = acc[NMAT - 1][t] + bias_at(a.bias[1], a.bias_type[1], brow);
-                    a.out[o] = swiglu(gv, uv);
-                    if (a.tap[0]) a.tap[0][o] = gv;
-                    if (a.tap[1]) a.tap[1][o] = uv;
-                } else {
-                    a.out[o] = acc[0][t] + bias_at(a.bias[0], a.bias_type[0], brow);
-                }
-            }
-        }
-        __syncthreads();
-    }
-}
-
-template <int MODE, int MAXP>
-static hipError_t launch_mx_mode(hipStream_t s, const MxGemvArgs &a, int slots) {
-    constexpr int NT = 4;
-    const int tiles = (a.rows + kRowsPerWG - 1) / kRowsPerWG;
-    size_t lds = (size_t)NT * a.nb * (32 + 4);
-    hipLaunchKernelGGL((k_mx_gemv<MODE, MAXP, NT>), dim3(slots * tiles), dim3(kWG), lds, s, a);
-    return hipGetLastError();
-}
-
-template <int MODE>
-static hipError_t launch_mx_maxp(hipStream_t s, const MxGemvArgs &a, int slots) {
-    const int per_lane = (a.nb + 15) / 16;
-    if (per_lane <= 1) return launch_mx_mode<MODE, 1>(s, a, slots);
-    if (per_lane <= 2) return launch_mx_mode<MODE, 2>(s, a, slots);
-    if (per_lane <= 4) return launch_mx_mode<MODE, 4>(s, a, slots);
-    return launch_mx_mode<MODE, 6>(s, a, slots);
-}
-
-hipError_t launch_mx_gemv(hipStream_t s, GemvMode mode, const MxGemvArgs &a, int slots) {
-    if (slots <= 0 || a.rows <= 0) return hipSuccess;
-    switch (mode) {
-    case kGateUp: return launch_mx_maxp<kGateUp>(s, a, slots);
-    case kDown: return launch_mx_maxp<kDown>(s, a, slots);
-    default: return launch_mx_maxp<kRows>(s, a, slots);
-    }
 }
 
 // ---------------------------------------------------------------------------
