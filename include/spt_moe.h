@@ -130,12 +130,13 @@ int spt_ctx_set_cancel_flag(struct spt_ctx *ctx, const volatile int32_t *flag);
  * each launch (measurement instrumentation, off by default).  Kernel kinds: */
 enum {
     SPT_KERNEL_QUANTIZE = 0, /* activation -> Q8_0                           */
-    SPT_KERNEL_ROUTE = 1,    /* router logits + top-k + per-expert packing   */
+    SPT_KERNEL_ROUTE = 1,    /* router logits (+ Q8_0 of the input)          */
     SPT_KERNEL_GATE_UP = 2,  /* grouped gate/up GEMV + bias + SwiGLU        */
     SPT_KERNEL_DOWN = 3,     /* grouped down GEMV + bias                      */
     SPT_KERNEL_COMBINE = 4,  /* weighted combine                              */
     SPT_KERNEL_Q40 = 5,      /* Q4_0 GEMV / small GEMM                        */
-    SPT_KERNEL_KINDS = 6
+    SPT_KERNEL_SELECT = 6,   /* top-k + softmax + per-expert packing          */
+    SPT_KERNEL_KINDS = 7
 };
 int spt_ctx_enable_timing(struct spt_ctx *ctx, int enable);
 /* Synchronise, then write the summed milliseconds and launch counts of each

@@ -23,7 +23,6 @@ struct spt_ctx {
     const volatile int32_t *cancel = nullptr;
     void *scratch = nullptr;
     size_t scratch_bytes = 0;
-    uint32_t *counter = nullptr;  // last-workgroup counter of the router
     bool timing = false;
     std::vector<std::pair<int, std::pair<hipEvent_t, hipEvent_t>>> pending;
     std::vector<hipEvent_t> free_events;
@@ -285,20 +284,22 @@ int run_moe(spt_ctx *ctx, const spt_moe_layer *lw, const float *x, float *out, c
                       (int32_t *)(S + o_na)};
     hipStream_t s = ctx->stream;
 
-    if ((rc = check_cancel(ctx))) return rc;
-    SPT_HIP(timed(ctx, SPT_KERNEL_QUANTIZE, [&] {
-        return spt::launch_quantize(s, x, B * nbh, xc, xs, nullptr, xm, taps ? (uint8_t *)taps->xq : nullptr);
-    }));
+    const spt::QuantOut xq{xc, xs, xm, taps ? (uint8_t *)taps->xq : nullptr};
     if ((rc = check_cancel(ctx))) return rc;
     if (taps && taps->logits_in) {
-        SPT_HIP(timed(ctx, SPT_KERNEL_ROUTE, [&] { return spt::launch_select(s, taps->logits_in, (int)B, (int)E, (int)k, so); }));
+        SPT_HIP(timed(ctx, SPT_KERNEL_QUANTIZE, [&] {
+            return spt::launch_quantize(s, x, B * nbh, xq.codes, xq.scales, nullptr, xq.mxtab, xq.blocks34);
+        }));
+        SPT_HIP(timed(ctx, SPT_KERNEL_SELECT, [&] { return spt::launch_select(s, taps->logits_in, (int)B, (int)E, (int)k, so); }));
         if ((rc = copy_tap(ctx, taps->logits, taps->logits_in, B * E * 4))) return rc;
     } else {
+        // router logits + Q8_0 of x in one launch, then top-k + lists
         SPT_HIP(timed(ctx, SPT_KERNEL_ROUTE, [&] {
             return spt::launch_route(s, (const float *)lw->ffn_gate_inp.data, bias_ptr(lw->ffn_gate_inp_bias),
-                                     bias_type(lw->ffn_gate_inp_bias), x, (int)B, (int)h, (int)E, logits,
-                                     (int)k, true, so, ctx->counter);
+                                     bias_type(lw->ffn_gate_inp_bias), x, (int)B, (int)h, (int)E, logits, xq);
         }));
+        if ((rc = check_cancel(ctx))) return rc;
+        SPT_HIP(timed(ctx, SPT_KERNEL_SELECT, [&] { return spt::launch_select(s, logits, (int)B, (int)E, (int)k, so); }));
         if (taps && (rc = copy_tap(ctx, taps->logits, logits, B * E * 4))) return rc;
     }
     const int slots = (int)(n < E ? n : E);
@@ -420,12 +421,6 @@ int spt_ctx_create(int device, void *hip_stream, spt_ctx **out) {
             return hip_fail(err, "hipSetDevice");
         }
         ctx->stream = (hipStream_t)hip_stream;  // NULL: the device's default stream
-        if ((err = hipMalloc(&ctx->counter, 256)) != hipSuccess ||
-            (err = hipMemset(ctx->counter, 0, 256)) != hipSuccess) {
-            if (ctx->own_stream) (void)hipStreamDestroy(ctx->stream);
-            delete ctx;
-            return hip_fail(err, "counter allocation");
-        }
     }
     *out = ctx;
     return SPT_OK;
@@ -437,7 +432,6 @@ int spt_ctx_destroy(spt_ctx *ctx) {
         (void)hipSetDevice(ctx->device);
         (void)hipStreamSynchronize(ctx->stream);
         if (ctx->scratch) (void)hipFree(ctx->scratch);
-        if (ctx->counter) (void)hipFree(ctx->counter);
         for (auto &p : ctx->pending) {
             (void)hipEventDestroy(p.second.first);
             (void)hipEventDestroy(p.second.second);
@@ -663,13 +657,13 @@ int spt_route_moe_batch(spt_ctx *ctx, const spt_tensor *router, const spt_tensor
     spt_tensor none{};
     if ((rc = validate_bias(bias ? bias : &none, E, 1))) return rc;
     if (h % 32 != 0) return fail(SPT_ERR_INVALID, "hidden dimension %lld is not a multiple of 32", (long long)h);
-    if (batch < 1 || batch > INT_MAX / E) return fail(SPT_ERR_INVALID, "invalid or oversized batch: %lld", (long long)batch);
+    if (E > 65535) return fail(SPT_ERR_INVALID, "too many experts: %lld", (long long)E);
+    if (batch < 1 || batch > 65535 || batch > INT_MAX / E) return fail(SPT_ERR_INVALID, "invalid or oversized batch: %lld", (long long)batch);
     if (!x_dev || !logits_dev) return fail(SPT_ERR_INVALID, "nil input or output");
     if ((rc = check_device(ctx)) || (rc = check_cancel(ctx))) return rc;
-    spt::SelectOut none_out{};
+    spt::QuantOut no_q{};
     SPT_HIP(spt::launch_route(ctx->stream, (const float *)router->data, bias ? bias_ptr(*bias) : nullptr,
-                              bias ? bias_type(*bias) : 0, x_dev, (int)batch, (int)h, (int)E, logits_dev, 1,
-                              false, none_out, ctx->counter));
+                              bias ? bias_type(*bias) : 0, x_dev, (int)batch, (int)h, (int)E, logits_dev, no_q));
     return SPT_OK;
 }
 

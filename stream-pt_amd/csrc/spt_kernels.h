@@ -7,7 +7,7 @@
 namespace spt {
 
 constexpr int kMaxTopK = 16;
-constexpr int kMaxExperts = 1024;
+constexpr int kMaxExperts = 256;
 constexpr int kMaxSelections = 4096;
 
 struct SelectOut {
@@ -18,6 +18,14 @@ struct SelectOut {
     int32_t *list;
     int32_t *active;
     int32_t *n_active;
+};
+
+// Optional Q8_0 outputs of a quantized activation (see write_q8_block).
+struct QuantOut {
+    int8_t *codes;
+    float *scales;
+    uint8_t *mxtab;
+    uint8_t *blocks34;
 };
 
 enum GemvMode { kGateUp = 0, kDown = 1, kRows = 2 };
@@ -68,9 +76,11 @@ struct Q40Args {
 
 hipError_t launch_quantize(hipStream_t s, const float *x, int64_t nblocks, int8_t *codes,
                            float *scales, int32_t *sumq, uint8_t *mxtab, uint8_t *blocks34);
+// Router logits [batch][experts]; Q8_0 of x into q when q.codes or q.blocks34 is set.
 hipError_t launch_route(hipStream_t s, const float *router, const void *bias, int bias_type,
                         const float *x, int batch, int hidden, int experts, float *logits,
-                        int topk, bool select, const SelectOut &o, uint32_t *counter);
+                        const QuantOut &q);
+// Top-k + softmax per token, then the per-expert lists (one workgroup).
 hipError_t launch_select(hipStream_t s, const float *logits, int batch, int experts, int topk,
                          const SelectOut &o);
 hipError_t launch_mx_mfma(hipStream_t s, GemvMode mode, const MxMfmaArgs &a, int slots);

@@ -70,179 +70,233 @@ __device__ inline float router_reduce(float a, int lane) {
     return (p + p1) + (p2 + p3);
 }
 
-// Top-k + softmax for every token, then the per-expert lists.  Runs on one
-// workgroup.  s_ids/s_w: [batch*k], s_cnt/s_off: [experts(+1)] in LDS.
-// Lane L owns experts L, L+64, ...; a per-lane bit mask marks the ones already
-// selected for the current token, so exclusion costs one bit test.
-__device__ void select_pack(const float *logits, int batch, int E, int k, const SelectOut &o,
-                            int32_t *s_ids, float *s_w, int32_t *s_cnt, int32_t *s_off) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
-    const int n = batch * k;
-    for (int t = wave; t < batch; t += nw) {
-        const float *lg = logits + (size_t)t * E;
-        uint32_t taken = 0;
-#pragma unroll 1
-        for (int r = 0; r < k; r++) {
-            // selectMoEBatch round r: strict '>' scan, lowest index wins
-            // ties, NaN and -Inf never win, picked experts are excluded.
-            float bv = -__builtin_inff();
-            int bi = -1;
-#pragma unroll 1
-            for (int ex = lane, i = 0; ex < E; ex += 64, i++) {
-                float v = lg[ex];
-                if (!((taken >> i) & 1u) && v > bv) {
-                    bv = v;
-                    bi = ex;
-                }
-            }
+// selectMoEBatch (forward/moe_batch.go:305-342) for one token by one
+// wavefront: k rounds of a strict '>' scan where the lowest index wins ties,
+// NaN and -Inf never win and picked experts are excluded (lane L owns experts
+// L, L+64, ...; a per-lane bit mask marks the picked ones); a round with
+// nothing selectable falls back to Index = round, logit 0.  Then the softmax
+// over the k logits: w = f32(exp(f64(l - max))) (lane r computes rank r's),
+// summed in f32 in rank order, scaled by 1/sum when sum > 0.  Results go to
+// LDS (s_ids/s_w, the token's k slots) and to global ids/weights.
+__device__ void select_token(const float *lg, int E, int k, int32_t *ids, float *weights,
+                             int32_t *s_ids, float *s_w) {
+    const int lane = threadIdx.x & 63;
+    float v[kMaxExperts / 64];
 #pragma unroll
-            for (int off = 32; off >= 1; off >>= 1) {
-                float ov = __shfl_xor(bv, off);
-                int oi = __shfl_xor(bi, off);
-                bool take = oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi));
-                if (take) {
-                    bv = ov;
-                    bi = oi;
-                }
-            }
-            if (bi < 0) {  // nothing selectable: fallback Index=k, logit 0
-                bi = r;
-                bv = 0.0f;
-            }
-            if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
-            if (lane == 0) {
-                s_ids[t * k + r] = bi;
-                s_w[t * k + r] = bv;
+    for (int i = 0; i < kMaxExperts / 64; i++) {
+        const int ex = lane + 64 * i;
+        v[i] = ex < E ? lg[ex] : -__builtin_inff();
+    }
+    uint32_t taken = 0;
+    int my_id = 0;
+    float my_val = 0.0f;
+    for (int r = 0; r < k; r++) {
+        float bv = -__builtin_inff();
+        int bi = -1;
+#pragma unroll
+        for (int i = 0; i < kMaxExperts / 64; i++) {
+            if (!((taken >> i) & 1u) && v[i] > bv) {
+                bv = v[i];
+                bi = lane + 64 * i;
             }
         }
-        if (lane == 0) {
-            float mx = -__builtin_inff();
-#pragma unroll 1
-            for (int r = 0; r < k; r++)
-                if (s_w[t * k + r] > mx) mx = s_w[t * k + r];
-            float sum = 0.0f;
-#pragma unroll 1
-            for (int r = 0; r < k; r++) {
-                float w = static_cast<float>(exp(static_cast<double>(s_w[t * k + r] - mx)));
-                s_w[t * k + r] = w;
-                sum += w;
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) {
+            const float ov = __shfl_xor(bv, off);
+            const int oi = __shfl_xor(bi, off);
+            const bool take = oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi));
+            if (take) {
+                bv = ov;
+                bi = oi;
             }
-            float inv = sum > 0.0f ? 1.0f / sum : 1.0f;
-#pragma unroll 1
-            for (int r = 0; r < k; r++) {
-                float w = s_w[t * k + r];
-                if (sum > 0.0f) w *= inv;
-                s_w[t * k + r] = w;
-                o.ids[t * k + r] = s_ids[t * k + r];
-                o.weights[t * k + r] = w;
-            }
+        }
+        if (bi < 0) {
+            bi = r;
+            bv = 0.0f;
+        }
+        if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
+        if (lane == r) {
+            my_id = bi;
+            my_val = bv;
         }
     }
-    for (int i = threadIdx.x; i < E; i += blockDim.x) s_cnt[i] = 0;
+    // max over ranks in order (NaN never replaces: strict '>')
+    float mx = -__builtin_inff();
+    for (int r = 0; r < k; r++) {
+        const float l = __shfl(my_val, r);
+        if (l > mx) mx = l;
+    }
+    const float e = lane < k ? static_cast<float>(exp(static_cast<double>(my_val - mx))) : 0.0f;
+    float sum = 0.0f;
+    for (int r = 0; r < k; r++) sum += __shfl(e, r);
+    if (lane < k) {
+        const float w = sum > 0.0f ? e * (1.0f / sum) : e;
+        s_ids[lane] = my_id;
+        s_w[lane] = w;
+        ids[lane] = my_id;
+        weights[lane] = w;
+    }
+}
+
+// Per-expert lists (forward/moe_batch.go:142-159) for n = batch*k selections
+// held in LDS (s_ids/s_w), by one workgroup of kSelWG threads.  Selections
+// with Weight <= 0 are skipped (NaN weights are kept); experts ascending;
+// inside a list descending idx, as the reference's push-at-head linked list
+// yields.  Counts by LDS atomics, offsets and the active-expert list by one
+// wavefront's prefix scan; ranks from kSelChunk-entry chunks taken in
+// descending idx order: a per-expert bit row marks the chunk's members, so an
+// entry's rank is its expert's running count plus the bits below it.
+constexpr int kSelWG = 1024;
+constexpr int kSelChunk = 512;
+constexpr int kSelWords = kSelChunk / 32;
+
+__device__ void pack_lists(int n, int E, const SelectOut &o, const int32_t *s_ids, const float *s_w,
+                           int32_t *s_cnt, int32_t *s_off, int32_t *s_run, uint32_t *s_bits) {
+    const int tid = threadIdx.x;
+    for (int i = tid; i < E; i += blockDim.x) {
+        s_cnt[i] = 0;
+        s_run[i] = 0;
+    }
     __syncthreads();
-    // Selections with Weight <= 0 are skipped (NaN weights are kept).
-    for (int i = threadIdx.x; i < n; i += blockDim.x)
+    for (int i = tid; i < n; i += blockDim.x)
         if (!(s_w[i] <= 0.0f)) atomicAdd(&s_cnt[s_ids[i]], 1);
     __syncthreads();
-    if (threadIdx.x == 0) {
+    if (tid < 64) {
         int pos = 0, na = 0;
-        for (int e = 0; e < E; e++) {
-            s_off[e] = pos;
-            pos += s_cnt[e];
-            if (s_cnt[e] > 0) o.active[na++] = e;
+        for (int e0 = 0; e0 < E; e0 += 64) {
+            const int e = e0 + tid;
+            const int c = e < E ? s_cnt[e] : 0;
+            int incl = c;
+#pragma unroll
+            for (int d = 1; d < 64; d <<= 1) {
+                const int up = __shfl_up(incl, d);
+                if (tid >= d) incl += up;
+            }
+            const uint64_t act = __ballot(c > 0);
+            const int arank = __builtin_popcountll(act & ((1ull << tid) - 1ull));
+            if (e < E) {
+                s_off[e] = pos + incl - c;
+                o.offsets[e] = pos + incl - c;
+                o.counts[e] = c;
+                if (c > 0) o.active[na + arank] = e;
+            }
+            pos += __shfl(incl, 63);
+            na += __builtin_popcountll(act);
         }
-        s_off[E] = pos;
-        *o.n_active = na;
+        if (tid == 0) {
+            s_off[E] = pos;
+            o.offsets[E] = pos;
+            *o.n_active = na;
+        }
     }
-    __syncthreads();
-    for (int i = threadIdx.x; i <= E; i += blockDim.x) {
-        o.offsets[i] = s_off[i];
-        if (i < E) o.counts[i] = s_cnt[i];
-    }
-    // Linked-list order: each expert's entries in descending idx.
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
-        if (s_w[i] <= 0.0f) continue;
-        int e = s_ids[i], rank = 0;
-        for (int q = i + 1; q < n; q++) rank += (s_ids[q] == e && !(s_w[q] <= 0.0f)) ? 1 : 0;
-        o.list[s_off[e] + rank] = i;
+    for (int p0 = 0; p0 < n; p0 += kSelChunk) {
+        for (int i = tid; i < E * kSelWords; i += blockDim.x) s_bits[i] = 0u;
+        __syncthreads();
+        const int p = p0 + tid;
+        const int idx = n - 1 - p;
+        const bool valid = tid < kSelChunk && p < n && !(s_w[idx] <= 0.0f);
+        const int e = valid ? s_ids[idx] : 0;
+        if (valid) atomicOr(&s_bits[e * kSelWords + (tid >> 5)], 1u << (tid & 31));
+        __syncthreads();
+        if (valid) {
+            int rank = s_run[e];
+            const int wi = tid >> 5;
+            for (int w = 0; w < wi; w++) rank += __builtin_popcount(s_bits[e * kSelWords + w]);
+            rank += __builtin_popcount(s_bits[e * kSelWords + wi] & ((1u << (tid & 31)) - 1u));
+            o.list[s_off[e] + rank] = idx;
+        }
+        __syncthreads();
+        for (int i = tid; i < E; i += blockDim.x) {
+            int add = 0;
+            for (int w = 0; w < kSelWords; w++) add += __builtin_popcount(s_bits[i * kSelWords + w]);
+            s_run[i] += add;
+        }
+        __syncthreads();
     }
 }
 
-constexpr int kRouteTokens = 8;
+static size_t select_lds(int n, int E) {
+    return sizeof(int32_t) * (2 * (size_t)n + 3 * (size_t)E + 1) + sizeof(uint32_t) * kSelWords * (size_t)E;
+}
 
+// Router logits: one workgroup per (4 experts, 1 token); wave w computes the
+// logit of expert 4*blockIdx.x + w for token blockIdx.y (16 chunk loads in
+// flight per lane).  With q set, workgroup (0, t) also quantizes token t's
+// row of x to Q8_0.
 __global__ __launch_bounds__(kWG) void k_route(const float *__restrict__ router,
                                                const void *bias, int bias_type,
-                                               const float *__restrict__ x, int batch, int H,
-                                               int E, float *logits, int topk, int do_select,
-                                               SelectOut o, uint32_t *counter) {
-    extern __shared__ int32_t smem_i[];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+                                               const float *__restrict__ x, int H, int E,
+                                               float *__restrict__ logits, QuantOut q) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int e = blockIdx.x * 4 + wave;
-    const int t0 = blockIdx.y * kRouteTokens;
-    if (e < E) {
-        const float *w = router + (size_t)e * H;
-        const float be = bias_at(bias, bias_type, e);
-        for (int t = t0; t < batch && t < t0 + kRouteTokens; t++) {
-            const float *xt = x + (size_t)t * H;
-            float acc = 0.0f;
-            int off = 0;
-            for (; off + 64 <= H; off += 64) acc = __builtin_fmaf(w[off + lane], xt[off + lane], acc);
-            if (off < H && lane < 32) acc = __builtin_fmaf(w[off + lane], xt[off + lane], acc);
-            float r = router_reduce(acc, lane);
-            if (lane == 0) {
-                logits[(size_t)t * E + e] = r + be;
-                __threadfence();
-            }
+    const int t = blockIdx.y;
+    const float *xt = x + (size_t)t * H;
+    if (blockIdx.x == 0 && (q.codes || q.blocks34)) {
+        for (int b = tid; b < H / 32; b += kWG) {
+            float v[32];
+#pragma unroll
+            for (int i = 0; i < 32; i++) v[i] = xt[b * 32 + i];
+            uint32_t w[8];
+            uint16_t dh;
+            q8_quantize32(v, w, &dh);
+            write_q8_block(w, dh, (size_t)t * (H / 32) + b, q.codes, q.scales, q.mxtab, q.blocks34);
         }
     }
-    if (!do_select) return;
-    __shared__ int s_last;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        __threadfence();
-        uint32_t total = gridDim.x * gridDim.y;
-        s_last = atomicAdd(counter, 1u) == total - 1;
+    if (e >= E) return;
+    const float *w = router + (size_t)e * H;
+    const int nfull = H / 64;
+    float acc = 0.0f;
+    for (int c0 = 0; c0 < nfull; c0 += 16) {
+        float wv[16], xv[16];
+#pragma unroll
+        for (int u = 0; u < 16; u++) {
+            const int cc = c0 + u;
+            if (cc < nfull) {
+                wv[u] = w[cc * 64 + lane];
+                xv[u] = xt[cc * 64 + lane];
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < 16; u++)
+            if (c0 + u < nfull) acc = __builtin_fmaf(wv[u], xv[u], acc);
     }
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-    const int n = batch * topk;
-    int32_t *s_ids = smem_i;
-    float *s_w = reinterpret_cast<float *>(smem_i + n);
-    int32_t *s_cnt = smem_i + 2 * n;
-    int32_t *s_off = s_cnt + E;
-    select_pack(logits, batch, E, topk, o, s_ids, s_w, s_cnt, s_off);
-    if (threadIdx.x == 0) atomicExch(counter, 0u);
+    if (nfull * 64 < H && lane < 32) acc = __builtin_fmaf(w[nfull * 64 + lane], xt[nfull * 64 + lane], acc);
+    const float r = router_reduce(acc, lane);
+    if (lane == 0) logits[(size_t)t * E + e] = r + bias_at(bias, bias_type, e);
 }
 
-__global__ __launch_bounds__(kWG) void k_select(const float *logits, int batch, int E, int topk,
-                                                SelectOut o) {
+// Selection and packing from the logits of a whole batch: one workgroup;
+// its wavefronts take tokens in turn, then the lists are packed.
+__global__ __launch_bounds__(kSelWG) void k_select(const float *__restrict__ logits, int batch, int E,
+                                                   int topk, SelectOut o) {
     extern __shared__ int32_t smem_i[];
     const int n = batch * topk;
     int32_t *s_ids = smem_i;
     float *s_w = reinterpret_cast<float *>(smem_i + n);
     int32_t *s_cnt = smem_i + 2 * n;
     int32_t *s_off = s_cnt + E;
-    select_pack(logits, batch, E, topk, o, s_ids, s_w, s_cnt, s_off);
-}
-
-static size_t select_lds(int batch, int E, int topk) {
-    return sizeof(int32_t) * (2 * (size_t)batch * topk + 2 * (size_t)E + 1);
+    int32_t *s_run = s_off + E + 1;
+    uint32_t *s_bits = reinterpret_cast<uint32_t *>(s_run + E);
+    const int wave = threadIdx.x >> 6;
+    for (int t = wave; t < batch; t += kSelWG / 64)
+        select_token(logits + (size_t)t * E, E, topk, o.ids + t * topk, o.weights + t * topk,
+                     s_ids + t * topk, s_w + t * topk);
+    __syncthreads();
+    pack_lists(n, E, o, s_ids, s_w, s_cnt, s_off, s_run, s_bits);
 }
 
 hipError_t launch_route(hipStream_t s, const float *router, const void *bias, int bias_type,
                         const float *x, int batch, int hidden, int experts, float *logits,
-                        int topk, bool select, const SelectOut &o, uint32_t *counter) {
-    dim3 grid((experts + 3) / 4, (batch + kRouteTokens - 1) / kRouteTokens);
-    size_t lds = select ? select_lds(batch, experts, topk) : 0;
-    hipLaunchKernelGGL(k_route, grid, dim3(kWG), lds, s, router, bias, bias_type, x, batch,
-                       hidden, experts, logits, topk, select ? 1 : 0, o, counter);
+                        const QuantOut &q) {
+    dim3 grid((experts + 3) / 4, batch);
+    hipLaunchKernelGGL(k_route, grid, dim3(kWG), 0, s, router, bias, bias_type, x, hidden, experts,
+                       logits, q);
     return hipGetLastError();
 }
 
 hipError_t launch_select(hipStream_t s, const float *logits, int batch, int experts, int topk,
                          const SelectOut &o) {
-    hipLaunchKernelGGL(k_select, dim3(1), dim3(kWG), select_lds(batch, experts, topk), s, logits,
+    hipLaunchKernelGGL(k_select, dim3(1), dim3(kSelWG), select_lds(batch * topk, experts), s, logits,
                        batch, experts, topk, o);
     return hipGetLastError();
 }

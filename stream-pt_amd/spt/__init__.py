@@ -31,7 +31,7 @@ EXPORTED = (
     "spt_forward_moe_batch_host", "spt_block_sums", "spt_synth_mxfp4",
     "spt_ctx_enable_timing", "spt_ctx_read_timing",
 )
-KERNEL_KINDS = ("quantize", "route", "gate_up", "down", "combine", "q40")
+KERNEL_KINDS = ("quantize", "route", "gate_up", "down", "combine", "q40", "select")
 
 
 class SptError(RuntimeError):

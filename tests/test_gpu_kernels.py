@@ -194,3 +194,34 @@ def test_router_logits_bit_exact(gpu_ctx, O, hidden, batch):
     want = O.route(W, b, x, batch, hidden, E)
     got = logits.cpu().numpy()
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), np.nonzero(got != want)[0][:8]
+
+
+def test_mxfp4_all_scales(gpu_ctx, O):
+    """TestMXFP4AllScales (mxfp4_optimization_test.go:52-78) through the Q8_0
+    path: one block per row, every E8M0 exponent, nibbles 0x22 (1.0),
+    x = 1/32; exponent 255 with zero nibbles must give NaN.  Row tiles
+    holding exponents outside [4, 254] take the integer-decode fallback."""
+    import math
+
+    import torch
+
+    import spt
+
+    rows = 257
+    data = np.zeros((rows, 17), np.uint8)
+    data[:256, 0] = np.arange(256)
+    data[:256, 1:] = 0x22
+    data[256, 0] = 255
+    data = data.reshape(-1)
+    x = np.full(32, 1.0 / 32, np.float32)
+    wd, xd = _dev(data), _dev(x)
+    y = torch.zeros(rows, dtype=torch.float32, device="cuda")
+    t = spt.Tensor.make("w", spt.TYPE_MXFP4, [32, rows, 1], wd.data_ptr(), data.size)
+    gpu_ctx.mul_mxfp4_expert(t, None, 0, xd, y, 1)
+    torch.cuda.synchronize()
+    got = y.cpu().numpy()
+    want = O.mul_mxfp4_q8(data, _q8_of(O, x), None, 32, rows)
+    assert_close(got, want, what="all scales vs Q8_0 oracle")
+    assert np.isnan(got[256]) and np.isinf(got[255])
+    ref = np.array([math.ldexp(1, s - 127) for s in range(255)], np.float64)
+    assert np.all(np.abs(got[:255] - ref) <= 1e-3 * ref), "closed form 2^(s-127)"
