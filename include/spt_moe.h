@@ -161,12 +161,12 @@ int spt_tensor_upload(struct spt_ctx *ctx, spt_tensor *t, const void *src_host);
  * No reference counterpart: the activation quantizer of this path. */
 int spt_quantize_q8_0(struct spt_ctx *ctx, const float *x_dev, int64_t n, void *out_dev);
 
-/* forward.MulQ40Into (forward/q40.go:128-133): y = W x for a Q4_0 [in, out]
+/* forward.MulQ40Into (forward/q40.go:33-38): y = W x for a Q4_0 [in, out]
  * matrix.  x_len/y_len are element counts (len(x), len(y)). */
 int spt_mul_q40_into(struct spt_ctx *ctx, const spt_tensor *w, const float *x_dev,
                      int64_t x_len, float *y_dev, int64_t y_len);
 
-/* forward.MulQ40BatchInto (forward/q40.go:135-198): batch consecutive
+/* forward.MulQ40BatchInto (forward/q40.go:40-103): batch consecutive
  * vectors, y[b*out + row]. */
 int spt_mul_q40_batch_into(struct spt_ctx *ctx, const spt_tensor *w, const float *x_dev,
                            int64_t x_len, float *y_dev, int64_t y_len, int64_t batch);

@@ -419,7 +419,7 @@ static inline float go_max(float a, float b) {
     return signbit(a) ? b : a;
 }
 
-/* forward/moe.go:195-199 (gptOSSSwiGLU). */
+/* forward/moe.go:66-70 (gptOSSSwiGLU). */
 float so_swiglu(float gate, float up) {
     float g = go_min(gate, 7.0f);
     float u = go_max(-7.0f, go_min(up, 7.0f));

@@ -21,6 +21,16 @@
  * Every function is pinned by tests/test_oracle_*.py against the reference's
  * own known-answer tests, its deterministic fixture formulas evaluated in
  * float64, closed forms, and library routines (numpy float16, math.ldexp).
+ *
+ * Parity unpinned (bit level only): the reference is Go with the
+ * experimental simd package and no Go toolchain is present, so the exact
+ * fp32 bit patterns of its AVX2 reductions (so_dot_mxfp4_f32, so_dot_q40_f32,
+ * so_dot_q80_f32, so_dot_q40_batch_f32, so_dot_f32 / so_route) and of Go's
+ * math.Exp inside so_select / so_swiglu cannot be observed.  These functions
+ * follow the documented lane order and are pinned to the reference tests'
+ * tolerances (3e-5 / 1e-4 relative) and, lane by lane, to scalar
+ * restatements; their bits against Go itself stay unpinned.  The codecs, the
+ * Q8_0 quantizer, the integer block sums and the grouping are pinned exactly.
  */
 #ifndef SPT_ORACLE_H
 #define SPT_ORACLE_H

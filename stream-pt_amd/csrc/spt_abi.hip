@@ -148,7 +148,7 @@ struct Carve {
     }
 };
 
-// q40Shape (forward/q40.go:200-225).
+// q40Shape (forward/q40.go:105-130).
 int q40_shape(const spt_tensor *t, int64_t *in, int64_t *out, int64_t *row_bytes) {
     if (t->type != SPT_TYPE_Q4_0)
         return fail(SPT_ERR_INVALID, "\"%s\": GGML type %u instead of Q4_0 (2)", tname(t), t->type);

@@ -309,7 +309,7 @@ __device__ inline void write_q8_lane(int q, uint16_t dh, int lane, size_t blk, i
     }
 }
 
-// ---- clamped SwiGLU (forward/moe.go:195-199) ------------------------------------
+// ---- clamped SwiGLU (forward/moe.go:66-70) ------------------------------------
 // Go's min/max return NaN when either operand is NaN; the comparisons below
 // keep that (a NaN gate or up propagates).
 __device__ inline float swiglu(float gate, float up) {
