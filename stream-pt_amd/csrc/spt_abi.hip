@@ -212,6 +212,7 @@ int validate_bias(const spt_tensor *t, int64_t dim, int64_t count) {
 
 const void *bias_ptr(const spt_tensor &t) { return named(t) ? t.data : nullptr; }
 int bias_type(const spt_tensor &t) { return named(t) ? (int)t.type : 0; }
+uint64_t bias_bytes(const spt_tensor &t) { return named(t) ? t.nbytes : 0; }
 
 struct MoEDims {
     int64_t h, d, E, k, batch;
@@ -269,7 +270,7 @@ int run_moe(spt_ctx *ctx, const spt_moe_layer *lw, const float *x, float *out, c
     size_t o_xc = c.take(B * h), o_xs = c.take(B * nbh * 4), o_xm = c.take(B * nbh * 64);
     size_t o_logits = c.take(B * E * 4);
     size_t o_ids = c.take(n * 4), o_w = c.take(n * 4), o_cnt = c.take(E * 4), o_off = c.take((E + 1) * 4);
-    size_t o_list = c.take(n * 4), o_act_list = c.take(E * 4), o_na = c.take(4);
+    size_t o_list = c.take(n * 4), o_act_list = c.take(E * 4), o_na = c.take(4), o_pass = c.take((E + 1) * 4);
     size_t o_act = c.take(n * d * 4), o_ac = c.take(n * d), o_as = c.take(n * nbd * 4), o_am = c.take(n * nbd * 64);
     size_t o_res = c.take(n * h * 4);
     char *S;
@@ -281,7 +282,7 @@ int run_moe(spt_ctx *ctx, const spt_moe_layer *lw, const float *x, float *out, c
     float *as = (float *)(S + o_as), *res = (float *)(S + o_res);
     spt::SelectOut so{(int32_t *)(S + o_ids), (float *)(S + o_w), (int32_t *)(S + o_cnt),
                       (int32_t *)(S + o_off), (int32_t *)(S + o_list), (int32_t *)(S + o_act_list),
-                      (int32_t *)(S + o_na)};
+                      (int32_t *)(S + o_na), (int32_t *)(S + o_pass)};
     hipStream_t s = ctx->stream;
 
     const spt::QuantOut xq{xc, xs, xm, taps ? (uint8_t *)taps->xq : nullptr};
@@ -311,13 +312,16 @@ int run_moe(spt_ctx *ctx, const spt_moe_layer *lw, const float *x, float *out, c
     ga.nb = (int)nbh;
     ga.bias[0] = bias_ptr(lw->ffn_gate_exps_bias);
     ga.bias_type[0] = bias_type(lw->ffn_gate_exps_bias);
+    ga.bias_bytes[0] = bias_bytes(lw->ffn_gate_exps_bias);
     ga.bias[1] = bias_ptr(lw->ffn_up_exps_bias);
     ga.bias_type[1] = bias_type(lw->ffn_up_exps_bias);
+    ga.bias_bytes[1] = bias_bytes(lw->ffn_up_exps_bias);
     ga.mxtab = xm;
     ga.scales = xs;
     ga.codes = xc;
     ga.active = so.active;
     ga.n_active = so.n_active;
+    ga.pass_off = so.pass_off;
     ga.offsets = so.offsets;
     ga.list = so.list;
     ga.topk = (int)k;
@@ -337,11 +341,13 @@ int run_moe(spt_ctx *ctx, const spt_moe_layer *lw, const float *x, float *out, c
     da.nb = (int)nbd;
     da.bias[0] = bias_ptr(lw->ffn_down_exps_bias);
     da.bias_type[0] = bias_type(lw->ffn_down_exps_bias);
+    da.bias_bytes[0] = bias_bytes(lw->ffn_down_exps_bias);
     da.mxtab = am;
     da.scales = as;
     da.codes = ac;
     da.active = so.active;
     da.n_active = so.n_active;
+    da.pass_off = so.pass_off;
     da.offsets = so.offsets;
     da.list = so.list;
     da.topk = (int)k;
@@ -634,6 +640,7 @@ int spt_mul_mxfp4_expert(spt_ctx *ctx, const spt_tensor *w, const spt_tensor *bi
     a.nb = (int)nb;
     a.bias[0] = bias ? bias_ptr(*bias) : nullptr;
     a.bias_type[0] = bias ? bias_type(*bias) : 0;
+    a.bias_bytes[0] = bias ? bias_bytes(*bias) : 0;
     a.mxtab = mxtab;
     a.codes = codes;
     a.scales = scales;

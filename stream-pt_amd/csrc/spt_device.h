@@ -92,6 +92,35 @@ __device__ inline float bias_at(const void *p, int type, uint64_t i) {
     return reinterpret_cast<const float *>(p)[i];
 }
 
+// The same decode through a buffer descriptor: an absent bias is a zero-length
+// range, so the load is issued unconditionally and reads 0.
+struct BiasView {
+    rsrc_t r;
+    int type;
+};
+
+__device__ inline BiasView make_bias_view(const void *p, uint64_t nbytes, int type) {
+    BiasView v;
+    const uint32_t n = p ? (uint32_t)(nbytes < 0xFFFFFFF0ull ? nbytes : 0xFFFFFFF0ull) : 0u;
+    v.r = __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)n, kRsrcWord3);
+    v.type = p ? type : 0;
+    return v;
+}
+
+// Raw dword holding element i (one load for every type, no branch), then the
+// conversion where the value is used.
+__device__ inline uint32_t bias_raw(const BiasView &v, uint32_t i) {
+    const uint32_t off = v.type == 0 ? i * 4u : (i * 2u) & ~3u;
+    return __builtin_amdgcn_raw_buffer_load_b32(v.r, off, 0, 0);
+}
+
+__device__ inline float bias_value(const BiasView &v, uint32_t raw, uint32_t i) {
+    const uint32_t h = (i & 1u) ? raw >> 16 : raw & 0xFFFFu;
+    if (v.type == 1) return f16_bits_to_f32(h);
+    if (v.type == 30) return __uint_as_float(h << 16);
+    return __uint_as_float(raw);
+}
+
 // ---- MXFP4 block decode ------------------------------------------------------
 // LUT2 = 2*E2M1 = {0,1,2,3,4,6,8,12} and their negatives: exact int8 values,
 // so sdot4 against Q8_0 codes gives the exact block sum; the block scale of

@@ -9,6 +9,8 @@ namespace spt {
 constexpr int kMaxTopK = 16;
 constexpr int kMaxExperts = 256;
 constexpr int kMaxSelections = 4096;
+// Tokens of an expert's list per pass of the grouped GEMV over its weights.
+constexpr int kGemvTokens = 4;
 
 struct SelectOut {
     int32_t *ids;
@@ -18,6 +20,7 @@ struct SelectOut {
     int32_t *list;
     int32_t *active;
     int32_t *n_active;
+    int32_t *pass_off;  // [E+1] prefix over active experts of ceil(count / kGemvTokens)
 };
 
 // Optional Q8_0 outputs of a quantized activation (see write_q8_block).
@@ -43,12 +46,14 @@ struct MxMfmaArgs {
     int rows;                // output rows per expert (= bias dim)
     int nb;                  // input blocks of 32 per row
     const void *bias[2];     // optional [rows][experts] biases
+    uint64_t bias_bytes[2];
     int bias_type[2];
     const uint8_t *mxtab;    // activation E4M3 digit table [*][nb][64]
     const float *scales;     // activation Q8_0 scales [*][nb]
     const int8_t *codes;     // activation Q8_0 codes [*][nb*32]
     const int32_t *active;   // grouped modes: packed expert lists
     const int32_t *n_active;
+    const int32_t *pass_off;
     const int32_t *offsets;
     const int32_t *list;
     int topk;
@@ -83,6 +88,7 @@ hipError_t launch_route(hipStream_t s, const float *router, const void *bias, in
 // Top-k + softmax per token, then the per-expert lists (one workgroup).
 hipError_t launch_select(hipStream_t s, const float *logits, int batch, int experts, int topk,
                          const SelectOut &o);
+// slots: upper bound of the active experts (1 for kRows).
 hipError_t launch_mx_mfma(hipStream_t s, GemvMode mode, const MxMfmaArgs &a, int slots);
 hipError_t launch_q40_gemv(hipStream_t s, const Q40Args &a);
 hipError_t launch_combine(hipStream_t s, const float *results, const float *weights, int batch,

@@ -162,15 +162,21 @@ __device__ void pack_lists(int n, int E, const SelectOut &o, const int32_t *s_id
         if (!(s_w[i] <= 0.0f)) atomicAdd(&s_cnt[s_ids[i]], 1);
     __syncthreads();
     if (tid < 64) {
-        int pos = 0, na = 0;
+        // offsets (scan of counts), the active list and the pass prefix
+        // (scan of ceil(count / kGemvTokens) in active order)
+        int pos = 0, na = 0, npass = 0;
         for (int e0 = 0; e0 < E; e0 += 64) {
             const int e = e0 + tid;
             const int c = e < E ? s_cnt[e] : 0;
-            int incl = c;
+            const int np = (c + kGemvTokens - 1) / kGemvTokens;
+            int incl = c, pincl = np;
 #pragma unroll
             for (int d = 1; d < 64; d <<= 1) {
-                const int up = __shfl_up(incl, d);
-                if (tid >= d) incl += up;
+                const int up = __shfl_up(incl, d), pup = __shfl_up(pincl, d);
+                if (tid >= d) {
+                    incl += up;
+                    pincl += pup;
+                }
             }
             const uint64_t act = __ballot(c > 0);
             const int arank = __builtin_popcountll(act & ((1ull << tid) - 1ull));
@@ -178,15 +184,20 @@ __device__ void pack_lists(int n, int E, const SelectOut &o, const int32_t *s_id
                 s_off[e] = pos + incl - c;
                 o.offsets[e] = pos + incl - c;
                 o.counts[e] = c;
-                if (c > 0) o.active[na + arank] = e;
+                if (c > 0) {
+                    o.active[na + arank] = e;
+                    o.pass_off[na + arank] = npass + pincl - np;
+                }
             }
             pos += __shfl(incl, 63);
+            npass += __shfl(pincl, 63);
             na += __builtin_popcountll(act);
         }
         if (tid == 0) {
             s_off[E] = pos;
             o.offsets[E] = pos;
             *o.n_active = na;
+            o.pass_off[na] = npass;
         }
     }
     for (int p0 = 0; p0 < n; p0 += kSelChunk) {
