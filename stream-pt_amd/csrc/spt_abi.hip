@@ -325,7 +325,7 @@ int run_moe(spt_ctx *ctx, const spt_moe_layer *lw, const float *x, float *out, c
     ga.offsets = so.offsets;
     ga.list = so.list;
     ga.topk = (int)k;
-    ga.out = act;
+    ga.out = taps && taps->act ? act : nullptr;  // fp32 act only for the tap
     ga.tap[0] = taps ? taps->gate : nullptr;
     ga.tap[1] = taps ? taps->up : nullptr;
     ga.act_codes = ac;

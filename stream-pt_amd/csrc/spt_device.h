@@ -101,7 +101,10 @@ struct BiasView {
 
 __device__ inline BiasView make_bias_view(const void *p, uint64_t nbytes, int type) {
     BiasView v;
-    const uint32_t n = p ? (uint32_t)(nbytes < 0xFFFFFFF0ull ? nbytes : 0xFFFFFFF0ull) : 0u;
+    // whole dwords: the last 2-byte element of an odd count sits in a dword
+    // that crosses the end, and a load crossing the range's end reads zero
+    const uint64_t nw = (nbytes + 3u) & ~uint64_t(3);
+    const uint32_t n = p ? (uint32_t)(nw < 0xFFFFFFF0ull ? nw : 0xFFFFFFF0ull) : 0u;
     v.r = __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)n, kRsrcWord3);
     v.type = p ? type : 0;
     return v;

@@ -21,6 +21,8 @@
 // scale 255, or scales whose products could leave the normal fp32 range) are
 // computed with the integer LUT decode instead, so the results keep the
 // reference's special-value semantics.
+#include <type_traits>
+
 #include "spt_device.h"
 #include "spt_kernels.h"
 
@@ -58,36 +60,38 @@ __device__ float lut_row_dot(const ByteView &v, uint32_t row_pos, int nb, const 
 
 }  // namespace
 
-// Weights reach the MFMA through a wave-private LDS tile.  A wave owns 16
-// weight rows and walks K in segments of kKSeg = 16 blocks.  Each load
-// instruction covers four rows x 16 consecutive blocks (four 272-byte
-// runs), lane j taking row 4q + (j >> 4), block j & 15, as 20 aligned bytes;
-// the 16 nibble bytes are realigned in registers and stored with the E8M0
-// byte into the tile, where the MFMA's lane (g, i) reads row i, block 4c + g.
-// Tile slots are XOR-swizzled (slot = block ^ row) so both the stores (16
-// consecutive blocks of one row) and the MFMA reads (16 rows of one block)
-// are free of bank conflicts.  Segments stream through a ring of NBUF
-// register buffers, NBUF - 1 of them in flight while one is stored.
-constexpr int kKSeg = 16;
-constexpr int kRowsPerLoad = 64 / kKSeg;
-constexpr int kSegLoads = 16 / kRowsPerLoad;
-constexpr int kChunks = kKSeg / 4;
-constexpr int kATile = 16 * kKSeg * 16;   // bytes of nibble data per wave
-constexpr int kETile = 16 * kKSeg;        // bytes of E8M0 per wave
-constexpr int kWaveLds = kATile + kETile;
-constexpr uint32_t kOutOfRange = 0x80000000u;  // byte offset past any expert matrix (< 4 GiB)
-constexpr size_t kMaxMxLds = 48 * 1024;        // dynamic LDS of three workgroups per CU within 160 KB
+// Weights reach the MFMA through a wave-private LDS image of the wave's 16
+// rows.  The rows of an expert matrix are contiguous, so a wave's 16 rows are
+// one run of 16 * nb * 17 bytes: the wave streams it with fully coalesced
+// 16-byte loads (64 lanes x 16 B = 1 KB per instruction) starting at the
+// 16-byte boundary at or below the run's first byte, stores the image to LDS
+// unchanged, and the MFMA lanes read their blocks back at any byte alignment
+// (five dwords, realigned by byte permutes).  While a wave multiplies one
+// tile the loads of its next tile are in flight.  The image of one tile (nb
+// up to kMaxNb) plus the token tables must fit the LDS of a CU, which holds
+// one workgroup of four waves.
+constexpr int kMaxNb = 96;
+constexpr int kMaxNbp = (kMaxNb + 7) / 8 * 8;
+// 1 KB loads of a tile image: 16 rows plus up to 15 bytes before them.
+__host__ __device__ constexpr int tile_loads(int nb) { return (16 * nb * kMxBlock + 15 + 1023) / 1024; }
+// LDS bytes of a wave's image: whole groups of four loads, and room for the
+// reads of the blocks past nb in the last chunk pair (up to nb + 6, 20 bytes
+// each from a dword boundary).
+__host__ __device__ constexpr int tile_region(int nb) {
+    return (4 * ((tile_loads(nb) + 3) / 4) > (16 * nb * kMxBlock + 137 + 1023) / 1024
+                ? 4 * ((tile_loads(nb) + 3) / 4)
+                : (16 * nb * kMxBlock + 137 + 1023) / 1024) *
+           1024;
+}
+constexpr int kTileGroups = (tile_loads(kMaxNb) + 3) / 4;  // groups of four 1 KB loads
+constexpr int kTabLoads = (16 * kMaxNbp + kWG - 1) / kWG;  // 16-byte digit-table pieces per thread
+constexpr int kDxLoads = (kTokPerPass * kMaxNbp + kWG - 1) / kWG;  // d_x entries per thread
+constexpr size_t kMaxMxLds = 146 * 1024;  // dynamic LDS; with the static part (< 14 KB) within 160 KB
 
-// Ring depth and occupancy per mode.  Gate/up carries the SwiGLU and the
-// Q8_0 of act in its epilogue and runs two waves per SIMD with four
-// segments in flight per wave; down and single-expert run three waves per
-// SIMD with two in flight.
 template <int MODE> struct MxTraits {
-    static constexpr int kNBuf = MODE == kGateUp ? 5 : 3;
-    static constexpr int kWavesPerEU = MODE == kGateUp ? 2 : 3;
     // Unit outputs staged in LDS before a flush, and the values staged per
     // row and token (gate/up: act, gate, up; down: the result).
-    static constexpr int kStageUnits = MODE == kGateUp ? 8 : 6;
+    static constexpr int kStageUnits = MODE == kGateUp ? 4 : 6;
     static constexpr int kStageVals = MODE == kGateUp ? 3 : 1;
     static constexpr int kUnitRows = MODE == kGateUp ? 32 : 64;
 };
@@ -101,195 +105,248 @@ __device__ inline void wave_lds_fence() {
 
 // Workgroup barrier ordering LDS only.  All communication between the
 // waves of k_mx_mfma goes through LDS, and __syncthreads() would also wait
-// for every outstanding global load, draining the weight segments in flight.
+// for every outstanding global load, draining the next tile in flight.
 __device__ inline void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-// Static lane roles.  Loads: row lr = lane / kKSeg of each row group, block
-// bl = lane % kKSeg of the segment.  MFMA A: row i = lane & 15, block gb =
-// lane >> 4 of each chunk.  MFMA B: column c = 8*slot + 4*part + gc holds
-// digit `part` of token `slot`'s block gc; its non-zero half is lo (A blocks
-// gb>>1) or hi (A blocks (gb>>1)+2) of this lane, or neither.
+typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+
+// A tile image in flight: four loads of 1 KB per group, held in the
+// accumulation registers so the VGPRs serve the multiply.  The loads are
+// issued and waited for with inline assembly (the compiler does not place
+// global loads in accumulation registers): tile_issue writes the registers
+// asynchronously, tile_wait (s_waitcnt vmcnt(0)) names every one of them,
+// and only tile_store reads them, after the wait.  Each issue block opens
+// with five wait states: its descriptor and offset SGPRs may have just been
+// written by a VALU instruction, which a following VMEM read must not see
+// early, and the compiler cannot pad inside inline assembly.  Offsets past
+// the descriptor's range read zeros.
+struct TileRegs {
+    u32x4v q[4 * kTileGroups];
+};
+
+template <int G>
+__device__ inline void tile_issue(TileRegs &t, uint32_t vo, const u32x4v &rs, uint32_t so) {
+    asm volatile(
+        "s_nop 4\n\t"
+        "buffer_load_dwordx4 %0, %4, %5, %6 offen\n\t"
+        "buffer_load_dwordx4 %1, %4, %5, %6 offen offset:1024\n\t"
+        "buffer_load_dwordx4 %2, %4, %5, %6 offen offset:2048\n\t"
+        "buffer_load_dwordx4 %3, %4, %5, %6 offen offset:3072"
+        : "=&a"(t.q[4 * G]), "=&a"(t.q[4 * G + 1]), "=&a"(t.q[4 * G + 2]), "=&a"(t.q[4 * G + 3])
+        : "v"(vo), "s"(rs), "s"(so));
+}
+
+__device__ inline void tile_wait(TileRegs &t) {
+    static_assert(kTileGroups == 7, "operand list below");
+    asm volatile("s_waitcnt vmcnt(0)"
+                 : "+a"(t.q[0]), "+a"(t.q[1]), "+a"(t.q[2]), "+a"(t.q[3]), "+a"(t.q[4]), "+a"(t.q[5]),
+                   "+a"(t.q[6]), "+a"(t.q[7]), "+a"(t.q[8]), "+a"(t.q[9]), "+a"(t.q[10]), "+a"(t.q[11]),
+                   "+a"(t.q[12]), "+a"(t.q[13]), "+a"(t.q[14]), "+a"(t.q[15]), "+a"(t.q[16]), "+a"(t.q[17]),
+                   "+a"(t.q[18]), "+a"(t.q[19]), "+a"(t.q[20]), "+a"(t.q[21]), "+a"(t.q[22]), "+a"(t.q[23]),
+                   "+a"(t.q[24]), "+a"(t.q[25]), "+a"(t.q[26]), "+a"(t.q[27]));
+}
+
+template <int G>
+__device__ inline void tile_store(uint32_t lds, const TileRegs &t) {
+    asm volatile(
+        "ds_write_b128 %0, %1\n\t"
+        "ds_write_b128 %0, %2 offset:1024\n\t"
+        "ds_write_b128 %0, %3 offset:2048\n\t"
+        "ds_write_b128 %0, %4 offset:3072"
+        :
+        : "v"(lds), "a"(t.q[4 * G]), "a"(t.q[4 * G + 1]), "a"(t.q[4 * G + 2]), "a"(t.q[4 * G + 3])
+        : "memory");
+}
+
+// Static lane roles.  MFMA A: row i = lane & 15, block gb = lane >> 4 of each
+// chunk.  MFMA B: column c = 8*slot + 4*part + gc holds digit `part` of token
+// `slot`'s block gc; its non-zero half is lo (A blocks gb>>1) or hi (A
+// blocks (gb>>1)+2) of this lane, or neither.
 struct LaneRole {
-    int lr, bl, i, gb, gc, slot, boff, sb;
+    int i, gb, gc, slot, boff, sb;
     bool lo_on, hi_on;
 };
 
-// Per token pass: LDS byte offsets of this lane's B rows and d_x entries for
-// each token pair, at block 0 (add 64 * block / 4 * block).  A half that is
-// off reads 16 zero bytes instead.
+// Per token pass and token pair: where this lane's B operand halves and d_x
+// are read at chunk 0 (add 256 bytes and 4 floats per chunk).  A half that
+// carries no data reads the zero area, which is as long as the tables.
 struct PassRole {
-    uint32_t tb[2], db[2];
-    bool lo[2], hi[2];
+    const uint8_t *bl[2], *bh[2];
+    const float *dx[2];
 };
 
-// The weight stream is issued with inline assembly, out of sight of the
-// compiler's wait-count analysis, and waited for explicitly (stream_wait):
-// the compiler's analysis turns conservative (a full drain) at control-flow
-// joins around stores and around the loop, which would empty the ring of
-// segments in flight every step.  Loads complete in order, so waiting until
-// at most N loads are outstanding, with N the number of stream loads issued
-// after a segment, is exact whatever else was issued in between.
-typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+// The LDS words of one chunk: the five dwords holding this lane's A block,
+// and per token pair the two halves of the B operand and d_x.
+template <int NP>
+struct ChunkRaw {
+    uint32_t d[5];
+    u32x4v blo[NP], bhi[NP];
+    float x[NP];
+};
 
-// Buffer descriptor words, the layout __builtin_amdgcn_make_buffer_rsrc
-// builds: base, base_hi | stride << 16 (stride 0), num_records, flags.
-__device__ inline u32x4v rsrc_words(const void *base, uint32_t nrec) {
-    const uint64_t a = reinterpret_cast<uint64_t>(base);
-    return u32x4v{(uint32_t)a, (uint32_t)(a >> 32) & 0xFFFFu, nrec, (uint32_t)kRsrcWord3};
+template <int NP>
+__device__ __attribute__((always_inline)) inline void chunk_fetch(ChunkRaw<NP> &r, const uint32_t *pa, const PassRole &P, int c) {
+#pragma unroll
+    for (int i = 0; i < 5; i++) r.d[i] = pa[17 * c + i];
+#pragma unroll
+    for (int tp = 0; tp < NP; tp++) {
+        r.blo[tp] = *reinterpret_cast<const u32x4v *>(P.bl[tp] + 256 * c);
+        r.bhi[tp] = *reinterpret_cast<const u32x4v *>(P.bh[tp] + 256 * c);
+        r.x[tp] = P.dx[tp][4 * c];
+    }
 }
 
-// A segment in registers: per load instruction q, the 16-byte word at the
-// block's aligned start and the next dword; plus the raw bias words of the
-// segment's unit (loaded first).
-struct SegRegs {
-    u32x4v q4[kSegLoads];
-    uint32_t q1[kSegLoads];
-    uint32_t b0, b1;
-};
-
-// One segment's stream loads in one block: the bias word(s), then per load
-// instruction q the 16 bytes at off[q] and the dword after them.  The block
-// opens with five wait states: descriptor SGPRs may have just been written
-// by a VALU instruction (a spill reload), which a following VMEM read must
-// not see early, and the compiler cannot pad inside inline assembly.
-// Offsets past a descriptor's range read as zeros.
-template <bool TWO_BIAS>
-__device__ inline void stream_fetch(SegRegs &d, uint32_t bo0, uint32_t bo1, const u32x4v &brs0,
-                                    const u32x4v &brs1, const uint32_t off[kSegLoads], const u32x4v &rs) {
-    static_assert(kSegLoads == 4, "operand list below");
-    if constexpr (TWO_BIAS) {
-        asm volatile(
-            "s_nop 4\n\t"
-            "buffer_load_dword %0, %10, %12, 0 offen\n\t"
-            "buffer_load_dword %1, %11, %13, 0 offen\n\t"
-            "buffer_load_dwordx4 %2, %14, %18, 0 offen\n\t"
-            "buffer_load_dword %6, %14, %18, 0 offen offset:16\n\t"
-            "buffer_load_dwordx4 %3, %15, %18, 0 offen\n\t"
-            "buffer_load_dword %7, %15, %18, 0 offen offset:16\n\t"
-            "buffer_load_dwordx4 %4, %16, %18, 0 offen\n\t"
-            "buffer_load_dword %8, %16, %18, 0 offen offset:16\n\t"
-            "buffer_load_dwordx4 %5, %17, %18, 0 offen\n\t"
-            "buffer_load_dword %9, %17, %18, 0 offen offset:16"
-            : "=&v"(d.b0), "=&v"(d.b1), "=&v"(d.q4[0]), "=&v"(d.q4[1]), "=&v"(d.q4[2]), "=&v"(d.q4[3]),
-              "=&v"(d.q1[0]), "=&v"(d.q1[1]), "=&v"(d.q1[2]), "=&v"(d.q1[3])
-            : "v"(bo0), "v"(bo1), "s"(brs0), "s"(brs1), "v"(off[0]), "v"(off[1]), "v"(off[2]), "v"(off[3]),
-              "s"(rs));
+// MFMAs of a fetched chunk.  MASK: the chunk may hold blocks past nb, which
+// get scale 2^0 (their tables and d_x are zero, so they add 0) and stay out
+// of the special-scale check.
+template <int NP, bool MASK>
+__device__ __attribute__((always_inline)) inline void chunk_mfma(const ChunkRaw<NP> &r, int c, int nb, uint32_t sel, uint32_t esh, const LaneRole &L,
+                                  float acc[2][4], uint32_t &emin, uint32_t &emax) {
+    const uint32_t ev = __builtin_amdgcn_ubfe(r.d[0], esh, 8u);
+    int sa = (int)ev;
+    if (MASK) {
+        const bool in = 4 * c + L.gb < nb;
+        sa = in ? sa : 127;
+        emin = in ? min(emin, ev) : emin;
+        emax = in ? max(emax, ev) : emax;
     } else {
-        asm volatile(
-            "s_nop 4\n\t"
-            "buffer_load_dword %0, %9, %10, 0 offen\n\t"
-            "buffer_load_dwordx4 %1, %11, %15, 0 offen\n\t"
-            "buffer_load_dword %5, %11, %15, 0 offen offset:16\n\t"
-            "buffer_load_dwordx4 %2, %12, %15, 0 offen\n\t"
-            "buffer_load_dword %6, %12, %15, 0 offen offset:16\n\t"
-            "buffer_load_dwordx4 %3, %13, %15, 0 offen\n\t"
-            "buffer_load_dword %7, %13, %15, 0 offen offset:16\n\t"
-            "buffer_load_dwordx4 %4, %14, %15, 0 offen\n\t"
-            "buffer_load_dword %8, %14, %15, 0 offen offset:16"
-            : "=&v"(d.b0), "=&v"(d.q4[0]), "=&v"(d.q4[1]), "=&v"(d.q4[2]), "=&v"(d.q4[3]), "=&v"(d.q1[0]),
-              "=&v"(d.q1[1]), "=&v"(d.q1[2]), "=&v"(d.q1[3])
-            : "v"(bo0), "s"(brs0), "v"(off[0]), "v"(off[1]), "v"(off[2]), "v"(off[3]), "s"(rs));
-        d.b1 = 0u;
+        emin = min(emin, ev);
+        emax = max(emax, ev);
+    }
+    const v8i A = {(int)__builtin_amdgcn_perm(r.d[1], r.d[0], sel), (int)__builtin_amdgcn_perm(r.d[2], r.d[1], sel),
+                   (int)__builtin_amdgcn_perm(r.d[3], r.d[2], sel), (int)__builtin_amdgcn_perm(r.d[4], r.d[3], sel),
+                   0, 0, 0, 0};
+#pragma unroll
+    for (int tp = 0; tp < NP; tp++) {
+        const v8i B = __builtin_bit_cast(v8i, __builtin_shufflevector(r.blo[tp], r.bhi[tp], 0, 1, 2, 3, 4, 5, 6, 7));
+        v4f dd = {0.0f, 0.0f, 0.0f, 0.0f};
+        dd = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A, B, dd, 4, 0, 0, sa, 0, L.sb);
+#pragma unroll
+        for (int k = 0; k < 4; k++) acc[tp][k] = __builtin_fmaf(dd[k], r.x[tp], acc[tp][k]);
     }
 }
 
-// Per-lane offsets of a segment's load instructions; a slot outside the
-// matrix reads past the buffer's range, which returns zeros, so the number
-// of stream loads per segment is fixed.
-__device__ inline void seg_offsets(uint32_t p0, bool bin, uint32_t grp_step, uint32_t off[kSegLoads]) {
-#pragma unroll
-    for (int q = 0; q < kSegLoads; q++) off[q] = bin ? ((p0 + (uint32_t)q * grp_step) & ~3u) : kOutOfRange;
-}
-
-// Wait until at most N stream loads are outstanding; the segment's registers
-// are operands, so nothing reads them before the wait.
-template <int N>
-__device__ inline void stream_wait(SegRegs &d) {
-    static_assert(kSegLoads == 4, "operand list below");
-    asm volatile("s_waitcnt vmcnt(%10)"
-                 : "+v"(d.q4[0]), "+v"(d.q4[1]), "+v"(d.q4[2]), "+v"(d.q4[3]), "+v"(d.q1[0]), "+v"(d.q1[1]),
-                   "+v"(d.q1[2]), "+v"(d.q1[3]), "+v"(d.b0), "+v"(d.b1)
-                 : "n"(N));
-}
-
-// Realign the loaded blocks and store them into the wave's tile.  Blocks
-// outside the matrix load as zeros and get scale 2^0, contributing 0; a
-// block with a special E8M0 gets scale 2^0 and flags its rows, which are
-// then recomputed with the integer decode.
-__device__ inline void seg_store(const SegRegs &sr, uint32_t p0, bool bin, uint32_t grp_step,
-                                 int row0, int rows, const LaneRole &L, uint4 *sA, uint8_t *sE, bool &special) {
-#pragma unroll
-    for (int q = 0; q < kSegLoads; q++) {
-        const uint32_t d[5] = {sr.q4[q].x, sr.q4[q].y, sr.q4[q].z, sr.q4[q].w, sr.q1[q]};
-        const int rl = kRowsPerLoad * q + L.lr;
-        const bool in = bin && row0 + rl < rows;
-        const uint32_t o = (p0 + (uint32_t)q * grp_step) & 3u;
-        const uint32_t sel = 0x04030201u + o * 0x01010101u;
-        const uint32_t ev = __builtin_amdgcn_ubfe(d[0], o * 8u, 8u);
-        const bool normal = ev - (uint32_t)kEMin <= (uint32_t)(kEMax - kEMin);
-        special |= in && !normal;
-        uint4 nib;
-        nib.x = __builtin_amdgcn_perm(d[1], d[0], sel);
-        nib.y = __builtin_amdgcn_perm(d[2], d[1], sel);
-        nib.z = __builtin_amdgcn_perm(d[3], d[2], sel);
-        nib.w = __builtin_amdgcn_perm(d[4], d[3], sel);
-        sA[rl * kKSeg + (L.bl ^ rl)] = nib;
-        sE[rl * kKSeg + L.bl] = (uint8_t)(in && normal ? ev : 127u);
-    }
-}
-
-// MFMAs of one segment: for each chunk c of 4 blocks, A from the tile and
-// up to two token pairs of B from the staged digit tables (padded to whole
-// segments with zeros); each lane accumulates its own column,
-// acc[tp][k] += D[k] * d_x (the h and l columns are summed per unit).
-__device__ inline void seg_mfma(int ks, int npair, const LaneRole &L, const PassRole &P, const uint8_t *s_zero,
-                                const uint4 *sA, const uint8_t *sE, const uint8_t *s_mx, const uint8_t *s_dxb,
-                                float acc[2][4]) {
-#pragma unroll 1
-    for (int c = 0; c < kChunks; c++) {
-        const uint4 a4 = sA[L.i * kKSeg + ((4 * c + L.gb) ^ L.i)];
-        const int sa = sE[L.i * kKSeg + 4 * c + L.gb];
-        const v8i A = {(int)a4.x, (int)a4.y, (int)a4.z, (int)a4.w, 0, 0, 0, 0};
-        const uint32_t blk0 = (uint32_t)(ks * kKSeg + 4 * c);  // uniform
-#pragma unroll
-        for (int tp = 0; tp < 2; tp++) {
-            if (tp >= npair) break;
-            const uint32_t at = P.tb[tp] + blk0 * 64u;
-            const uint4 lo = *reinterpret_cast<const uint4 *>(P.lo[tp] ? s_mx + at : s_zero);
-            const uint4 hi = *reinterpret_cast<const uint4 *>(P.hi[tp] ? s_mx + at : s_zero);
-            const v8i B = {(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
-            const float dx = *reinterpret_cast<const float *>(s_dxb + P.db[tp] + blk0 * 4u);
-            v4f dd = {0.0f, 0.0f, 0.0f, 0.0f};
-            dd = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A, B, dd, 4, 0, 0, sa, 0, L.sb);
-#pragma unroll
-            for (int k = 0; k < 4; k++) acc[tp][k] = __builtin_fmaf(dd[k], dx, acc[tp][k]);
-        }
-    }
-}
-
-// Position of the lead cursor in a workgroup's stream of weight segments.
-// Work items are (slot, pass, tile) in that order, w = (pass_off[slot] +
-// pass) * tiles + tile: slot = an active expert, pass = kTokPerPass tokens
-// of its list, tile = a row tile; each item is nseg K segments.
-struct Cursor {
-    int w, slot, p, tile, ks, e, begin, count, npass;
-    bool done;
+// Per-lane view of a tile image.  Chunk c covers blocks 4c..4c+3 of the 16
+// rows: A lane (gb, i) takes row i, block 4c + gb, at byte rpos + 17 *
+// (4c + gb) of the image; a chunk advances 68 bytes (17 dwords), so the
+// lane's byte offset within a dword, and with it the realigning permute, is
+// fixed for the tile.
+struct TileView {
+    const uint32_t *pa;
+    uint32_t sel, esh;
+    uint32_t emin, emax;
 };
 
-// What a buffer holds, packed into three scalars: m0 = expert | ks << 16,
-// m1 = tile | pass << 16, m2 = slot | done << 31.
-struct Meta {
-    uint32_t m0, m1, m2;
-    __device__ int e() const { return (int)(m0 & 0xFFFFu); }
-    __device__ int ks() const { return (int)(m0 >> 16); }
-    __device__ int tile() const { return (int)(m1 & 0xFFFFu); }
-    __device__ int p() const { return (int)(m1 >> 16); }
-    __device__ int slot() const { return (int)(m2 & 0x7FFFFFFFu); }
-    __device__ bool done() const { return (m2 >> 31) != 0; }
+__device__ __attribute__((always_inline)) inline TileView tile_view(const uint8_t *img, uint32_t rpos, const LaneRole &L) {
+    const uint32_t pos0 = rpos + (uint32_t)L.gb * kMxBlock;
+    const uint32_t o = pos0 & 3u;
+    TileView v;
+    v.pa = reinterpret_cast<const uint32_t *>(img + (pos0 & ~3u));
+    v.sel = 0x04030201u + o * 0x01010101u;  // bytes o+1 .. o+4
+    v.esh = o * 8u;
+    v.emin = 255u;
+    v.emax = 0u;
+    return v;
+}
+
+// A special E8M0 (outside [4, 254]) in the tile's valid blocks: the tile's
+// rows are then recomputed with the integer decode, so the MFMA results of
+// such a tile are unused.
+__device__ inline bool tile_special(const TileView &v, bool row_ok) {
+    return row_ok && (v.emin < (uint32_t)kEMin || v.emax > (uint32_t)kEMax);
+}
+
+// Four chunks: their LDS reads, then their MFMAs.
+template <int NP, bool MASK>
+__device__ __attribute__((always_inline)) inline void chunk_quad(TileView &v, int c0, int nb, const LaneRole &L, const PassRole &P, float acc[2][4]) {
+    ChunkRaw<NP> r[4];
+#pragma unroll
+    for (int h = 0; h < 4; h++) chunk_fetch<NP>(r[h], v.pa, P, c0 + h);
+#pragma unroll
+    for (int h = 0; h < 4; h++) chunk_mfma<NP, MASK>(r[h], c0 + h, nb, v.sel, v.esh, L, acc, v.emin, v.emax);
+}
+
+template <int NP, bool MASK>
+__device__ __attribute__((always_inline)) inline void chunk_pair(TileView &v, int c0, int nb, const LaneRole &L, const PassRole &P, float acc[2][4]) {
+    ChunkRaw<NP> r[2];
+#pragma unroll
+    for (int h = 0; h < 2; h++) chunk_fetch<NP>(r[h], v.pa, P, c0 + h);
+#pragma unroll
+    for (int h = 0; h < 2; h++) chunk_mfma<NP, MASK>(r[h], c0 + h, nb, v.sel, v.esh, L, acc, v.emin, v.emax);
+}
+
+// Segment g (0..5) of a tile's chunks.  Before segment g the caller issues
+// group g of the next tile's loads, so the next tile's requests spread over
+// the multiply.  24 chunks (nb in [89, 96]: the GPT-OSS dimension 2880 has
+// nb = 90) are straight-line quads, chunks 22 and 23 masked; any other
+// (even) chunk count splits its chunk pairs evenly over the segments, the
+// pairs holding blocks past nb masked.
+template <int NP>
+__device__ __attribute__((always_inline)) inline void tile_segment(int g, TileView &v, int nb, int nch, const LaneRole &L, const PassRole &P,
+                                    float acc[2][4]) {
+    if (nch == 24) {
+        if (g < 5) {
+            chunk_quad<NP, false>(v, 4 * g, nb, L, P, acc);
+        } else {
+            chunk_pair<NP, false>(v, 20, nb, L, P, acc);
+            chunk_pair<NP, true>(v, 22, nb, L, P, acc);
+        }
+        return;
+    }
+    const int npairs = nch / 2, nfull = nb / 8;  // pairs, and pairs whose 8 blocks are all < nb
+    for (int p = g * npairs / 6; p < (g + 1) * npairs / 6; p++) {
+        if (p < nfull)
+            chunk_pair<NP, false>(v, 2 * p, nb, L, P, acc);
+        else
+            chunk_pair<NP, true>(v, 2 * p, nb, L, P, acc);
+    }
+}
+
+// Sum over each group of eight lanes (every lane of the group gets it),
+// pairing lanes by DPP: lane ^ 7, then ^ 1, then ^ 2.
+__device__ __attribute__((always_inline)) inline float sum8(float v) {
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+    return v;
+}
+
+// Largest value over each half-wave (32 lanes) of non-negative non-NaN
+// floats given as bit patterns (which order like the values): DPP lane ^ 15,
+// ^ 7, ^ 1, ^ 2 within rows of 16, then a swizzle for lane ^ 16.
+__device__ __attribute__((always_inline)) inline uint32_t max32_bits(uint32_t m) {
+    m = max(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x140, 0xF, 0xF, false));
+    m = max(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x141, 0xF, 0xF, false));
+    m = max(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0xB1, 0xF, 0xF, false));
+    m = max(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x4E, 0xF, 0xF, false));
+    m = max(m, (uint32_t)__builtin_amdgcn_ds_swizzle((int)m, 0x401F));
+    return m;
+}
+
+// Q8_0 of a 32-element block held one element per lane by each half-wave:
+// the arithmetic of q8_quantize_lane (scale amax / 127, a NaN anywhere in
+// the block makes the scale NaN), with the reductions done per half-wave.
+__device__ __attribute__((always_inline)) inline int q8_quantize_half(float v, int lane, uint16_t *dbits) {
+    const float a = __builtin_fabsf(v);
+    const uint64_t nanm = __ballot(a != a);
+    const bool nan_any = ((lane < 32 ? nanm : nanm >> 32) & 0xFFFFFFFFull) != 0;
+    const float m = __uint_as_float(max32_bits(a == a ? __float_as_uint(a) : 0u));
+    const float d = nan_any ? __builtin_nanf("") : m / 127.0f;
+    const float id = (d != 0.0f) ? 1.0f / d : 0.0f;
+    *dbits = f32_to_f16_bits(d);
+    const float r = __builtin_roundf(v * id);
+    return (r != r) ? 0 : (r > 127.0f ? 127 : (r < -127.0f ? -127 : (int)r));
+}
+
+// Position in a workgroup's range of work items (slot, pass, tile), in that
+// order: w = (pass_off[slot] + pass) * tiles + tile.  slot = an active
+// expert, pass = kTokPerPass tokens of its list, tile = a row tile.
+struct Cursor {
+    int w, slot, p, tile, e, begin, count, npass;
 };
 
 // Routing arrays of the select kernel, read-only here.
@@ -315,14 +372,8 @@ __device__ inline void slot_info(const MxMfmaArgs &a, const Route &rt, Cursor &c
 }
 
 template <int MODE>
-__device__ inline void cursor_advance(const MxMfmaArgs &a, const Route &rt, Cursor &c, int nseg, int tiles, int w1) {
-    if (c.done) return;
-    if (++c.ks < nseg) return;
-    c.ks = 0;
-    if (++c.w >= w1) {
-        c.done = true;
-        return;
-    }
+__device__ inline void cursor_advance(const MxMfmaArgs &a, const Route &rt, Cursor &c, int tiles) {
+    ++c.w;
     if (++c.tile < tiles) return;
     c.tile = 0;
     if (++c.p < c.npass) return;
@@ -331,55 +382,93 @@ __device__ inline void cursor_advance(const MxMfmaArgs &a, const Route &rt, Curs
     slot_info<MODE>(a, rt, c);
 }
 
-// Persistent workgroups: workgroup b takes work items [b*W/G, (b+1)*W/G)
-// of the W = total passes x row tiles, in order, so consecutive items share
-// an expert's token pass and its staged token tables, and every workgroup
-// streams the same number of weight bytes.  Each wave streams its 16 rows
-// segment after segment with the next NBUF - 1 segments in flight, across
-// tile, pass and expert boundaries.  Gate/up units are 32 output rows
-// (waves 0-1 gate, 2-3 up, so SwiGLU and the Q8_0 of the 32-element act
-// block stay in the workgroup); down and single-expert units are 64 rows.
+// The tokens of a cursor's pass: list entries (idx = token * topk + rank for
+// the grouped modes, the token for kRows) and the rows of the activation
+// tables they read (gate/up: the token; down: the entry).
+struct PassTokens {
+    int nt;
+    int ent[kTokPerPass], arow[kTokPerPass];
+};
+
 template <int MODE>
-__global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(MxTraits<MODE>::kWavesPerEU))) void k_mx_mfma(MxMfmaArgs a, const int32_t *__restrict__ r_active,
-                                                                                  const int32_t *__restrict__ r_offsets,
-                                                                                  const int32_t *__restrict__ r_pass_off,
-                                                                                  const int32_t *__restrict__ r_list,
-                                                                                  const int32_t *__restrict__ r_n_active) {
+__device__ inline PassTokens pass_tokens(const MxMfmaArgs &a, const Route &rt, const Cursor &c) {
+    PassTokens pt;
+    pt.nt = min(kTokPerPass, c.count - c.p * kTokPerPass);
+#pragma unroll
+    for (int t = 0; t < kTokPerPass; t++) {
+        int ent = 0;
+        if (t < pt.nt) ent = MODE == kRows ? c.p * kTokPerPass + t : rt.list[c.begin + c.p * kTokPerPass + t];
+        pt.ent[t] = ent;
+        pt.arow[t] = MODE == kGateUp ? ent / a.topk : ent;
+    }
+    return pt;
+}
+
+__device__ inline int pick4(const int (&v)[kTokPerPass], int t) {
+    return t == 0 ? v[0] : t == 1 ? v[1] : t == 2 ? v[2] : v[3];
+}
+
+// Persistent workgroups, one per CU: workgroup b takes work items
+// [b*W/G, (b+1)*W/G) of the W = total passes x row tiles, in order, so
+// consecutive items share an expert's token pass and its staged token
+// tables, and every workgroup streams the same number of weight bytes.
+// Gate/up units are 32 output rows (waves 0-1 gate, 2-3 up, so SwiGLU and
+// the Q8_0 of the 32-element act block stay in the workgroup); down and
+// single-expert units are 64 rows, 16 per wave.
+//
+// Each step: wait for the prefetched tile and write it (and, at a new pass,
+// the token tables) to LDS; issue the next unit's loads; flush staged
+// outputs if the stage is full; multiply; reduce and stage the unit's
+// outputs.  The only wait for global loads is at the top of a step, for
+// loads issued a whole step earlier.
+template <int MODE>
+__global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(1))) void k_mx_mfma(MxMfmaArgs a, const int32_t *__restrict__ r_active,
+                                                                      const int32_t *__restrict__ r_offsets,
+                                                                      const int32_t *__restrict__ r_pass_off,
+                                                                      const int32_t *__restrict__ r_list,
+                                                                      const int32_t *__restrict__ r_n_active) {
     extern __shared__ __align__(16) uint8_t smem_b[];
     // Output pointers of the epilogue, kept in LDS rather than in scalar
-    // registers across the stream.
+    // registers across the loop.
     struct EpiPtrs {
         float *out, *tap0, *tap1, *act_scales;
         int8_t *act_codes;
         uint8_t *act_mxtab, *act_blocks34;
     };
     __shared__ EpiPtrs s_epi;
-    __shared__ int s_entry[kTokPerPass];
-    __shared__ int s_arow[kTokPerPass];
-    __shared__ float s_res[4][16][kTokPerPass];
-    __shared__ __align__(16) uint8_t s_zero[16];
+    // Row sums of a unit per wave (double-buffered by step parity, so a
+    // step's staging and the next step's sums do not need a barrier apart).
+    __shared__ float s_res[2][4][16][kTokPerPass];
     // Outputs of finished units, written to global memory kStageUnits units
-    // at a time.  Vector-memory stores and loads share one counter and may
-    // complete out of order, so while a store is outstanding a wave can only
-    // wait for all of its loads; flushing in batches keeps the weight
-    // segments in flight across most unit boundaries.
+    // at a time, at the top of a step.  Gate/up also stages each act block's
+    // Q8_0 codes, digit-table bytes and fp16 scale bits.
     constexpr int kStage = MxTraits<MODE>::kStageUnits;
     constexpr int kUnitRows = MxTraits<MODE>::kUnitRows;
+    constexpr int kQStage = MODE == kGateUp ? kStage : 1;
     __shared__ float s_stage[kStage][MxTraits<MODE>::kStageVals][kTokPerPass][kUnitRows];
+    __shared__ int8_t s_sq[kQStage][kTokPerPass][32];
+    __shared__ uint8_t s_smx[kQStage][kTokPerPass][64];
+    __shared__ uint16_t s_sdh[kQStage][kTokPerPass];
     __shared__ int s_stage_ent[kStage][kTokPerPass];
     __shared__ int s_stage_tile[kStage];
     __shared__ int s_stage_nt[kStage];
 
     const int nb = a.nb;
-    const int nseg = (nb + kKSeg - 1) / kKSeg;
-    const int nbp = nseg * kKSeg;  // token tables padded with zero blocks
-    // wave-uniform: keeps the per-wave buffer descriptors in scalar registers
+    const int nbp = (nb + 7) & ~7;  // token tables padded with zero blocks to whole chunk pairs
+    const int nch = nbp / 4;
+    const uint32_t row_bytes = (uint32_t)nb * kMxBlock;
+    const int ngroups = (tile_loads(nb) + 3) / 4;
+    const int region = tile_region(nb);
+    // wave-uniform: keeps per-wave descriptors and offsets in scalar registers
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    // LDS: per-wave weight tiles, then [tok][nbp][64] digit tables, [tok][nbp] d_x
-    uint4 *sA = reinterpret_cast<uint4 *>(smem_b + (size_t)wave * kATile);
-    uint8_t *sE = smem_b + 4 * kATile + wave * kETile;
-    uint8_t *s_mx = smem_b + 4 * kWaveLds;
+    // LDS: per-wave tile images, then [tok][nbp][64] digit tables, [tok][nbp] d_x
+    uint8_t *img = smem_b + (size_t)wave * region;
+    uint8_t *s_mx = smem_b + (size_t)4 * region;
+    // LDS address of this lane's 16 bytes of the image
+    typedef __attribute__((address_space(3))) uint8_t lds_u8;
+    const uint32_t img_lds = (uint32_t)reinterpret_cast<uintptr_t>((lds_u8 *)img) + 16u * (uint32_t)lane;
     float *s_dx = reinterpret_cast<float *>(s_mx + (size_t)kTokPerPass * nbp * 64);
+    uint8_t *s_zero = reinterpret_cast<uint8_t *>(s_dx + kTokPerPass * nbp);  // nbp * 64 bytes of zeros
 
     const int tile_rows = MODE == kGateUp ? 32 : 64;
     const int tiles = (a.rows + tile_rows - 1) / tile_rows;
@@ -404,11 +493,7 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(MxTraits<MO
 
     const int m = MODE == kGateUp ? (wave >> 1) : 0;
     const int roff = MODE == kGateUp ? (wave & 1) * 16 : wave * 16;
-    const uint32_t row_bytes = (uint32_t)nb * kMxBlock;
-    const uint32_t grp_step = (uint32_t)kRowsPerLoad * row_bytes;
     LaneRole L;
-    L.lr = lane / kKSeg;
-    L.bl = lane % kKSeg;
     L.i = lane & 15;
     L.gb = lane >> 4;
     const int c16 = lane & 15;
@@ -419,78 +504,75 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(MxTraits<MO
     L.hi_on = L.gc == (L.gb >> 1) + 2;
     L.boff = part * 32 + 16 * (L.gb & 1);
     L.sb = (L.gb == L.gc) ? (part == 0 ? 131 : 127) : 127;
-    if (tid < 4) reinterpret_cast<uint32_t *>(s_zero)[tid] = 0u;
     if (tid == 0) s_epi = EpiPtrs{a.out, a.tap[0], a.tap[1], a.act_scales, a.act_codes, a.act_mxtab, a.act_blocks34};
+    for (int i = tid; i < nbp * 4; i += kWG) reinterpret_cast<u32x4v *>(s_zero)[i] = u32x4v{0u, 0u, 0u, 0u};
 
     // Epilogue element of this thread: gate/up: row tid&31 of the unit,
     // token tid>>5; down/rows: row tid&63, token tid>>6.
     const int erow = MODE == kGateUp ? (tid & 31) : (tid & 63);
     const BiasView bv0 = make_bias_view(a.bias[0], a.bias_bytes[0], a.bias_type[0]);
     const BiasView bv1 = make_bias_view(a.bias[1], a.bias_bytes[1], a.bias_type[1]);
-    auto bias_words = [](const void *p, uint64_t nbytes) {
-        return rsrc_words(p, p ? (uint32_t)(nbytes < 0xFFFFFFF0ull ? nbytes : 0xFFFFFFF0ull) : 0u);
-    };
-    const u32x4v brs0 = bias_words(a.bias[0], a.bias_bytes[0]);
-    const u32x4v brs1 = bias_words(a.bias[1], a.bias_bytes[1]);
-    // expert matrices: 4-byte aligned base below the expert's first byte,
-    // `lead` bytes before it (the same for every expert when expert_bytes is
-    // a multiple of 4, else recomputed per expert)
     const uint8_t *wbase = a.w[m];
 
-    Cursor lead;
-    lead.w = w0;
-    lead.slot = slot0;
-    lead.p = MODE == kRows ? q0 : q0 - rt.pass_off[slot0];
-    lead.tile = w0 - q0 * tiles;
-    lead.ks = 0;
-    lead.done = false;
-    slot_info<MODE>(a, rt, lead);
+    Cursor cur;
+    cur.w = w0;
+    cur.slot = slot0;
+    cur.p = MODE == kRows ? q0 : q0 - rt.pass_off[slot0];
+    cur.tile = w0 - q0 * tiles;
+    slot_info<MODE>(a, rt, cur);
 
-    // Per-lane byte position (relative to the view's aligned base) of this
-    // lane's first block of a segment, and whether that block exists.
-    auto seg_pos = [&](int tile, int ks, bool done, uint32_t lead, uint32_t &p0, bool &bin) {
-        const int blk = (done ? nseg : ks) * kKSeg + L.bl;
-        bin = blk < nb;
-        p0 = (uint32_t)(tile * tile_rows + roff + L.lr) * row_bytes + (uint32_t)blk * kMxBlock + lead;
+    // Registers of the next unit: its tile image, its pass's token tables
+    // (only loaded when the pass changes) and the epilogue element's raw
+    // bias words.
+    TileRegs tr;
+    // the next unit's tile: descriptor, aligned start, and whether this wave loads it
+    u32x4v nrs = {0u, 0u, 0u, 0u};
+    uint32_t na0 = 0u;
+    bool nxt_ok = false;
+    const uint32_t vo = 16u * (uint32_t)lane;
+    // group G of the next tile's loads (G a compile-time constant, so every
+    // issue block writes fixed registers)
+    auto issue = [&](auto gc) {
+        constexpr int G = decltype(gc)::value;
+        static_assert(G < kTileGroups, "group");
+        if (nxt_ok && G < ngroups) tile_issue<G>(tr, vo, nrs, na0 + 4096u * G);
     };
-    // Stream descriptor of expert e's matrix and its lead.
-    auto expert_words = [&](int e, uint32_t &lead) {
-        const uintptr_t p = reinterpret_cast<uintptr_t>(wbase + (uint64_t)e * a.expert_bytes);
-        lead = (uint32_t)(p & 3u);
-        return rsrc_words(reinterpret_cast<const void *>(p - lead),
-                          (uint32_t)((a.expert_bytes + lead + 3u) & ~uint64_t(3)));
+    auto issue_all = [&]() {
+        static_assert(kTileGroups == 7, "list below");
+        issue(std::integral_constant<int, 0>{});
+        issue(std::integral_constant<int, 1>{});
+        issue(std::integral_constant<int, 2>{});
+        issue(std::integral_constant<int, 3>{});
+        issue(std::integral_constant<int, 4>{});
+        issue(std::integral_constant<int, 5>{});
+        issue(std::integral_constant<int, 6>{});
     };
-    // A buffer holds a segment's weights, its place, and the raw bias words
-    // of its unit's epilogue element, loaded before the segment so that the
-    // epilogue's wait for them never drains the segments in flight.
-    struct SegBuf {
-        SegRegs r;
-        Meta m;
-    };
-    constexpr int kStreamPerSeg = 2 * kSegLoads + (MODE == kGateUp ? 2 : 1);
-    auto fetch = [&](SegBuf &buf) {
-        buf.m = Meta{(uint32_t)lead.e | ((uint32_t)lead.ks << 16), (uint32_t)lead.tile | ((uint32_t)lead.p << 16),
-                     (uint32_t)lead.slot | (lead.done ? 0x80000000u : 0u)};
-        const uint32_t brow = (uint32_t)lead.e * (uint32_t)a.rows + (uint32_t)(lead.tile * tile_rows + erow);
-        // bias dword offsets as bias_raw computes them
-        const uint32_t bo0 = bv0.type == 0 ? brow * 4u : (brow * 2u) & ~3u;
-        const uint32_t bo1 = bv1.type == 0 ? brow * 4u : (brow * 2u) & ~3u;
-        uint32_t ld;
-        const u32x4v rs = expert_words(lead.e, ld);
-        uint32_t p0, off[kSegLoads];
-        bool bin;
-        seg_pos(lead.tile, lead.ks, lead.done, ld, p0, bin);
-        seg_offsets(p0, bin, grp_step, off);
-        stream_fetch<MODE == kGateUp>(buf.r, bo0, bo1, brs0, brs1, off, rs);
-        cursor_advance<MODE>(a, rt, lead, nseg, tiles, w1);
+    uint32_t b0r = 0u, b1r = 0u;
+    auto prefetch = [&](const Cursor &c) {
+        const uint32_t brow = (uint32_t)c.e * (uint32_t)a.rows + (uint32_t)(c.tile * tile_rows + erow);
+        b0r = bias_raw(bv0, brow);
+        if (MODE == kGateUp) b1r = bias_raw(bv1, brow);
+        const int row0 = c.tile * tile_rows + roff;
+        nxt_ok = false;
+        if (row0 < a.rows) {
+            // The expert matrix from the 16-byte boundary at or below its
+            // first byte to the one at or above its end (a 16-byte load
+            // that crosses the range's end reads zeros, and the bytes up to
+            // that boundary share the last byte's page); loads past it read
+            // zeros.  Bytes past the matrix only reach rows past a.rows.
+            const uintptr_t mb = reinterpret_cast<uintptr_t>(wbase + (uint64_t)c.e * a.expert_bytes);
+            const uint32_t le = (uint32_t)(mb & 15u);
+            const uint64_t base = mb - le;
+            // descriptor words: base, base_hi (stride 0), num_records, format
+            const u32x4v rs = {(uint32_t)base, (uint32_t)(base >> 32) & 0xFFFFu,
+                               (uint32_t)((a.expert_bytes + le + 15u) & ~15ull), (uint32_t)kRsrcWord3};
+            nrs = rs;
+            na0 = (le + (uint32_t)row0 * row_bytes) & ~15u;
+            nxt_ok = true;
+        }
     };
 
-    constexpr int NBUF = MxTraits<MODE>::kNBuf;
-    SegBuf bufs[NBUF];
-#pragma unroll
-    for (int k = 0; k < NBUF - 1; k++) fetch(bufs[k]);
-
-    int staged_slot = -1, staged_p = -1, nt = 0, npair = 0;
+    int staged_slot = -1, staged_p = -1, npair = 0;
     PassRole PR;
     float acc[2][4];
 #pragma unroll
@@ -499,31 +581,42 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(MxTraits<MO
         for (int i = 0; i < 4; i++) acc[p][i] = 0.0f;
     bool special = false;
 
-    // Write out the staged units (all waves).  Gate/up: wave-per-token act
-    // rows, their Q8_0 block in every layout, and the gate/up taps; down:
-    // thread-per-element results.
+    // Write out the staged units (all waves, after a barrier).  Gate/up:
+    // thread-per-element act (for the tap), the gate/up taps and the act
+    // blocks' Q8_0 in every layout (the unit is one Q8_0 block of each
+    // token's act row); down: thread-per-element results.
     int n_staged = 0;
     auto flush = [&](int count) {
         const EpiPtrs ep = s_epi;
         if constexpr (MODE == kGateUp) {
-            for (int pi = wave; pi < count * kTokPerPass; pi += 4) {
-                const int k = pi / kTokPerPass, t = pi % kTokPerPass;
+            for (int i = tid; i < count * kTokPerPass * 32; i += kWG) {
+                const int k = i >> 7, t = (i >> 5) & 3, e = i & 31;
                 if (t >= s_stage_nt[k]) continue;
                 const int tile = s_stage_tile[k], ent = s_stage_ent[k][t];
-                const int r = tile * 32 + (lane & 31);
-                const float v = lane < 32 ? s_stage[k][0][t][lane] : 0.0f;
-                if (lane < 32 && r < a.rows) {
+                const int r = tile * 32 + e;
+                if (r < a.rows) {
                     const size_t o = (size_t)ent * a.rows + r;
-                    ep.out[o] = v;
-                    if (ep.tap0) ep.tap0[o] = s_stage[k][1][t][lane];
-                    if (ep.tap1) ep.tap1[o] = s_stage[k][2][t][lane];
+                    if (ep.out) ep.out[o] = s_stage[k][0][t][e];
+                    if (ep.tap0) ep.tap0[o] = s_stage[k][1][t][e];
+                    if (ep.tap1) ep.tap1[o] = s_stage[k][2][t][e];
                 }
-                // the unit is one Q8_0 block of the token's act row
                 if (ep.act_codes && tile * 32 + 32 <= a.rows) {
-                    uint16_t dh;
-                    const int q = q8_quantize_lane(v, lane, &dh);
                     const size_t blk = (size_t)ent * (a.rows / 32) + tile;
-                    write_q8_lane(q, dh, lane, blk, ep.act_codes, ep.act_scales, ep.act_mxtab, ep.act_blocks34);
+                    const int8_t qv = s_sq[k][t][e];
+                    const uint16_t dh = s_sdh[k][t];
+                    ep.act_codes[blk * 32 + e] = qv;
+                    if (ep.act_mxtab) {
+                        ep.act_mxtab[blk * 64 + e] = s_smx[k][t][e];
+                        ep.act_mxtab[blk * 64 + 32 + e] = s_smx[k][t][32 + e];
+                    }
+                    if (ep.act_scales && e == 0) ep.act_scales[blk] = f16_bits_to_f32(dh);
+                    if (ep.act_blocks34) {
+                        if (e == 0) {
+                            ep.act_blocks34[blk * kQ80Block] = (uint8_t)(dh & 0xff);
+                            ep.act_blocks34[blk * kQ80Block + 1] = (uint8_t)(dh >> 8);
+                        }
+                        ep.act_blocks34[blk * kQ80Block + 2 + e] = (uint8_t)qv;
+                    }
                 }
             }
         } else {
@@ -534,169 +627,194 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(MxTraits<MO
                     ep.out[(size_t)s_stage_ent[k][t] * a.rows + row] = s_stage[k][0][t][r];
             }
         }
-        // Leave with the stores complete so the compiler's wait counts on
-        // the streaming path stay exact.
-        __builtin_amdgcn_s_waitcnt(0);
     };
 
-    // One segment of the stream: cur is stored and multiplied, nxt is
-    // refilled with the lead cursor's segment.
-    auto step = [&](SegBuf &cur, SegBuf &nxt) -> bool {
-        const Meta cm = cur.m;
-        if (cm.done()) return true;
-        const int ce = cm.e(), cks = cm.ks(), ctile = cm.tile(), cp = cm.p(), cslot = cm.slot();
-        if (cks == 0 && (cslot != staged_slot || cp != staged_p)) {
-            // New token set.  Every wave is past the previous epilogue's
-            // final barrier, so the tables are free.
-            const int begin = MODE == kRows ? 0 : rt.offsets[ce];
-            const int count = MODE == kRows ? a.ntok : rt.offsets[ce + 1] - begin;
-            nt = min(kTokPerPass, count - cp * kTokPerPass);
-            npair = (nt + 1) >> 1;
-            if (tid < kTokPerPass) {
-                int ent = 0, arow = 0;
-                if (tid < nt) {
-                    ent = MODE == kRows ? cp * kTokPerPass + tid : rt.list[begin + cp * kTokPerPass + tid];
-                    arow = MODE == kGateUp ? ent / a.topk : ent;
-                }
-                s_entry[tid] = ent;
-                s_arow[tid] = arow;
+    PassTokens npt = pass_tokens<MODE>(a, rt, cur);  // tokens of the unit in the registers
+    prefetch(cur);
+    issue_all();
+
+    for (int w = w0; w < w1; w++) {
+        const Cursor u = cur;
+        const PassTokens pt = npt;
+        const bool new_tab = u.slot != staged_slot || u.p != staged_p;
+        if (new_tab) {
+            // Every wave is past the previous unit's final barrier, so the
+            // tables are free.  Digit tables [tok][nbp][64] and d_x
+            // [tok][nbp] of the pass's tokens, zero past nb and for the
+            // unused token slots.  A pass change is rare (each workgroup
+            // walks a contiguous range of work items), so these loads are
+            // not prefetched.
+            u32x4v tq[kTabLoads];
+            float tdx[kDxLoads];
+#pragma unroll
+            for (int k = 0; k < kTabLoads; k++) {
+                const int j = tid + kWG * k;  // 16-byte piece of [tok][nbp][64]
+                const int t = j / (4 * nbp), rem = j - t * 4 * nbp, b = rem >> 2;
+                u32x4v v = {0u, 0u, 0u, 0u};
+                if (t < pt.nt && b < nb)
+                    v = *reinterpret_cast<const u32x4v *>(a.mxtab + ((size_t)pick4(pt.arow, t) * nb + b) * 64 +
+                                                          (rem & 3) * 16);
+                tq[k] = v;
             }
-            lds_barrier();
-            // Tables of the nt tokens, zero past block nb; d_x zero past nb
-            // and for the unused token slots.
-            const int mxw = nbp * 16;  // dwords of digit table per token
-            for (int t = 0; t < nt; t++) {
-                uint32_t *dst = reinterpret_cast<uint32_t *>(s_mx + (size_t)t * nbp * 64);
-                const uint32_t *src = reinterpret_cast<const uint32_t *>(a.mxtab + (size_t)s_arow[t] * nb * 64);
-                for (int i = tid; i < mxw; i += kWG) dst[i] = i < nb * 16 ? src[i] : 0u;
-            }
-            for (int i = tid; i < kTokPerPass * nbp; i += kWG) {
+#pragma unroll
+            for (int k = 0; k < kDxLoads; k++) {
+                const int i = tid + kWG * k;
                 const int t = i / nbp, b = i - t * nbp;
-                s_dx[i] = (t < nt && b < nb) ? a.scales[(size_t)s_arow[t] * nb + b] : 0.0f;
+                float v = 0.0f;
+                if (t < pt.nt && b < nb) v = a.scales[(size_t)pick4(pt.arow, t) * nb + b];
+                tdx[k] = v;
+            }
+#pragma unroll
+            for (int k = 0; k < kTabLoads; k++) {
+                const int j = tid + kWG * k;
+                if (j < 16 * nbp) *reinterpret_cast<u32x4v *>(s_mx + (size_t)j * 16) = tq[k];
+            }
+#pragma unroll
+            for (int k = 0; k < kDxLoads; k++) {
+                const int i = tid + kWG * k;
+                if (i < kTokPerPass * nbp) s_dx[i] = tdx[k];
             }
 #pragma unroll
             for (int tp = 0; tp < 2; tp++) {
                 const int t = 2 * tp + L.slot;
-                PR.tb[tp] = (uint32_t)((t * nbp + L.gc) * 64 + L.boff);
-                PR.db[tp] = (uint32_t)((t * nbp + L.gc) * 4);
-                PR.lo[tp] = L.lo_on && t < nt;
-                PR.hi[tp] = L.hi_on && t < nt;
+                const uint8_t *tb = s_mx + (t * nbp + L.gc) * 64 + L.boff;
+                PR.bl[tp] = (L.lo_on && t < pt.nt) ? tb : s_zero;
+                PR.bh[tp] = (L.hi_on && t < pt.nt) ? tb : s_zero;
+                PR.dx[tp] = s_dx + t * nbp + L.gc;
             }
-            lds_barrier();
-            staged_slot = cslot;
-            staged_p = cp;
-            // This rare path loads in loops; ending it with nothing
-            // outstanding keeps the compiler's wait counts on the common
-            // path exact.
-            __builtin_amdgcn_s_waitcnt(0);
+            npair = (pt.nt + 1) >> 1;
+            staged_slot = u.slot;
+            staged_p = u.p;
         }
-        fetch(nxt);
+        const int row0 = u.tile * tile_rows + roff;
+        const bool wave_ok = row0 < a.rows;
+        tile_wait(tr);
+        if (wave_ok) {
+            tile_store<0>(img_lds, tr);
+            if (ngroups > 1) tile_store<1>(img_lds + 4096u, tr);
+            if (ngroups > 2) tile_store<2>(img_lds + 8192u, tr);
+            if (ngroups > 3) tile_store<3>(img_lds + 12288u, tr);
+            if (ngroups > 4) tile_store<4>(img_lds + 16384u, tr);
+            if (ngroups > 5) tile_store<5>(img_lds + 20480u, tr);
+            if (ngroups > 6) tile_store<6>(img_lds + 24576u, tr);
+        }
+        // The bias words arrived with the tile; take them now so no later
+        // use waits on the next unit's loads.
+        uint32_t bw0 = b0r, bw1 = b1r;
+        asm volatile("" : "+v"(bw0), "+v"(bw1));
+        nxt_ok = false;
+        if (w + 1 < w1) {
+            cursor_advance<MODE>(a, rt, cur, tiles);
+            const bool ntab = cur.slot != u.slot || cur.p != u.p;
+            if (ntab) npt = pass_tokens<MODE>(a, rt, cur);
+            prefetch(cur);
+        }
+        if (new_tab)
+            lds_barrier();
+        else
+            wave_lds_fence();
+        if (n_staged == kStage) {
+            lds_barrier();  // every wave's staging is complete
+            flush(n_staged);
+            n_staged = 0;
+        }
 
-        const int r0 = ctile * tile_rows + roff;
-        const ByteView cview = make_view(wbase + (uint64_t)ce * a.expert_bytes, a.expert_bytes);
-        // cur's loads are complete once no more than the later segments'
-        // stream loads are outstanding
-        stream_wait<(NBUF - 1) * kStreamPerSeg>(cur.r);
+        const uint8_t *view_base = wbase + (uint64_t)u.e * a.expert_bytes;
         {
-            uint32_t p0;
-            bool bin;
-            seg_pos(ctile, cks, false, cview.lead, p0, bin);
-            seg_store(cur.r, p0, bin, grp_step, r0, a.rows, L, sA, sE, special);
+            const uint32_t lead = (uint32_t)((reinterpret_cast<uintptr_t>(view_base) & 15u) + (uint32_t)row0 * row_bytes) & 15u;
+            TileView tv = tile_view(img, lead + (uint32_t)L.i * row_bytes, L);
+            auto segment = [&](auto gc) {
+                constexpr int G = decltype(gc)::value;
+                issue(gc);
+                if (G < 6 && wave_ok) {
+                    if (npair == 2)
+                        tile_segment<2>(G, tv, nb, nch, L, PR, acc);
+                    else
+                        tile_segment<1>(G, tv, nb, nch, L, PR, acc);
+                }
+            };
+            static_assert(kTileGroups == 7, "segments below");
+            segment(std::integral_constant<int, 0>{});
+            segment(std::integral_constant<int, 1>{});
+            segment(std::integral_constant<int, 2>{});
+            segment(std::integral_constant<int, 3>{});
+            segment(std::integral_constant<int, 4>{});
+            segment(std::integral_constant<int, 5>{});
+            segment(std::integral_constant<int, 6>{});
+            special = wave_ok && tile_special(tv, row0 + L.i < a.rows);
         }
         wave_lds_fence();
-        seg_mfma(cks, npair, L, PR, s_zero, sA, sE, s_mx, reinterpret_cast<const uint8_t *>(s_dx), acc);
-        wave_lds_fence();
 
-        if (cks == nseg - 1) {
-            // Sum the eight columns of each token slot (parts h/l x blocks).
+        // Sum the eight columns of each token slot (parts h/l x blocks).
 #pragma unroll
-            for (int tp = 0; tp < 2; tp++)
+        for (int tp = 0; tp < 2; tp++)
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    float v = acc[tp][i];
-                    v += __shfl_xor(v, 4, 8);
-                    v += __shfl_xor(v, 1, 4);
-                    v += __shfl_xor(v, 2, 4);
-                    acc[tp][i] = v;
-                }
-            if ((c16 & 7) == 0) {
+            for (int i = 0; i < 4; i++) acc[tp][i] = sum8(acc[tp][i]);
+        float(*res)[16][kTokPerPass] = s_res[w & 1];
+        if ((c16 & 7) == 0) {
 #pragma unroll
-                for (int tp = 0; tp < 2; tp++) {
-                    const int t = 2 * tp + L.slot;
-                    if (t < nt) {
+            for (int tp = 0; tp < 2; tp++) {
+                const int t = 2 * tp + L.slot;
+                if (t < pt.nt) {
 #pragma unroll
-                        for (int i = 0; i < 4; i++) s_res[wave][4 * L.gb + i][t] = acc[tp][i];
-                    }
+                    for (int i = 0; i < 4; i++) res[wave][4 * L.gb + i][t] = acc[tp][i];
                 }
             }
-            // Rows with special scales: recompute with the integer decode.
-            if (__any(special)) {
-                const int row_l = lane >> 2, sub = lane & 3;
-                const int row = r0 + row_l;
-                const uint32_t pos = (uint32_t)(row < a.rows ? row : 0) * row_bytes;
-                for (int t = 0; t < nt; t++) {
-                    const uint32_t *codes = reinterpret_cast<const uint32_t *>(a.codes + (size_t)s_arow[t] * nb * 32);
-                    float v = lut_row_dot(cview, pos, nb, codes, s_dx + t * nbp, sub);
-                    if (sub == 0) s_res[wave][row_l][t] = v;
-                }
-                __builtin_amdgcn_s_waitcnt(0);
+        }
+        // Rows with special scales: recompute with the integer decode.
+        if (__any(special)) {
+            const ByteView cview = make_view(view_base, a.expert_bytes);
+            const int row_l = lane >> 2, sub = lane & 3;
+            const int row = row0 + row_l;
+            const uint32_t pos = (uint32_t)(row < a.rows ? row : 0) * row_bytes;
+            for (int t = 0; t < pt.nt; t++) {
+                const uint32_t *codes = reinterpret_cast<const uint32_t *>(a.codes + (size_t)pick4(pt.arow, t) * nb * 32);
+                const float v = lut_row_dot(cview, pos, nb, codes, s_dx + t * nbp, sub);
+                if (sub == 0) res[wave][row_l][t] = v;
             }
-            lds_barrier();
-            const int tile = ctile;
-            const uint32_t brow = (uint32_t)ce * (uint32_t)a.rows + (uint32_t)(tile * tile_rows + erow);
-            const int k = n_staged;
-            if (tid == 0) {
-                s_stage_tile[k] = tile;
-                s_stage_nt[k] = nt;
-            }
-            if (tid < kTokPerPass) s_stage_ent[k][tid] = s_entry[tid];
-            if constexpr (MODE == kGateUp) {
-                // 32 rows x nt tokens: bias, clamped SwiGLU.
+        }
+        lds_barrier();
+        const uint32_t brow = (uint32_t)u.e * (uint32_t)a.rows + (uint32_t)(u.tile * tile_rows + erow);
+        const int k = n_staged;
+        if (tid == 0) {
+            s_stage_tile[k] = u.tile;
+            s_stage_nt[k] = pt.nt;
+        }
+        if (tid < kTokPerPass) s_stage_ent[k][tid] = pick4(pt.ent, tid);
+        if constexpr (MODE == kGateUp) {
+            // 32 rows x nt tokens (waves 0-1, a half-wave per token): bias,
+            // clamped SwiGLU, and the Q8_0 block of the act row.
+            if (wave < 2) {
                 const int t = tid >> 5;
-                const float b0 = bias_value(bv0, cur.r.b0, brow), b1 = bias_value(bv1, cur.r.b1, brow);
-                if (t < nt) {
-                    const float gv = s_res[erow >> 4][erow & 15][t] + b0;
-                    const float uv = s_res[2 + (erow >> 4)][erow & 15][t] + b1;
-                    s_stage[k][0][t][erow] = swiglu(gv, uv);
-                    s_stage[k][MxTraits<MODE>::kStageVals - 2][t][erow] = gv;
-                    s_stage[k][MxTraits<MODE>::kStageVals - 1][t][erow] = uv;
+                const float b0 = bias_value(bv0, bw0, brow), b1 = bias_value(bv1, bw1, brow);
+                const float gv = res[erow >> 4][erow & 15][t] + b0;
+                const float uv = res[2 + (erow >> 4)][erow & 15][t] + b1;
+                const float v = swiglu(gv, uv);
+                uint16_t dh;
+                const int qv = q8_quantize_half(v, lane, &dh);
+                if (t < pt.nt) {
+                    s_stage[k][0][t][erow] = v;
+                    s_stage[k][1][t][erow] = gv;
+                    s_stage[k][2][t][erow] = uv;
+                    s_sq[k][t][erow] = (int8_t)qv;
+                    const int pn = 2 * (erow & 15) + (erow >> 4);  // nibble position of element erow
+                    s_smx[k][t][pn] = (uint8_t)e4m3_small(qv >> 4);
+                    s_smx[k][t][32 + pn] = (uint8_t)e4m3_small(qv & 15);
+                    if (erow == 0) s_sdh[k][t] = dh;
                 }
-            } else {
-                const int t = tid >> 6;
-                const float b0 = bias_value(bv0, cur.r.b0, brow);
-                if (t < nt) s_stage[k][0][t][erow] = s_res[erow >> 4][erow & 15][t] + b0;
             }
-            if (++n_staged == kStage) {
-                lds_barrier();
-                flush(n_staged);
-                n_staged = 0;
-            }
-            lds_barrier();
-#pragma unroll
-            for (int p = 0; p < 2; p++)
-#pragma unroll
-                for (int i = 0; i < 4; i++) acc[p][i] = 0.0f;
-            special = false;
+        } else {
+            const int t = tid >> 6;
+            const float b0 = bias_value(bv0, bw0, brow);
+            if (t < pt.nt) s_stage[k][0][t][erow] = res[erow >> 4][erow & 15][t] + b0;
         }
-        return false;
-    };
-
-    // The ring, unrolled so every buffer keeps fixed registers; leaving by
-    // jump keeps the load count at the loop's back edge the same on every
-    // path, so the compiler's wait counts stay exact.
-    for (;;) {
+        ++n_staged;
 #pragma unroll
-        for (int k = 0; k < NBUF; k++) {
-            if (step(bufs[k], bufs[(k + NBUF - 1) % NBUF])) goto ring_done;
-        }
+        for (int p = 0; p < 2; p++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc[p][i] = 0.0f;
+        special = false;
     }
-ring_done:
-    // The last NBUF - 1 fetches (past the end, reading zeros) are still in
-    // flight and will write their registers; keep those registers reserved
-    // until the loads have landed, so the code below cannot be handed a
-    // register that a late load overwrites.
-#pragma unroll
-    for (int k = 0; k < NBUF; k++) stream_wait<0>(bufs[k].r);
     if (n_staged > 0) {
         lds_barrier();
         flush(n_staged);
@@ -705,9 +823,23 @@ ring_done:
 
 hipError_t launch_mx_mfma(hipStream_t s, GemvMode mode, const MxMfmaArgs &a, int slots) {
     if (slots <= 0 || a.rows <= 0) return hipSuccess;
-    const int nbp = (a.nb + kKSeg - 1) / kKSeg * kKSeg;
-    const size_t lds = 4 * (size_t)kWaveLds + (size_t)kTokPerPass * nbp * (64 + 4);
+    if (a.nb <= 0 || a.nb > kMaxNb) return hipErrorInvalidConfiguration;
+    const size_t nbp = (size_t)(a.nb + 7) / 8 * 8;
+    const size_t lds = 4 * (size_t)tile_region(a.nb) + (size_t)kTokPerPass * nbp * (64 + 4) + nbp * 64;
     if (lds > kMaxMxLds) return hipErrorInvalidConfiguration;
+    // one-time opt-in to more than 64 KB of dynamic LDS
+    static const hipError_t attr = [] {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_mx_mfma<kGateUp>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxMxLds);
+        if (e == hipSuccess)
+            e = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_mx_mfma<kDown>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxMxLds);
+        if (e == hipSuccess)
+            e = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_mx_mfma<kRows>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxMxLds);
+        return e;
+    }();
+    if (attr != hipSuccess) return attr;
     static int n_cu = 0;
     if (n_cu == 0) {
         int dev = 0;
@@ -719,9 +851,8 @@ hipError_t launch_mx_mfma(hipStream_t s, GemvMode mode, const MxMfmaArgs &a, int
     const int tile_rows = mode == kGateUp ? 32 : 64;
     const int max_passes = mode == kRows ? (a.ntok + kTokPerPass - 1) / kTokPerPass : slots;
     const int64_t items = (int64_t)max_passes * ((a.rows + tile_rows - 1) / tile_rows);
-    // workgroups of four waves: as many per CU as waves per SIMD
-    const int per_cu = mode == kGateUp ? MxTraits<kGateUp>::kWavesPerEU : MxTraits<kDown>::kWavesPerEU;
-    const int grid = items < per_cu * n_cu ? (int)items : per_cu * n_cu;
+    // one workgroup of four waves per CU (its LDS holds four tile images)
+    const int grid = items < n_cu ? (int)items : n_cu;
     if (mode == kGateUp) {
         hipLaunchKernelGGL(k_mx_mfma<kGateUp>, dim3(grid), dim3(kWG), lds, s, a, a.active, a.offsets, a.pass_off,
                            a.list, a.n_active);

@@ -143,6 +143,36 @@ def test_mxfp4_expert_gemv(gpu_ctx, O, input_dim, output_dim, batch):
         assert_close(got[t], want, what=f"token {t}")
 
 
+@pytest.mark.parametrize("bias_type", [1, 30])
+def test_mxfp4_expert_gemv_odd_half_bias(gpu_ctx, O, bias_type):
+    """One expert of 257 rows with a 2-byte bias: the last bias element sits
+    in a dword that crosses the tensor's end, and the matrix (257 * 17
+    bytes) ends inside a 16-byte load."""
+    import torch
+
+    import spt
+    from spt import synth
+
+    input_dim, output_dim = 64, 257
+    nb = input_dim // 32
+    w = synth.mxfp4_expert_bytes(synth.stream_key(8, 1), 0, output_dim * nb)
+    b32 = synth.normal(synth.stream_key(9, 1), output_dim, 0.0, 0.5)
+    if bias_type == 1:
+        bh = b32.astype(np.float16).view(np.uint16)
+        bias = bh.view(np.float16).astype(np.float32)
+    else:
+        bh = (b32.view(np.uint32) >> 16).astype(np.uint16)
+        bias = (bh.astype(np.uint32) << 16).view(np.float32)
+    x = synth.normal(synth.stream_key(10, 1), input_dim)
+    wd, bd, xd = _dev(w), _dev(bh), _dev(x)
+    y = torch.zeros(output_dim, dtype=torch.float32, device="cuda")
+    bt = spt.Tensor.make("b", bias_type, [output_dim, 1], bd.data_ptr(), output_dim * 2)
+    gpu_ctx.mul_mxfp4_expert(_mx_tensor(wd, input_dim, output_dim, 1), bt, 0, xd, y, 1)
+    torch.cuda.synchronize()
+    want = O.mul_mxfp4_q8(w, _q8_of(O, x), bias, input_dim, output_dim)
+    assert_close(y.cpu().numpy(), want, what="odd-count 2-byte bias")
+
+
 @pytest.mark.parametrize("input_dim,output_dim", [(2880, 4096), (2880, 512), (4096, 2880), (32, 17)])
 @pytest.mark.parametrize("batch", [1, 32])
 def test_q40_gemv(gpu_ctx, O, input_dim, output_dim, batch):
