@@ -186,6 +186,9 @@ int validate_expert(const spt_tensor *t, int64_t input, int64_t output, int64_t 
     if (!t->data) return fail(SPT_ERR_INVALID, "\"%s\": tensor is not resident (nil data)", tname(t));
     if ((uint64_t)(input / 32 * 17) * (uint64_t)output > 0xFFFFFFF0ull)
         return fail(SPT_ERR_INVALID, "\"%s\": expert matrix larger than 4 GiB is not supported", tname(t));
+    if (input > spt::kMxMaxInput)
+        return fail(SPT_ERR_INVALID, "\"%s\": MXFP4 input dimension %lld exceeds the supported %d", tname(t),
+                    (long long)input, spt::kMxMaxInput);
     return SPT_OK;
 }
 

@@ -11,6 +11,9 @@ constexpr int kMaxExperts = 256;
 constexpr int kMaxSelections = 4096;
 // Tokens of an expert's list per pass of the grouped GEMV over its weights.
 constexpr int kGemvTokens = 4;
+// Largest MXFP4 input dimension of the grouped GEMV: a workgroup stages four
+// 16-row tiles of whole rows in LDS (GPT-OSS uses 2880 for both projections).
+constexpr int kMxMaxInput = 2880;
 
 struct SelectOut {
     int32_t *ids;

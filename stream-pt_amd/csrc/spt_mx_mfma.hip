@@ -33,7 +33,8 @@ namespace {
 typedef int v8i __attribute__((ext_vector_type(8)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 
-constexpr int kWG = 256;
+constexpr int kWaves = 8;
+constexpr int kWG = 64 * kWaves;
 constexpr int kTokPerPass = kGemvTokens;  // two MFMA token slots x two MFMAs per chunk
 constexpr int kEMin = 4, kEMax = 254;
 
@@ -70,7 +71,7 @@ __device__ float lut_row_dot(const ByteView &v, uint32_t row_pos, int nb, const 
 // tile the loads of its next tile are in flight.  The image of one tile (nb
 // up to kMaxNb) plus the token tables must fit the LDS of a CU, which holds
 // one workgroup of four waves.
-constexpr int kMaxNb = 96;
+constexpr int kMaxNb = kMxMaxInput / 32;
 constexpr int kMaxNbp = (kMaxNb + 7) / 8 * 8;
 // 1 KB loads of a tile image: 16 rows plus up to 15 bytes before them.
 __host__ __device__ constexpr int tile_loads(int nb) { return (16 * nb * kMxBlock + 15 + 1023) / 1024; }
@@ -83,7 +84,8 @@ __host__ __device__ constexpr int tile_region(int nb) {
                 : (16 * nb * kMxBlock + 137 + 1023) / 1024) *
            1024;
 }
-constexpr int kTileGroups = (tile_loads(kMaxNb) + 3) / 4;  // groups of four 1 KB loads
+constexpr int kTileGroups = (tile_loads(kMaxNb) + 3) / 4;  // groups of four 1 KB loads per tile
+constexpr int kWaveGroups = (kTileGroups + 1) / 2;            // of them, loaded by one wave
 constexpr int kTabLoads = (16 * kMaxNbp + kWG - 1) / kWG;  // 16-byte digit-table pieces per thread
 constexpr int kDxLoads = (kTokPerPass * kMaxNbp + kWG - 1) / kWG;  // d_x entries per thread
 constexpr size_t kMaxMxLds = 146 * 1024;  // dynamic LDS; with the static part (< 14 KB) within 160 KB
@@ -114,10 +116,10 @@ __device__ inline void lds_barrier() {
 
 typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
 
-// A tile image in flight: four loads of 1 KB per group, held in the
-// accumulation registers so the VGPRs serve the multiply.  The loads are
-// issued and waited for with inline assembly (the compiler does not place
-// global loads in accumulation registers): tile_issue writes the registers
+// A wave's part of a tile image in flight: four loads of 1 KB per group.
+// The loads are issued and waited for with inline assembly, out of sight of
+// the compiler's wait-count analysis, which turns conservative (a full
+// drain) at the loop's control-flow joins: tile_issue writes the registers
 // asynchronously, tile_wait (s_waitcnt vmcnt(0)) names every one of them,
 // and only tile_store reads them, after the wait.  Each issue block opens
 // with five wait states: its descriptor and offset SGPRs may have just been
@@ -125,7 +127,7 @@ typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
 // early, and the compiler cannot pad inside inline assembly.  Offsets past
 // the descriptor's range read zeros.
 struct TileRegs {
-    u32x4v q[4 * kTileGroups];
+    u32x4v q[4 * kWaveGroups];
 };
 
 template <int G>
@@ -136,18 +138,15 @@ __device__ inline void tile_issue(TileRegs &t, uint32_t vo, const u32x4v &rs, ui
         "buffer_load_dwordx4 %1, %4, %5, %6 offen offset:1024\n\t"
         "buffer_load_dwordx4 %2, %4, %5, %6 offen offset:2048\n\t"
         "buffer_load_dwordx4 %3, %4, %5, %6 offen offset:3072"
-        : "=&a"(t.q[4 * G]), "=&a"(t.q[4 * G + 1]), "=&a"(t.q[4 * G + 2]), "=&a"(t.q[4 * G + 3])
+        : "=&v"(t.q[4 * G]), "=&v"(t.q[4 * G + 1]), "=&v"(t.q[4 * G + 2]), "=&v"(t.q[4 * G + 3])
         : "v"(vo), "s"(rs), "s"(so));
 }
 
 __device__ inline void tile_wait(TileRegs &t) {
-    static_assert(kTileGroups == 7, "operand list below");
+    static_assert(kWaveGroups == 3, "operand list below");
     asm volatile("s_waitcnt vmcnt(0)"
-                 : "+a"(t.q[0]), "+a"(t.q[1]), "+a"(t.q[2]), "+a"(t.q[3]), "+a"(t.q[4]), "+a"(t.q[5]),
-                   "+a"(t.q[6]), "+a"(t.q[7]), "+a"(t.q[8]), "+a"(t.q[9]), "+a"(t.q[10]), "+a"(t.q[11]),
-                   "+a"(t.q[12]), "+a"(t.q[13]), "+a"(t.q[14]), "+a"(t.q[15]), "+a"(t.q[16]), "+a"(t.q[17]),
-                   "+a"(t.q[18]), "+a"(t.q[19]), "+a"(t.q[20]), "+a"(t.q[21]), "+a"(t.q[22]), "+a"(t.q[23]),
-                   "+a"(t.q[24]), "+a"(t.q[25]), "+a"(t.q[26]), "+a"(t.q[27]));
+                 : "+v"(t.q[0]), "+v"(t.q[1]), "+v"(t.q[2]), "+v"(t.q[3]), "+v"(t.q[4]), "+v"(t.q[5]),
+                   "+v"(t.q[6]), "+v"(t.q[7]), "+v"(t.q[8]), "+v"(t.q[9]), "+v"(t.q[10]), "+v"(t.q[11]));
 }
 
 template <int G>
@@ -158,7 +157,7 @@ __device__ inline void tile_store(uint32_t lds, const TileRegs &t) {
         "ds_write_b128 %0, %3 offset:2048\n\t"
         "ds_write_b128 %0, %4 offset:3072"
         :
-        : "v"(lds), "a"(t.q[4 * G]), "a"(t.q[4 * G + 1]), "a"(t.q[4 * G + 2]), "a"(t.q[4 * G + 3])
+        : "v"(lds), "v"(t.q[4 * G]), "v"(t.q[4 * G + 1]), "v"(t.q[4 * G + 2]), "v"(t.q[4 * G + 3])
         : "memory");
 }
 
@@ -279,18 +278,20 @@ __device__ __attribute__((always_inline)) inline void chunk_pair(TileView &v, in
     for (int h = 0; h < 2; h++) chunk_mfma<NP, MASK>(r[h], c0 + h, nb, v.sel, v.esh, L, acc, v.emin, v.emax);
 }
 
-// Segment g (0..5) of a tile's chunks.  Before segment g the caller issues
-// group g of the next tile's loads, so the next tile's requests spread over
-// the multiply.  24 chunks (nb in [89, 96]: the GPT-OSS dimension 2880 has
-// nb = 90) are straight-line quads, chunks 22 and 23 masked; any other
-// (even) chunk count splits its chunk pairs evenly over the segments, the
-// pairs holding blocks past nb masked.
+// Part `part` (0..2) of the chunks of wave half h (the waves of a row tile
+// split its chunks in halves, each in three parts; before each part a wave
+// issues one group of the next tile's loads).  24 chunks (nb in [89, 96]:
+// the GPT-OSS dimension 2880 has nb = 90): half h takes chunks 12h..12h+11
+// as three straight-line quads, chunks 22-23 (possibly past nb) masked; any
+// other even chunk count: half h takes half of the chunk pairs, split over
+// the three parts, the pairs holding blocks past nb masked.
 template <int NP>
-__device__ __attribute__((always_inline)) inline void tile_segment(int g, TileView &v, int nb, int nch, const LaneRole &L, const PassRole &P,
-                                    float acc[2][4]) {
+__device__ __attribute__((always_inline)) inline void tile_part(int part, int h, TileView &v, int nb, int nch,
+                                                                const LaneRole &L, const PassRole &P, float acc[2][4]) {
     if (nch == 24) {
-        if (g < 5) {
-            chunk_quad<NP, false>(v, 4 * g, nb, L, P, acc);
+        const int c0 = 12 * h + 4 * part;
+        if (c0 < 20) {
+            chunk_quad<NP, false>(v, c0, nb, L, P, acc);
         } else {
             chunk_pair<NP, false>(v, 20, nb, L, P, acc);
             chunk_pair<NP, true>(v, 22, nb, L, P, acc);
@@ -298,7 +299,8 @@ __device__ __attribute__((always_inline)) inline void tile_segment(int g, TileVi
         return;
     }
     const int npairs = nch / 2, nfull = nb / 8;  // pairs, and pairs whose 8 blocks are all < nb
-    for (int p = g * npairs / 6; p < (g + 1) * npairs / 6; p++) {
+    const int p0 = h ? npairs / 2 : 0, np = h ? npairs - npairs / 2 : npairs / 2;
+    for (int p = p0 + part * np / 3; p < p0 + (part + 1) * np / 3; p++) {
         if (p < nfull)
             chunk_pair<NP, false>(v, 2 * p, nb, L, P, acc);
         else
@@ -408,21 +410,25 @@ __device__ inline int pick4(const int (&v)[kTokPerPass], int t) {
     return t == 0 ? v[0] : t == 1 ? v[1] : t == 2 ? v[2] : v[3];
 }
 
-// Persistent workgroups, one per CU: workgroup b takes work items
-// [b*W/G, (b+1)*W/G) of the W = total passes x row tiles, in order, so
+// Persistent workgroups, one per CU, of eight waves: workgroup b takes work
+// items [b*W/G, (b+1)*W/G) of the W = total passes x row tiles, in order, so
 // consecutive items share an expert's token pass and its staged token
 // tables, and every workgroup streams the same number of weight bytes.
-// Gate/up units are 32 output rows (waves 0-1 gate, 2-3 up, so SwiGLU and
-// the Q8_0 of the 32-element act block stay in the workgroup); down and
-// single-expert units are 64 rows, 16 per wave.
+// Gate/up units are 32 output rows (row tiles 0-1 gate, 2-3 up, so SwiGLU
+// and the Q8_0 of the 32-element act block stay in the workgroup); down and
+// single-expert units are 64 rows; a row tile is 16 rows.  Waves r and r + 4
+// (the same SIMD) share row tile r's image: each loads half of its load
+// groups and multiplies half of its chunks, and their partial row sums are
+// added in the epilogue, so every SIMD runs two waves that hide each
+// other's latencies.
 //
 // Each step: wait for the prefetched tile and write it (and, at a new pass,
-// the token tables) to LDS; issue the next unit's loads; flush staged
-// outputs if the stage is full; multiply; reduce and stage the unit's
-// outputs.  The only wait for global loads is at the top of a step, for
-// loads issued a whole step earlier.
+// the token tables) to LDS; flush staged outputs if the stage is full;
+// multiply, issuing the next unit's load groups between parts of the
+// multiply; reduce and stage the unit's outputs.  The only wait for global
+// loads is at the top of a step, for loads issued during the step before.
 template <int MODE>
-__global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(1))) void k_mx_mfma(MxMfmaArgs a, const int32_t *__restrict__ r_active,
+__global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(2))) void k_mx_mfma(MxMfmaArgs a, const int32_t *__restrict__ r_active,
                                                                       const int32_t *__restrict__ r_offsets,
                                                                       const int32_t *__restrict__ r_pass_off,
                                                                       const int32_t *__restrict__ r_list,
@@ -436,9 +442,11 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(1))) void k
         uint8_t *act_mxtab, *act_blocks34;
     };
     __shared__ EpiPtrs s_epi;
-    // Row sums of a unit per wave (double-buffered by step parity, so a
-    // step's staging and the next step's sums do not need a barrier apart).
-    __shared__ float s_res[2][4][16][kTokPerPass];
+    // Partial row sums of a unit per wave half and row tile, and the waves'
+    // special-scale flags (double-buffered by step parity, so a step's
+    // staging and the next step's sums need no barrier apart).
+    __shared__ float s_res[2][2][4][16][kTokPerPass];
+    __shared__ int s_special[2][kWaves];
     // Outputs of finished units, written to global memory kStageUnits units
     // at a time, at the top of a step.  Gate/up also stages each act block's
     // Q8_0 codes, digit-table bytes and fp16 scale bits.
@@ -461,12 +469,17 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(1))) void k
     const int region = tile_region(nb);
     // wave-uniform: keeps per-wave descriptors and offsets in scalar registers
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    // LDS: per-wave tile images, then [tok][nbp][64] digit tables, [tok][nbp] d_x
-    uint8_t *img = smem_b + (size_t)wave * region;
+    const int rt4 = wave & 3, half = wave >> 2;  // row tile, and which half of it this wave takes
+    // load groups of this wave: [g0, g0 + gmine)
+    const int g0 = half ? (ngroups + 1) / 2 : 0;
+    const int gmine = half ? ngroups / 2 : (ngroups + 1) / 2;
+    // LDS: row tiles' images, then [tok][nbp][64] digit tables, [tok][nbp] d_x, zeros
+    uint8_t *img = smem_b + (size_t)rt4 * region;
     uint8_t *s_mx = smem_b + (size_t)4 * region;
-    // LDS address of this lane's 16 bytes of the image
+    // LDS address of this lane's 16 bytes of the image's first group of this wave
     typedef __attribute__((address_space(3))) uint8_t lds_u8;
-    const uint32_t img_lds = (uint32_t)reinterpret_cast<uintptr_t>((lds_u8 *)img) + 16u * (uint32_t)lane;
+    const uint32_t img_lds =
+        (uint32_t)reinterpret_cast<uintptr_t>((lds_u8 *)img) + 4096u * (uint32_t)g0 + 16u * (uint32_t)lane;
     float *s_dx = reinterpret_cast<float *>(s_mx + (size_t)kTokPerPass * nbp * 64);
     uint8_t *s_zero = reinterpret_cast<uint8_t *>(s_dx + kTokPerPass * nbp);  // nbp * 64 bytes of zeros
 
@@ -491,8 +504,8 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(1))) void k
         slot0 = ones - 1;
     }
 
-    const int m = MODE == kGateUp ? (wave >> 1) : 0;
-    const int roff = MODE == kGateUp ? (wave & 1) * 16 : wave * 16;
+    const int m = MODE == kGateUp ? (rt4 >> 1) : 0;
+    const int roff = MODE == kGateUp ? (rt4 & 1) * 16 : rt4 * 16;
     LaneRole L;
     L.i = lane & 15;
     L.gb = lane >> 4;
@@ -508,7 +521,7 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(1))) void k
     for (int i = tid; i < nbp * 4; i += kWG) reinterpret_cast<u32x4v *>(s_zero)[i] = u32x4v{0u, 0u, 0u, 0u};
 
     // Epilogue element of this thread: gate/up: row tid&31 of the unit,
-    // token tid>>5; down/rows: row tid&63, token tid>>6.
+    // token tid>>5 (waves 0-1); down/rows: row tid&63, token tid>>6 (waves 0-3).
     const int erow = MODE == kGateUp ? (tid & 31) : (tid & 63);
     const BiasView bv0 = make_bias_view(a.bias[0], a.bias_bytes[0], a.bias_type[0]);
     const BiasView bv1 = make_bias_view(a.bias[1], a.bias_bytes[1], a.bias_type[1]);
@@ -521,31 +534,21 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(1))) void k
     cur.tile = w0 - q0 * tiles;
     slot_info<MODE>(a, rt, cur);
 
-    // Registers of the next unit: its tile image, its pass's token tables
-    // (only loaded when the pass changes) and the epilogue element's raw
-    // bias words.
+    // Registers of the next unit: this wave's groups of its tile image, and
+    // the epilogue element's raw bias words.
     TileRegs tr;
-    // the next unit's tile: descriptor, aligned start, and whether this wave loads it
+    // the next unit's tile: descriptor, aligned start of this wave's groups,
+    // and whether this wave loads it
     u32x4v nrs = {0u, 0u, 0u, 0u};
     uint32_t na0 = 0u;
     bool nxt_ok = false;
     const uint32_t vo = 16u * (uint32_t)lane;
-    // group G of the next tile's loads (G a compile-time constant, so every
-    // issue block writes fixed registers)
+    // local group G of the next tile's loads (G a compile-time constant, so
+    // every issue block writes fixed registers)
     auto issue = [&](auto gc) {
         constexpr int G = decltype(gc)::value;
-        static_assert(G < kTileGroups, "group");
-        if (nxt_ok && G < ngroups) tile_issue<G>(tr, vo, nrs, na0 + 4096u * G);
-    };
-    auto issue_all = [&]() {
-        static_assert(kTileGroups == 7, "list below");
-        issue(std::integral_constant<int, 0>{});
-        issue(std::integral_constant<int, 1>{});
-        issue(std::integral_constant<int, 2>{});
-        issue(std::integral_constant<int, 3>{});
-        issue(std::integral_constant<int, 4>{});
-        issue(std::integral_constant<int, 5>{});
-        issue(std::integral_constant<int, 6>{});
+        static_assert(G < kWaveGroups, "group");
+        if (nxt_ok && G < gmine) tile_issue<G>(tr, vo, nrs, na0 + 4096u * G);
     };
     uint32_t b0r = 0u, b1r = 0u;
     auto prefetch = [&](const Cursor &c) {
@@ -567,7 +570,7 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(1))) void k
             const u32x4v rs = {(uint32_t)base, (uint32_t)(base >> 32) & 0xFFFFu,
                                (uint32_t)((a.expert_bytes + le + 15u) & ~15ull), (uint32_t)kRsrcWord3};
             nrs = rs;
-            na0 = (le + (uint32_t)row0 * row_bytes) & ~15u;
+            na0 = ((le + (uint32_t)row0 * row_bytes) & ~15u) + 4096u * (uint32_t)g0;
             nxt_ok = true;
         }
     };
@@ -579,7 +582,6 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(1))) void k
     for (int p = 0; p < 2; p++)
 #pragma unroll
         for (int i = 0; i < 4; i++) acc[p][i] = 0.0f;
-    bool special = false;
 
     // Write out the staged units (all waves, after a barrier).  Gate/up:
     // thread-per-element act (for the tap), the gate/up taps and the act
@@ -631,19 +633,22 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(1))) void k
 
     PassTokens npt = pass_tokens<MODE>(a, rt, cur);  // tokens of the unit in the registers
     prefetch(cur);
-    issue_all();
+    static_assert(kWaveGroups == 3, "issue list below");
+    issue(std::integral_constant<int, 0>{});
+    issue(std::integral_constant<int, 1>{});
+    issue(std::integral_constant<int, 2>{});
 
     for (int w = w0; w < w1; w++) {
         const Cursor u = cur;
         const PassTokens pt = npt;
         const bool new_tab = u.slot != staged_slot || u.p != staged_p;
         if (new_tab) {
-            // Every wave is past the previous unit's final barrier, so the
-            // tables are free.  Digit tables [tok][nbp][64] and d_x
-            // [tok][nbp] of the pass's tokens, zero past nb and for the
-            // unused token slots.  A pass change is rare (each workgroup
-            // walks a contiguous range of work items), so these loads are
-            // not prefetched.
+            // Every wave is past the previous unit's first epilogue barrier,
+            // after its last table read, so the tables are free.  Digit
+            // tables [tok][nbp][64] and d_x [tok][nbp] of the pass's tokens,
+            // zero past nb and for the unused token slots.  A pass change is
+            // rare (each workgroup walks a contiguous range of work items),
+            // so these loads are not prefetched.
             u32x4v tq[kTabLoads];
             float tdx[kDxLoads];
 #pragma unroll
@@ -689,14 +694,13 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(1))) void k
         const int row0 = u.tile * tile_rows + roff;
         const bool wave_ok = row0 < a.rows;
         tile_wait(tr);
+        // Both waves of a row tile have passed the previous unit's first
+        // epilogue barrier, after their last read of the image.
         if (wave_ok) {
-            tile_store<0>(img_lds, tr);
-            if (ngroups > 1) tile_store<1>(img_lds + 4096u, tr);
-            if (ngroups > 2) tile_store<2>(img_lds + 8192u, tr);
-            if (ngroups > 3) tile_store<3>(img_lds + 12288u, tr);
-            if (ngroups > 4) tile_store<4>(img_lds + 16384u, tr);
-            if (ngroups > 5) tile_store<5>(img_lds + 20480u, tr);
-            if (ngroups > 6) tile_store<6>(img_lds + 24576u, tr);
+            static_assert(kWaveGroups == 3, "stores below");
+            if (gmine > 0) tile_store<0>(img_lds, tr);
+            if (gmine > 1) tile_store<1>(img_lds + 4096u, tr);
+            if (gmine > 2) tile_store<2>(img_lds + 8192u, tr);
         }
         // The bias words arrived with the tile; take them now so no later
         // use waits on the next unit's loads.
@@ -709,71 +713,79 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(1))) void k
             if (ntab) npt = pass_tokens<MODE>(a, rt, cur);
             prefetch(cur);
         }
-        if (new_tab)
-            lds_barrier();
-        else
-            wave_lds_fence();
+        // the other wave's half of the image, and new tables, are in place
+        lds_barrier();
         if (n_staged == kStage) {
-            lds_barrier();  // every wave's staging is complete
             flush(n_staged);
             n_staged = 0;
         }
 
         const uint8_t *view_base = wbase + (uint64_t)u.e * a.expert_bytes;
+        bool special = false;
         {
             const uint32_t lead = (uint32_t)((reinterpret_cast<uintptr_t>(view_base) & 15u) + (uint32_t)row0 * row_bytes) & 15u;
             TileView tv = tile_view(img, lead + (uint32_t)L.i * row_bytes, L);
             auto segment = [&](auto gc) {
                 constexpr int G = decltype(gc)::value;
                 issue(gc);
-                if (G < 6 && wave_ok) {
+                if (wave_ok) {
                     if (npair == 2)
-                        tile_segment<2>(G, tv, nb, nch, L, PR, acc);
+                        tile_part<2>(G, half, tv, nb, nch, L, PR, acc);
                     else
-                        tile_segment<1>(G, tv, nb, nch, L, PR, acc);
+                        tile_part<1>(G, half, tv, nb, nch, L, PR, acc);
                 }
             };
-            static_assert(kTileGroups == 7, "segments below");
+            static_assert(kWaveGroups == 3, "segments below");
             segment(std::integral_constant<int, 0>{});
             segment(std::integral_constant<int, 1>{});
             segment(std::integral_constant<int, 2>{});
-            segment(std::integral_constant<int, 3>{});
-            segment(std::integral_constant<int, 4>{});
-            segment(std::integral_constant<int, 5>{});
-            segment(std::integral_constant<int, 6>{});
             special = wave_ok && tile_special(tv, row0 + L.i < a.rows);
         }
-        wave_lds_fence();
 
         // Sum the eight columns of each token slot (parts h/l x blocks).
 #pragma unroll
         for (int tp = 0; tp < 2; tp++)
 #pragma unroll
             for (int i = 0; i < 4; i++) acc[tp][i] = sum8(acc[tp][i]);
-        float(*res)[16][kTokPerPass] = s_res[w & 1];
+        const int par = w & 1;
         if ((c16 & 7) == 0) {
 #pragma unroll
             for (int tp = 0; tp < 2; tp++) {
                 const int t = 2 * tp + L.slot;
                 if (t < pt.nt) {
 #pragma unroll
-                    for (int i = 0; i < 4; i++) res[wave][4 * L.gb + i][t] = acc[tp][i];
+                    for (int i = 0; i < 4; i++) s_res[par][half][rt4][4 * L.gb + i][t] = acc[tp][i];
                 }
             }
         }
-        // Rows with special scales: recompute with the integer decode.
-        if (__any(special)) {
-            const ByteView cview = make_view(view_base, a.expert_bytes);
-            const int row_l = lane >> 2, sub = lane & 3;
-            const int row = row0 + row_l;
-            const uint32_t pos = (uint32_t)(row < a.rows ? row : 0) * row_bytes;
-            for (int t = 0; t < pt.nt; t++) {
-                const uint32_t *codes = reinterpret_cast<const uint32_t *>(a.codes + (size_t)pick4(pt.arow, t) * nb * 32);
-                const float v = lut_row_dot(cview, pos, nb, codes, s_dx + t * nbp, sub);
-                if (sub == 0) res[wave][row_l][t] = v;
-            }
-        }
+        const bool wsp = __any(special);
+        if (lane == 0) s_special[par][wave] = wsp ? 1 : 0;
         lds_barrier();
+        // Row tiles with special scales: the half-0 wave recomputes all 16
+        // rows with the integer decode (workgroup-uniform test, so the
+        // barrier after it is reached by every wave).
+        bool any_special = false;
+#pragma unroll
+        for (int i = 0; i < kWaves; i++) any_special |= s_special[par][i] != 0;
+        if (any_special) {
+            if (half == 0 && (s_special[par][rt4] | s_special[par][rt4 + 4])) {
+                const ByteView cview = make_view(view_base, a.expert_bytes);
+                const int row_l = lane >> 2, sub = lane & 3;
+                const int row = row0 + row_l;
+                const uint32_t pos = (uint32_t)(row < a.rows ? row : 0) * row_bytes;
+                for (int t = 0; t < pt.nt; t++) {
+                    const uint32_t *codes = reinterpret_cast<const uint32_t *>(a.codes + (size_t)pick4(pt.arow, t) * nb * 32);
+                    const float v = lut_row_dot(cview, pos, nb, codes, s_dx + t * nbp, sub);
+                    if (sub == 0) {
+                        s_res[par][0][rt4][row_l][t] = v;
+                        s_res[par][1][rt4][row_l][t] = 0.0f;
+                    }
+                }
+            }
+            lds_barrier();
+        }
+        float(*res0)[16][kTokPerPass] = s_res[par][0];
+        float(*res1)[16][kTokPerPass] = s_res[par][1];
         const uint32_t brow = (uint32_t)u.e * (uint32_t)a.rows + (uint32_t)(u.tile * tile_rows + erow);
         const int k = n_staged;
         if (tid == 0) {
@@ -787,8 +799,9 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(1))) void k
             if (wave < 2) {
                 const int t = tid >> 5;
                 const float b0 = bias_value(bv0, bw0, brow), b1 = bias_value(bv1, bw1, brow);
-                const float gv = res[erow >> 4][erow & 15][t] + b0;
-                const float uv = res[2 + (erow >> 4)][erow & 15][t] + b1;
+                const int rg = erow >> 4, ri = erow & 15;
+                const float gv = (res0[rg][ri][t] + res1[rg][ri][t]) + b0;
+                const float uv = (res0[2 + rg][ri][t] + res1[2 + rg][ri][t]) + b1;
                 const float v = swiglu(gv, uv);
                 uint16_t dh;
                 const int qv = q8_quantize_half(v, lane, &dh);
@@ -804,21 +817,22 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(1))) void k
                 }
             }
         } else {
-            const int t = tid >> 6;
-            const float b0 = bias_value(bv0, bw0, brow);
-            if (t < pt.nt) s_stage[k][0][t][erow] = res[erow >> 4][erow & 15][t] + b0;
+            if (wave < 4) {
+                const int t = tid >> 6;
+                const float b0 = bias_value(bv0, bw0, brow);
+                const int rg = erow >> 4, ri = erow & 15;
+                if (t < pt.nt) s_stage[k][0][t][erow] = (res0[rg][ri][t] + res1[rg][ri][t]) + b0;
+            }
         }
         ++n_staged;
 #pragma unroll
         for (int p = 0; p < 2; p++)
 #pragma unroll
             for (int i = 0; i < 4; i++) acc[p][i] = 0.0f;
-        special = false;
+        // the stage is complete before the next step's flush
+        if (n_staged == kStage || w + 1 == w1) lds_barrier();
     }
-    if (n_staged > 0) {
-        lds_barrier();
-        flush(n_staged);
-    }
+    if (n_staged > 0) flush(n_staged);
 }
 
 hipError_t launch_mx_mfma(hipStream_t s, GemvMode mode, const MxMfmaArgs &a, int slots) {
@@ -851,7 +865,7 @@ hipError_t launch_mx_mfma(hipStream_t s, GemvMode mode, const MxMfmaArgs &a, int
     const int tile_rows = mode == kGateUp ? 32 : 64;
     const int max_passes = mode == kRows ? (a.ntok + kTokPerPass - 1) / kTokPerPass : slots;
     const int64_t items = (int64_t)max_passes * ((a.rows + tile_rows - 1) / tile_rows);
-    // one workgroup of four waves per CU (its LDS holds four tile images)
+    // one workgroup of eight waves per CU (its LDS holds four tile images)
     const int grid = items < n_cu ? (int)items : n_cu;
     if (mode == kGateUp) {
         hipLaunchKernelGGL(k_mx_mfma<kGateUp>, dim3(grid), dim3(kWG), lds, s, a, a.active, a.offsets, a.pass_off,

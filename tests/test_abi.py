@@ -103,6 +103,18 @@ def test_moe_batch_validation(vctx, batch):
     assert _call_moe(vctx, cfg, lw, X, 64, OUT, 64, batch) == spt.ERR_INVALID
 
 
+def test_moe_input_dimension_limit(vctx):
+    """The grouped GEMV stages whole rows in LDS: MXFP4 input dimensions up to
+    2880 (GPT-OSS) are accepted, larger ones rejected before any launch."""
+    cfg, lw = _moe_descriptors(H=2880, D=64)
+    assert _call_moe(vctx, cfg, lw, X, 2 * 2880, OUT, 2 * 2880, 2) == spt.ERR_DEVICE
+    cfg, lw = _moe_descriptors(H=2912, D=64)
+    assert _call_moe(vctx, cfg, lw, X, 2 * 2912, OUT, 2 * 2912, 2) == spt.ERR_INVALID
+    assert b"exceeds the supported 2880" in spt.lib().spt_last_error()
+    cfg, lw = _moe_descriptors(H=32, D=2912)
+    assert _call_moe(vctx, cfg, lw, X, 64, OUT, 64, 2) == spt.ERR_INVALID
+
+
 def test_moe_nil_and_overlap(vctx):
     cfg, lw = _moe_descriptors()
     assert _call_moe(None, cfg, lw, X, 64, OUT, 64, 2) == spt.ERR_INVALID
