@@ -186,6 +186,12 @@ int validate_expert(const spt_tensor *t, int64_t input, int64_t output, int64_t 
     if (!t->data) return fail(SPT_ERR_INVALID, "\"%s\": tensor is not resident (nil data)", tname(t));
     if ((uint64_t)(input / 32 * 17) * (uint64_t)output > 0xFFFFFFF0ull)
         return fail(SPT_ERR_INVALID, "\"%s\": expert matrix larger than 4 GiB is not supported", tname(t));
+    return SPT_OK;
+}
+
+// The grouped GEMV stages whole weight rows in LDS (no counterpart in the
+// reference, whose CPU loops take any width).
+int validate_gemv_input(const spt_tensor *t, int64_t input) {
     if (input > spt::kMxMaxInput)
         return fail(SPT_ERR_INVALID, "\"%s\": MXFP4 input dimension %lld exceeds the supported %d", tname(t),
                     (long long)input, spt::kMxMaxInput);
@@ -242,6 +248,8 @@ int validate_moe(spt_ctx *ctx, const spt_moe_config *cfg, const spt_moe_layer *l
     if ((rc = validate_expert(&lw->ffn_gate_exps, h, d, E))) return rc;
     if ((rc = validate_expert(&lw->ffn_up_exps, h, d, E))) return rc;
     if ((rc = validate_expert(&lw->ffn_down_exps, d, h, E))) return rc;
+    if ((rc = validate_gemv_input(&lw->ffn_gate_exps, h))) return rc;
+    if ((rc = validate_gemv_input(&lw->ffn_down_exps, d))) return rc;
     if ((rc = validate_bias(&lw->ffn_gate_inp_bias, E, 1))) return rc;
     if ((rc = validate_bias(&lw->ffn_gate_exps_bias, d, E))) return rc;
     if ((rc = validate_bias(&lw->ffn_up_exps_bias, d, E))) return rc;
@@ -617,6 +625,7 @@ int spt_mul_mxfp4_expert(spt_ctx *ctx, const spt_tensor *w, const spt_tensor *bi
     if (w->n_dims != 3) return fail(SPT_ERR_INVALID, "\"%s\": expected MXFP4 expert tensor", tname(w));
     const int64_t in = (int64_t)w->shape[0], out = (int64_t)w->shape[1], E = (int64_t)w->shape[2];
     if ((rc = validate_expert(w, in, out, E))) return rc;
+    if ((rc = validate_gemv_input(w, in))) return rc;
     spt_tensor none{};
     if ((rc = validate_bias(bias ? bias : &none, out, E))) return rc;
     if (expert < 0 || expert >= E) return fail(SPT_ERR_INVALID, "expert %d out of range", expert);
