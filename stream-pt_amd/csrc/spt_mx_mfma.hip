@@ -259,23 +259,59 @@ __device__ inline bool tile_special(const TileView &v, bool row_ok) {
     return row_ok && (v.emin < (uint32_t)kEMin || v.emax > (uint32_t)kEMax);
 }
 
-// Four chunks: their LDS reads, then their MFMAs.
+// NC consecutive chunks from c0: all their LDS reads, then their A operands,
+// then all their MFMAs back to back, then the FMAs that apply d_x (in chunk
+// order per accumulator), so no FMA waits on the MFMA issued just before it.
+template <int NP, bool MASK, int NC>
+__device__ __attribute__((always_inline)) inline void chunk_run(TileView &v, int c0, int nb, const LaneRole &L,
+                                                                const PassRole &P, float acc[2][4]) {
+    ChunkRaw<NP> r[NC];
+#pragma unroll
+    for (int h = 0; h < NC; h++) chunk_fetch<NP>(r[h], v.pa, P, c0 + h);
+    v8i A[NC];
+    int sa[NC];
+#pragma unroll
+    for (int h = 0; h < NC; h++) {
+        const uint32_t ev = __builtin_amdgcn_ubfe(r[h].d[0], v.esh, 8u);
+        sa[h] = (int)ev;
+        if (MASK) {
+            const bool in = 4 * (c0 + h) + L.gb < nb;
+            sa[h] = in ? sa[h] : 127;
+            v.emin = in ? min(v.emin, ev) : v.emin;
+            v.emax = in ? max(v.emax, ev) : v.emax;
+        } else {
+            v.emin = min(v.emin, ev);
+            v.emax = max(v.emax, ev);
+        }
+        A[h] = v8i{(int)__builtin_amdgcn_perm(r[h].d[1], r[h].d[0], v.sel), (int)__builtin_amdgcn_perm(r[h].d[2], r[h].d[1], v.sel),
+                   (int)__builtin_amdgcn_perm(r[h].d[3], r[h].d[2], v.sel), (int)__builtin_amdgcn_perm(r[h].d[4], r[h].d[3], v.sel),
+                   0, 0, 0, 0};
+    }
+    v4f dd[NC][NP];
+#pragma unroll
+    for (int h = 0; h < NC; h++)
+#pragma unroll
+        for (int tp = 0; tp < NP; tp++) {
+            const v8i B = __builtin_bit_cast(v8i, __builtin_shufflevector(r[h].blo[tp], r[h].bhi[tp], 0, 1, 2, 3, 4, 5, 6, 7));
+            const v4f z = {0.0f, 0.0f, 0.0f, 0.0f};
+            dd[h][tp] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A[h], B, z, 4, 0, 0, sa[h], 0, L.sb);
+        }
+#pragma unroll
+    for (int h = 0; h < NC; h++)
+#pragma unroll
+        for (int tp = 0; tp < NP; tp++)
+#pragma unroll
+            for (int k = 0; k < 4; k++) acc[tp][k] = __builtin_fmaf(dd[h][tp][k], r[h].x[tp], acc[tp][k]);
+}
+
 template <int NP, bool MASK>
 __device__ __attribute__((always_inline)) inline void chunk_quad(TileView &v, int c0, int nb, const LaneRole &L, const PassRole &P, float acc[2][4]) {
-    ChunkRaw<NP> r[4];
-#pragma unroll
-    for (int h = 0; h < 4; h++) chunk_fetch<NP>(r[h], v.pa, P, c0 + h);
-#pragma unroll
-    for (int h = 0; h < 4; h++) chunk_mfma<NP, MASK>(r[h], c0 + h, nb, v.sel, v.esh, L, acc, v.emin, v.emax);
+    chunk_run<NP, MASK, 4>(v, c0, nb, L, P, acc);
 }
 
 template <int NP, bool MASK>
 __device__ __attribute__((always_inline)) inline void chunk_pair(TileView &v, int c0, int nb, const LaneRole &L, const PassRole &P, float acc[2][4]) {
-    ChunkRaw<NP> r[2];
-#pragma unroll
-    for (int h = 0; h < 2; h++) chunk_fetch<NP>(r[h], v.pa, P, c0 + h);
-#pragma unroll
-    for (int h = 0; h < 2; h++) chunk_mfma<NP, MASK>(r[h], c0 + h, nb, v.sel, v.esh, L, acc, v.emin, v.emax);
+    chunk_run<NP, MASK, 2>(v, c0, nb, L, P, acc);
 }
 
 // Part `part` (0..2) of the chunks of wave half h (the waves of a row tile
