@@ -268,6 +268,12 @@ __device__ __attribute__((always_inline)) inline void chunk_run(TileView &v, int
     ChunkRaw<NP> r[NC];
 #pragma unroll
     for (int h = 0; h < NC; h++) chunk_fetch<NP>(r[h], v.pa, P, c0 + h);
+    // d_x is first needed after the MFMAs; naming it here keeps its reads
+    // with the others, behind one wait, rather than late behind a second.
+#pragma unroll
+    for (int h = 0; h < NC; h++)
+#pragma unroll
+        for (int tp = 0; tp < NP; tp++) asm volatile("" : "+v"(r[h].x[tp]));
     v8i A[NC];
     int sa[NC];
 #pragma unroll
