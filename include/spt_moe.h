@@ -126,6 +126,14 @@ int spt_ctx_synchronize(struct spt_ctx *ctx);
 /* Register a host flag polled before each launch; NULL clears it. */
 int spt_ctx_set_cancel_flag(struct spt_ctx *ctx, const volatile int32_t *flag);
 
+/* Expert groups of at least min_group selections run through the grouped
+ * GEMM (bf16 MFMA, up to 64 selections per pass over the expert's weights);
+ * smaller groups through the grouped GEMV (4 per pass).  0 restores the
+ * default (9).  Results are the same either way within the fp32 tolerance
+ * (the per-block sums are exact on both).  No reference counterpart: the
+ * reference picks its CPU loop by tile size (forward/mxfp4_batch.go:55-95). */
+int spt_ctx_set_gemm_min_group(struct spt_ctx *ctx, int32_t min_group);
+
 /* Per-kernel timing with HIP events recorded on the context's stream around
  * each launch (measurement instrumentation, off by default).  Kernel kinds: */
 enum {
@@ -136,7 +144,9 @@ enum {
     SPT_KERNEL_COMBINE = 4,  /* weighted combine                              */
     SPT_KERNEL_Q40 = 5,      /* Q4_0 GEMV / small GEMM                        */
     SPT_KERNEL_SELECT = 6,   /* top-k + softmax + per-expert packing          */
-    SPT_KERNEL_KINDS = 7
+    SPT_KERNEL_GATE_UP_GEMM = 7, /* grouped gate/up GEMM (large groups)       */
+    SPT_KERNEL_DOWN_GEMM = 8,    /* grouped down GEMM (large groups)          */
+    SPT_KERNEL_KINDS = 9
 };
 int spt_ctx_enable_timing(struct spt_ctx *ctx, int enable);
 /* Synchronise, then write the summed milliseconds and launch counts of each

@@ -5,6 +5,7 @@
 // arena, and the launch sequences of the operators.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <climits>
 #include <cstdarg>
 #include <cstdio>
@@ -28,6 +29,7 @@ struct spt_ctx {
     std::vector<hipEvent_t> free_events;
     double total_ms[SPT_KERNEL_KINDS] = {};
     int64_t launches[SPT_KERNEL_KINDS] = {};
+    int32_t gemm_min_group = 0;  // 0: the default policy (gemm_min below)
 };
 
 namespace {
@@ -273,16 +275,29 @@ int copy_tap(spt_ctx *ctx, void *dst, const void *src, size_t bytes) {
     return SPT_OK;
 }
 
+// Smallest expert group that runs through the grouped GEMM: a group of this
+// many selections takes at least three passes of the grouped GEMV over the
+// expert's weights.
+constexpr int kGemmMinGroup = 9;
+
 int run_moe(spt_ctx *ctx, const spt_moe_layer *lw, const float *x, float *out, const MoEDims &m,
             const spt_moe_taps *taps) {
     const int64_t h = m.h, d = m.d, E = m.E, k = m.k, B = m.batch, n = B * k;
     const int64_t nbh = h / 32, nbd = d / 32;
+    // An expert's group holds at most n selections: with fewer than the
+    // threshold no expert can reach the GEMM, which is then not launched.
+    const int gemm_min = ctx->gemm_min_group > 0 ? ctx->gemm_min_group : kGemmMinGroup;
+    const bool use_gemm = n >= gemm_min;
     Carve c;
     size_t o_xc = c.take(B * h), o_xs = c.take(B * nbh * 4), o_xm = c.take(B * nbh * 64);
+    size_t o_xb = c.take(use_gemm ? B * nbh * 64 : 0);
     size_t o_logits = c.take(B * E * 4);
     size_t o_ids = c.take(n * 4), o_w = c.take(n * 4), o_cnt = c.take(E * 4), o_off = c.take((E + 1) * 4);
-    size_t o_list = c.take(n * 4), o_act_list = c.take(E * 4), o_na = c.take(4), o_pass = c.take((E + 1) * 4);
+    size_t o_list = c.take(n * 4), o_act_list = c.take(E * 4), o_na = c.take(4);
+    size_t o_gv = c.take(E * 4), o_gvn = c.take(4), o_gvp = c.take((E + 1) * 4);
+    size_t o_gm = c.take(E * 4), o_gmn = c.take(4), o_gmt = c.take((E + 1) * 4);
     size_t o_act = c.take(n * d * 4), o_ac = c.take(n * d), o_as = c.take(n * nbd * 4), o_am = c.take(n * nbd * 64);
+    size_t o_ab = c.take(use_gemm ? n * nbd * 64 : 0);
     size_t o_res = c.take(n * h * 4);
     char *S;
     int rc;
@@ -290,17 +305,30 @@ int run_moe(spt_ctx *ctx, const spt_moe_layer *lw, const float *x, float *out, c
     int8_t *xc = (int8_t *)(S + o_xc), *ac = (int8_t *)(S + o_ac);
     float *xs = (float *)(S + o_xs), *logits = (float *)(S + o_logits), *act = (float *)(S + o_act);
     uint8_t *xm = (uint8_t *)(S + o_xm), *am = (uint8_t *)(S + o_am);
+    uint32_t *xb = use_gemm ? (uint32_t *)(S + o_xb) : nullptr, *ab = use_gemm ? (uint32_t *)(S + o_ab) : nullptr;
     float *as = (float *)(S + o_as), *res = (float *)(S + o_res);
-    spt::SelectOut so{(int32_t *)(S + o_ids), (float *)(S + o_w), (int32_t *)(S + o_cnt),
-                      (int32_t *)(S + o_off), (int32_t *)(S + o_list), (int32_t *)(S + o_act_list),
-                      (int32_t *)(S + o_na), (int32_t *)(S + o_pass)};
+    spt::SelectOut so{};
+    so.ids = (int32_t *)(S + o_ids);
+    so.weights = (float *)(S + o_w);
+    so.counts = (int32_t *)(S + o_cnt);
+    so.offsets = (int32_t *)(S + o_off);
+    so.list = (int32_t *)(S + o_list);
+    so.active = (int32_t *)(S + o_act_list);
+    so.n_active = (int32_t *)(S + o_na);
+    so.gemm_min = use_gemm ? gemm_min : INT_MAX;
+    so.gv_active = (int32_t *)(S + o_gv);
+    so.gv_n = (int32_t *)(S + o_gvn);
+    so.gv_pass_off = (int32_t *)(S + o_gvp);
+    so.gm_active = (int32_t *)(S + o_gm);
+    so.gm_n = (int32_t *)(S + o_gmn);
+    so.gm_tile_off = (int32_t *)(S + o_gmt);
     hipStream_t s = ctx->stream;
 
-    const spt::QuantOut xq{xc, xs, xm, taps ? (uint8_t *)taps->xq : nullptr};
+    const spt::QuantOut xq{xc, xs, xm, taps ? (uint8_t *)taps->xq : nullptr, xb};
     if ((rc = check_cancel(ctx))) return rc;
     if (taps && taps->logits_in) {
         SPT_HIP(timed(ctx, SPT_KERNEL_QUANTIZE, [&] {
-            return spt::launch_quantize(s, x, B * nbh, xq.codes, xq.scales, nullptr, xq.mxtab, xq.blocks34);
+            return spt::launch_quantize(s, x, B * nbh, xq.codes, xq.scales, nullptr, xq.mxtab, xq.blocks34, xq.btab);
         }));
         SPT_HIP(timed(ctx, SPT_KERNEL_SELECT, [&] { return spt::launch_select(s, taps->logits_in, (int)B, (int)E, (int)k, so); }));
         if ((rc = copy_tap(ctx, taps->logits, taps->logits_in, B * E * 4))) return rc;
@@ -330,9 +358,9 @@ int run_moe(spt_ctx *ctx, const spt_moe_layer *lw, const float *x, float *out, c
     ga.mxtab = xm;
     ga.scales = xs;
     ga.codes = xc;
-    ga.active = so.active;
-    ga.n_active = so.n_active;
-    ga.pass_off = so.pass_off;
+    ga.active = so.gv_active;
+    ga.n_active = so.gv_n;
+    ga.pass_off = so.gv_pass_off;
     ga.offsets = so.offsets;
     ga.list = so.list;
     ga.topk = (int)k;
@@ -345,6 +373,44 @@ int run_moe(spt_ctx *ctx, const spt_moe_layer *lw, const float *x, float *out, c
     ga.act_blocks34 = taps ? (uint8_t *)taps->actq : nullptr;
     if ((rc = check_cancel(ctx))) return rc;
     SPT_HIP(timed(ctx, SPT_KERNEL_GATE_UP, [&] { return spt::launch_mx_mfma(s, spt::kGateUp, ga, slots); }));
+    // Upper bound of the GEMM work items (token tiles x row units): every
+    // GEMM expert holds at least gemm_min selections.
+    const int64_t gm_experts = use_gemm ? std::min<int64_t>(E, n / gemm_min) : 0;
+    const int64_t gm_tiles = gm_experts + (n + spt::kGemmTokens - 1) / spt::kGemmTokens;
+    spt::MxGemmArgs gg{};
+    if (use_gemm) {
+        gg.w[0] = ga.w[0];
+        gg.w[1] = ga.w[1];
+        gg.expert_bytes = ga.expert_bytes;
+        gg.rows = ga.rows;
+        gg.nb = ga.nb;
+        gg.bias[0] = ga.bias[0];
+        gg.bias[1] = ga.bias[1];
+        gg.bias_type[0] = ga.bias_type[0];
+        gg.bias_type[1] = ga.bias_type[1];
+        gg.btab = xb;
+        gg.scales = xs;
+        gg.codes = xc;
+        gg.gm_active = so.gm_active;
+        gg.gm_n = so.gm_n;
+        gg.gm_tile_off = so.gm_tile_off;
+        gg.offsets = so.offsets;
+        gg.list = so.list;
+        gg.topk = (int)k;
+        gg.out = ga.out;
+        gg.tap[0] = ga.tap[0];
+        gg.tap[1] = ga.tap[1];
+        gg.act_codes = ac;
+        gg.act_scales = as;
+        gg.act_mxtab = am;
+        gg.act_blocks34 = ga.act_blocks34;
+        gg.act_btab = ab;
+        const int64_t items = gm_tiles * ((d + 127) / 128);
+        if ((rc = check_cancel(ctx))) return rc;
+        SPT_HIP(timed(ctx, SPT_KERNEL_GATE_UP_GEMM, [&] {
+            return spt::launch_mx_gemm(s, spt::kGateUp, gg, (int)std::min<int64_t>(items, INT_MAX));
+        }));
+    }
     spt::MxMfmaArgs da{};
     da.w[0] = (const uint8_t *)lw->ffn_down_exps.data;
     da.expert_bytes = (uint64_t)nbd * 17 * h;
@@ -356,15 +422,39 @@ int run_moe(spt_ctx *ctx, const spt_moe_layer *lw, const float *x, float *out, c
     da.mxtab = am;
     da.scales = as;
     da.codes = ac;
-    da.active = so.active;
-    da.n_active = so.n_active;
-    da.pass_off = so.pass_off;
+    da.active = so.gv_active;
+    da.n_active = so.gv_n;
+    da.pass_off = so.gv_pass_off;
     da.offsets = so.offsets;
     da.list = so.list;
     da.topk = (int)k;
     da.out = res;
     if ((rc = check_cancel(ctx))) return rc;
     SPT_HIP(timed(ctx, SPT_KERNEL_DOWN, [&] { return spt::launch_mx_mfma(s, spt::kDown, da, slots); }));
+    if (use_gemm) {
+        spt::MxGemmArgs gd{};
+        gd.w[0] = da.w[0];
+        gd.expert_bytes = da.expert_bytes;
+        gd.rows = da.rows;
+        gd.nb = da.nb;
+        gd.bias[0] = da.bias[0];
+        gd.bias_type[0] = da.bias_type[0];
+        gd.btab = ab;
+        gd.scales = as;
+        gd.codes = ac;
+        gd.gm_active = so.gm_active;
+        gd.gm_n = so.gm_n;
+        gd.gm_tile_off = so.gm_tile_off;
+        gd.offsets = so.offsets;
+        gd.list = so.list;
+        gd.topk = (int)k;
+        gd.out = res;
+        const int64_t items = gm_tiles * ((h + 255) / 256);
+        if ((rc = check_cancel(ctx))) return rc;
+        SPT_HIP(timed(ctx, SPT_KERNEL_DOWN_GEMM, [&] {
+            return spt::launch_mx_gemm(s, spt::kDown, gd, (int)std::min<int64_t>(items, INT_MAX));
+        }));
+    }
     if ((rc = check_cancel(ctx))) return rc;
     SPT_HIP(timed(ctx, SPT_KERNEL_COMBINE, [&] { return spt::launch_combine(s, res, so.weights, (int)B, (int)k, (int)h, out); }));
     if (taps) {
@@ -394,7 +484,8 @@ int quantize_into_scratch(spt_ctx *ctx, const float *x, int64_t rows, int64_t nb
     *sumq = (int32_t *)(*S + o_q);
     if (mxtab) *mxtab = (uint8_t *)(*S + o_m);
     SPT_HIP(timed(ctx, SPT_KERNEL_QUANTIZE, [&] {
-        return spt::launch_quantize(ctx->stream, x, rows * nb, *codes, *scales, *sumq, mxtab ? *mxtab : nullptr, nullptr);
+        return spt::launch_quantize(ctx->stream, x, rows * nb, *codes, *scales, *sumq, mxtab ? *mxtab : nullptr, nullptr,
+                                    nullptr);
     }));
     return SPT_OK;
 }
@@ -497,6 +588,14 @@ int spt_ctx_synchronize(spt_ctx *ctx) {
     return SPT_OK;
 }
 
+int spt_ctx_set_gemm_min_group(spt_ctx *ctx, int32_t min_group) {
+    int rc;
+    if ((rc = check_ctx(ctx))) return rc;
+    if (min_group < 0) return fail(SPT_ERR_INVALID, "negative GEMM group threshold %d", (int)min_group);
+    ctx->gemm_min_group = min_group;
+    return SPT_OK;
+}
+
 int spt_ctx_set_cancel_flag(spt_ctx *ctx, const volatile int32_t *flag) {
     int rc;
     if ((rc = check_ctx(ctx))) return rc;
@@ -568,7 +667,8 @@ int spt_quantize_q8_0(spt_ctx *ctx, const float *x_dev, int64_t n, void *out_dev
     if (ranges_overlap(x_dev, (uint64_t)n * 4, out_dev, (uint64_t)n / 32 * 34))
         return fail(SPT_ERR_INVALID, "input and output must not overlap");
     if ((rc = check_device(ctx)) || (rc = check_cancel(ctx))) return rc;
-    SPT_HIP(spt::launch_quantize(ctx->stream, x_dev, n / 32, nullptr, nullptr, nullptr, nullptr, (uint8_t *)out_dev));
+    SPT_HIP(spt::launch_quantize(ctx->stream, x_dev, n / 32, nullptr, nullptr, nullptr, nullptr, (uint8_t *)out_dev,
+                                 nullptr));
     return SPT_OK;
 }
 

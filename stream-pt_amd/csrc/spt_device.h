@@ -258,8 +258,16 @@ __device__ inline uint32_t e4m3_small(int v) {
 //                                 order (position p <-> element (p>>1) +
 //                                 16*(p&1)): h digits at [0,32), l at [32,64)
 //   blocks34: u8  [blk][34]      GGML Q8_0 block
+//   btab   : u32 [blk][16]       bf16 codes for the bf16 MFMA, dword j =
+//                                 bf16(q[j]) | bf16(q[j+16]) << 16 (the
+//                                 MXFP4 nibble order of bytes 1+j)
+__device__ inline uint32_t bf16_code_pair(int lo, int hi) {
+    return (__float_as_uint((float)lo) >> 16) | (__float_as_uint((float)hi) & 0xFFFF0000u);
+}
+
 __device__ inline void write_q8_block(const uint32_t w[8], uint16_t dh, size_t blk, int8_t *codes,
-                                      float *scales, uint8_t *mxtab, uint8_t *blocks34) {
+                                      float *scales, uint8_t *mxtab, uint8_t *blocks34,
+                                      uint32_t *btab = nullptr) {
     if (codes) {
         uint32_t *c = reinterpret_cast<uint32_t *>(codes + blk * 32);
 #pragma unroll
@@ -297,6 +305,15 @@ __device__ inline void write_q8_block(const uint32_t w[8], uint16_t dh, size_t b
 #pragma unroll
             for (int i = 0; i < 4; i++) o[2 + 4 * k + i] = (uint8_t)(w[k] >> (8 * i));
     }
+    if (btab) {
+        uint32_t *o = btab + blk * 16;
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            const int lo = (int)(int8_t)(w[j >> 2] >> (8 * (j & 3)));
+            const int hi = (int)(int8_t)(w[4 + (j >> 2)] >> (8 * (j & 3)));
+            o[j] = bf16_code_pair(lo, hi);
+        }
+    }
 }
 
 // The same rule with one element per lane (lanes 0..31 of a wavefront hold
@@ -323,8 +340,12 @@ __device__ inline int q8_quantize_lane(float v, int lane, uint16_t *dbits) {
 // Lane i (< 32) of a wavefront stores element i of Q8_0 block `blk` (code q)
 // into every requested layout of write_q8_block; lane 0 also stores the scale.
 __device__ inline void write_q8_lane(int q, uint16_t dh, int lane, size_t blk, int8_t *codes,
-                                     float *scales, uint8_t *mxtab, uint8_t *blocks34) {
+                                     float *scales, uint8_t *mxtab, uint8_t *blocks34,
+                                     uint32_t *btab = nullptr) {
     if (lane >= 32) return;
+    if (btab)
+        reinterpret_cast<uint16_t *>(btab + blk * 16)[2 * (lane & 15) + (lane >> 4)] =
+            (uint16_t)(__float_as_uint((float)q) >> 16);
     if (codes) codes[blk * 32 + lane] = (int8_t)q;
     if (scales && lane == 0) scales[blk] = f16_bits_to_f32(dh);
     if (mxtab) {

@@ -11,6 +11,8 @@ constexpr int kMaxExperts = 256;
 constexpr int kMaxSelections = 4096;
 // Tokens of an expert's list per pass of the grouped GEMV over its weights.
 constexpr int kGemvTokens = 4;
+// List entries per work item of the grouped GEMM (spt_mx_gemm.hip).
+constexpr int kGemmTokens = 64;
 // Largest MXFP4 input dimension of the grouped GEMV: a workgroup stages four
 // 16-row tiles of whole rows in LDS (GPT-OSS uses 2880 for both projections).
 constexpr int kMxMaxInput = 2880;
@@ -23,7 +25,15 @@ struct SelectOut {
     int32_t *list;
     int32_t *active;
     int32_t *n_active;
-    int32_t *pass_off;  // [E+1] prefix over active experts of ceil(count / kGemvTokens)
+    // Experts with count >= gemm_min go to the grouped GEMM, the others to
+    // the grouped GEMV, each with its own packed expert list:
+    int32_t gemm_min;
+    int32_t *gv_active;    // [E] GEMV experts, ascending
+    int32_t *gv_n;
+    int32_t *gv_pass_off;  // [E+1] prefix over GEMV experts of ceil(count / kGemvTokens)
+    int32_t *gm_active;    // [E] GEMM experts, ascending
+    int32_t *gm_n;
+    int32_t *gm_tile_off;  // [E+1] prefix over GEMM experts of ceil(count / kGemmTokens)
 };
 
 // Optional Q8_0 outputs of a quantized activation (see write_q8_block).
@@ -32,6 +42,7 @@ struct QuantOut {
     float *scales;
     uint8_t *mxtab;
     uint8_t *blocks34;
+    uint32_t *btab;
 };
 
 enum GemvMode { kGateUp = 0, kDown = 1, kRows = 2 };
@@ -70,6 +81,36 @@ struct MxMfmaArgs {
     uint8_t *act_blocks34;
 };
 
+// Grouped MXFP4 x Q8_0 GEMM on the bf16 MFMA (spt_mx_gemm.hip) for the
+// experts of the GEMM list (SelectOut.gm_*): the kGateUp and kDown
+// semantics of MxMfmaArgs, with the activations read as bf16 code tables
+// (write_q8_block's btab layout) and the gate/up epilogue also writing the
+// btab table of act.
+struct MxGemmArgs {
+    const uint8_t *w[2];
+    uint64_t expert_bytes;
+    int rows;
+    int nb;
+    const void *bias[2];
+    int bias_type[2];
+    const uint32_t *btab;    // activation bf16 code tables [*][nb][16 dwords]
+    const float *scales;     // activation Q8_0 scales [*][nb]
+    const int8_t *codes;     // activation Q8_0 codes [*][nb*32] (special-scale rows)
+    const int32_t *gm_active;
+    const int32_t *gm_n;
+    const int32_t *gm_tile_off;
+    const int32_t *offsets;
+    const int32_t *list;
+    int topk;
+    float *out;
+    float *tap[2];
+    int8_t *act_codes;
+    float *act_scales;
+    uint8_t *act_mxtab;
+    uint8_t *act_blocks34;
+    uint32_t *act_btab;
+};
+
 struct Q40Args {
     const uint8_t *w;
     uint64_t nbytes;
@@ -83,7 +124,8 @@ struct Q40Args {
 };
 
 hipError_t launch_quantize(hipStream_t s, const float *x, int64_t nblocks, int8_t *codes,
-                           float *scales, int32_t *sumq, uint8_t *mxtab, uint8_t *blocks34);
+                           float *scales, int32_t *sumq, uint8_t *mxtab, uint8_t *blocks34,
+                           uint32_t *btab);
 // Router logits [batch][experts]; Q8_0 of x into q when q.codes or q.blocks34 is set.
 hipError_t launch_route(hipStream_t s, const float *router, const void *bias, int bias_type,
                         const float *x, int batch, int hidden, int experts, float *logits,
@@ -93,6 +135,8 @@ hipError_t launch_select(hipStream_t s, const float *logits, int batch, int expe
                          const SelectOut &o);
 // slots: upper bound of the active experts (1 for kRows).
 hipError_t launch_mx_mfma(hipStream_t s, GemvMode mode, const MxMfmaArgs &a, int slots);
+// max_items: upper bound of the GEMM work items (0: nothing to launch).
+hipError_t launch_mx_gemm(hipStream_t s, GemvMode mode, const MxGemmArgs &a, int max_items);
 hipError_t launch_q40_gemv(hipStream_t s, const Q40Args &a);
 hipError_t launch_combine(hipStream_t s, const float *results, const float *weights, int batch,
                           int topk, int hidden, float *out);

@@ -22,7 +22,8 @@ __global__ __launch_bounds__(kWG) void k_quantize(const float *__restrict__ x, i
                                                   float *__restrict__ scales,
                                                   int32_t *__restrict__ sumq,
                                                   uint8_t *__restrict__ mxtab,
-                                                  uint8_t *__restrict__ blocks34) {
+                                                  uint8_t *__restrict__ blocks34,
+                                                  uint32_t *__restrict__ btab) {
     int64_t b = (int64_t)blockIdx.x * kWG + threadIdx.x;
     if (b >= nblocks) return;
     float v[32];
@@ -31,7 +32,7 @@ __global__ __launch_bounds__(kWG) void k_quantize(const float *__restrict__ x, i
     uint32_t w[8];
     uint16_t dh;
     q8_quantize32(v, w, &dh);
-    write_q8_block(w, dh, (size_t)b, codes, scales, mxtab, blocks34);
+    write_q8_block(w, dh, (size_t)b, codes, scales, mxtab, blocks34, btab);
     if (sumq) {
         int32_t s = 0;
 #pragma unroll
@@ -41,10 +42,11 @@ __global__ __launch_bounds__(kWG) void k_quantize(const float *__restrict__ x, i
 }
 
 hipError_t launch_quantize(hipStream_t s, const float *x, int64_t nblocks, int8_t *codes,
-                           float *scales, int32_t *sumq, uint8_t *mxtab, uint8_t *blocks34) {
+                           float *scales, int32_t *sumq, uint8_t *mxtab, uint8_t *blocks34,
+                           uint32_t *btab) {
     if (nblocks <= 0) return hipSuccess;
     dim3 grid((unsigned)((nblocks + kWG - 1) / kWG));
-    hipLaunchKernelGGL(k_quantize, grid, dim3(kWG), 0, s, x, nblocks, codes, scales, sumq, mxtab, blocks34);
+    hipLaunchKernelGGL(k_quantize, grid, dim3(kWG), 0, s, x, nblocks, codes, scales, sumq, mxtab, blocks34, btab);
     return hipGetLastError();
 }
 
@@ -162,42 +164,59 @@ __device__ void pack_lists(int n, int E, const SelectOut &o, const int32_t *s_id
         if (!(s_w[i] <= 0.0f)) atomicAdd(&s_cnt[s_ids[i]], 1);
     __syncthreads();
     if (tid < 64) {
-        // offsets (scan of counts), the active list and the pass prefix
-        // (scan of ceil(count / kGemvTokens) in active order)
-        int pos = 0, na = 0, npass = 0;
+        // offsets (scan of counts), the active list, and the GEMV and GEMM
+        // expert lists with their prefixes (passes of kGemvTokens, tiles of
+        // kGemmTokens) in ascending expert order
+        int pos = 0, na = 0, nv = 0, nm = 0, npass = 0, ntile = 0;
+        const uint64_t below = (1ull << tid) - 1ull;
         for (int e0 = 0; e0 < E; e0 += 64) {
             const int e = e0 + tid;
             const int c = e < E ? s_cnt[e] : 0;
-            const int np = (c + kGemvTokens - 1) / kGemvTokens;
-            int incl = c, pincl = np;
+            const bool big = c > 0 && c >= o.gemm_min;
+            const int np = big ? 0 : (c + kGemvTokens - 1) / kGemvTokens;
+            const int ntl = big ? (c + kGemmTokens - 1) / kGemmTokens : 0;
+            int incl = c, pincl = np, tincl = ntl;
 #pragma unroll
             for (int d = 1; d < 64; d <<= 1) {
-                const int up = __shfl_up(incl, d), pup = __shfl_up(pincl, d);
+                const int up = __shfl_up(incl, d), pup = __shfl_up(pincl, d), tup = __shfl_up(tincl, d);
                 if (tid >= d) {
                     incl += up;
                     pincl += pup;
+                    tincl += tup;
                 }
             }
-            const uint64_t act = __ballot(c > 0);
-            const int arank = __builtin_popcountll(act & ((1ull << tid) - 1ull));
+            const uint64_t act = __ballot(c > 0), actv = __ballot(c > 0 && !big), actm = __ballot(big);
             if (e < E) {
                 s_off[e] = pos + incl - c;
                 o.offsets[e] = pos + incl - c;
                 o.counts[e] = c;
-                if (c > 0) {
-                    o.active[na + arank] = e;
-                    o.pass_off[na + arank] = npass + pincl - np;
+                if (c > 0) o.active[na + __builtin_popcountll(act & below)] = e;
+                if (c > 0 && !big) {
+                    const int r = nv + __builtin_popcountll(actv & below);
+                    o.gv_active[r] = e;
+                    o.gv_pass_off[r] = npass + pincl - np;
+                }
+                if (big) {
+                    const int r = nm + __builtin_popcountll(actm & below);
+                    o.gm_active[r] = e;
+                    o.gm_tile_off[r] = ntile + tincl - ntl;
                 }
             }
             pos += __shfl(incl, 63);
             npass += __shfl(pincl, 63);
+            ntile += __shfl(tincl, 63);
             na += __builtin_popcountll(act);
+            nv += __builtin_popcountll(actv);
+            nm += __builtin_popcountll(actm);
         }
         if (tid == 0) {
             s_off[E] = pos;
             o.offsets[E] = pos;
             *o.n_active = na;
-            o.pass_off[na] = npass;
+            *o.gv_n = nv;
+            o.gv_pass_off[nv] = npass;
+            *o.gm_n = nm;
+            o.gm_tile_off[nm] = ntile;
         }
     }
     for (int p0 = 0; p0 < n; p0 += kSelChunk) {
@@ -250,7 +269,7 @@ __global__ __launch_bounds__(kWG) void k_route(const float *__restrict__ router,
             uint32_t w[8];
             uint16_t dh;
             q8_quantize32(v, w, &dh);
-            write_q8_block(w, dh, (size_t)t * (H / 32) + b, q.codes, q.scales, q.mxtab, q.blocks34);
+            write_q8_block(w, dh, (size_t)t * (H / 32) + b, q.codes, q.scales, q.mxtab, q.blocks34, q.btab);
         }
     }
     if (e >= E) return;

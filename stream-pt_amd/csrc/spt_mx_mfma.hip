@@ -17,10 +17,12 @@
 // value as the integer form isum * 2^(e-128) (isum = sum of 2*E2M1*q).  The
 // activation scale d_x is applied per block with one FMA:
 //   acc = fma(D_h + D_l, d_x, acc)  ==  fma(float(isum), d_x * 2^(e-128), acc).
-// Rows of a 16-row tile that contain an E8M0 outside [4, 254] (the +Inf
-// scale 255, or scales whose products could leave the normal fp32 range) are
-// computed with the integer LUT decode instead, so the results keep the
-// reference's special-value semantics.
+// Rows of a 16-row tile that contain an E8M0 outside [4, 240] are computed
+// with the integer LUT decode instead, so the results keep the reference's
+// special-value semantics: 255 is the +Inf scale, and above 240 a D value
+// (up to 2^(e-127) * 16 * 32 * 6 * 8 = 2^(e-112.4)) can overflow fp32 where
+// the oracle's d_x * 2^(e-128) * isum stays finite; below 4 the smallest
+// products (2^(e-128)) leave the normal range.
 #include <type_traits>
 
 #include "spt_device.h"
@@ -36,7 +38,7 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 constexpr int kWaves = 8;
 constexpr int kWG = 64 * kWaves;
 constexpr int kTokPerPass = kGemvTokens;  // two MFMA token slots x two MFMAs per chunk
-constexpr int kEMin = 4, kEMax = 254;
+constexpr int kEMin = 4, kEMax = 240;
 
 // Integer-decode dot of one row (16 lanes of 64 cooperate: 4 lanes per row,
 // used for the rare tiles with special E8M0 scales).
@@ -252,7 +254,7 @@ __device__ __attribute__((always_inline)) inline TileView tile_view(const uint8_
     return v;
 }
 
-// A special E8M0 (outside [4, 254]) in the tile's valid blocks: the tile's
+// A special E8M0 (outside [4, 240]) in the tile's valid blocks: the tile's
 // rows are then recomputed with the integer decode, so the MFMA results of
 // such a tile are unused.
 __device__ inline bool tile_special(const TileView &v, bool row_ok) {

@@ -29,9 +29,9 @@ EXPORTED = (
     "spt_mul_q40_batch_into_host", "spt_mul_mxfp4_expert", "spt_route_moe_batch",
     "spt_forward_moe", "spt_forward_moe_batch", "spt_forward_moe_batch_ex",
     "spt_forward_moe_batch_host", "spt_block_sums", "spt_synth_mxfp4",
-    "spt_ctx_enable_timing", "spt_ctx_read_timing",
+    "spt_ctx_enable_timing", "spt_ctx_read_timing", "spt_ctx_set_gemm_min_group",
 )
-KERNEL_KINDS = ("quantize", "route", "gate_up", "down", "combine", "q40", "select")
+KERNEL_KINDS = ("quantize", "route", "gate_up", "down", "combine", "q40", "select", "gate_up_gemm", "down_gemm")
 
 
 class SptError(RuntimeError):
@@ -99,6 +99,7 @@ def lib():
         "spt_ctx_destroy": ([vp], C.c_int),
         "spt_ctx_synchronize": ([vp], C.c_int),
         "spt_ctx_set_cancel_flag": ([vp, vp], C.c_int),
+        "spt_ctx_set_gemm_min_group": ([vp, i32], C.c_int),
         "spt_alloc": ([vp, u64, C.POINTER(vp)], C.c_int),
         "spt_free": ([vp, vp], C.c_int),
         "spt_copy_h2d": ([vp, vp, vp, u64], C.c_int),
@@ -198,6 +199,11 @@ class Context:
         n = (C.c_int64 * len(KERNEL_KINDS))()
         _check(lib().spt_ctx_read_timing(self.handle, ms, n))
         return {k: (ms[i], n[i]) for i, k in enumerate(KERNEL_KINDS)}
+
+    def set_gemm_min_group(self, min_group: int):
+        """Expert groups of at least min_group selections use the grouped
+        GEMM, smaller ones the grouped GEMV; 0 restores the default."""
+        _check(lib().spt_ctx_set_gemm_min_group(self.handle, int(min_group)))
 
     def set_cancel_flag(self, flag_array):
         """flag_array: a host int32 numpy array of one element, or None."""

@@ -169,3 +169,12 @@ def test_quantize_validation(vctx):
     assert L.spt_quantize_q8_0(vctx.handle, X, 33, OUT) == spt.ERR_INVALID
     assert L.spt_quantize_q8_0(vctx.handle, X, 64, X + 4) == spt.ERR_INVALID
     assert L.spt_quantize_q8_0(vctx.handle, X, 64, OUT) == spt.ERR_DEVICE
+
+
+def test_gemm_min_group_setting(vctx):
+    L = spt.lib()
+    assert L.spt_ctx_set_gemm_min_group(vctx.handle, -1) == spt.ERR_INVALID
+    assert b"negative" in L.spt_last_error()
+    for v in (0, 1, 9, 1 << 30):
+        assert L.spt_ctx_set_gemm_min_group(vctx.handle, v) == spt.OK
+    assert L.spt_ctx_set_gemm_min_group(None, 1) == spt.ERR_INVALID

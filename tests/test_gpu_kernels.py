@@ -230,7 +230,7 @@ def test_mxfp4_all_scales(gpu_ctx, O):
     """TestMXFP4AllScales (mxfp4_optimization_test.go:52-78) through the Q8_0
     path: one block per row, every E8M0 exponent, nibbles 0x22 (1.0),
     x = 1/32; exponent 255 with zero nibbles must give NaN.  Row tiles
-    holding exponents outside [4, 254] take the integer-decode fallback."""
+    holding exponents outside [4, 240] take the integer-decode fallback."""
     import math
 
     import torch
@@ -255,3 +255,33 @@ def test_mxfp4_all_scales(gpu_ctx, O):
     assert np.isnan(got[256]) and np.isinf(got[255])
     ref = np.array([math.ldexp(1, s - 127) for s in range(255)], np.float64)
     assert np.all(np.abs(got[:255] - ref) <= 1e-3 * ref), "closed form 2^(s-127)"
+
+
+def test_mxfp4_large_scales_stay_finite(gpu_ctx, O):
+    """One 16-row tile with exponents 239..254 and the largest Q8_0 codes
+    (nibbles 0x22, x = 1/32, so q = 127 everywhere): the result 2^(e-127)
+    is finite for every row, although the unscaled block sums times
+    2^(e-127) exceed the fp32 range for e above 240."""
+    import math
+
+    import torch
+
+    import spt
+
+    rows = 16
+    data = np.zeros((rows, 17), np.uint8)
+    data[:, 0] = np.arange(239, 255)
+    data[:, 1:] = 0x22
+    data = data.reshape(-1)
+    x = np.full(32, 1.0 / 32, np.float32)
+    wd, xd = _dev(data), _dev(x)
+    y = torch.zeros(rows, dtype=torch.float32, device="cuda")
+    t = spt.Tensor.make("w", spt.TYPE_MXFP4, [32, rows, 1], wd.data_ptr(), data.size)
+    gpu_ctx.mul_mxfp4_expert(t, None, 0, xd, y, 1)
+    torch.cuda.synchronize()
+    got = y.cpu().numpy()
+    want = O.mul_mxfp4_q8(data, _q8_of(O, x), None, 32, rows)
+    assert np.all(np.isfinite(want)) and np.all(np.isfinite(got)), got
+    assert_close(got, want, what="large scales vs Q8_0 oracle")
+    ref = np.array([math.ldexp(1, s - 127) for s in range(239, 255)], np.float64)
+    assert np.all(np.abs(got - ref) <= 1e-3 * ref), "closed form 2^(s-127)"

@@ -74,8 +74,27 @@ def _bias_vec(lay, name, e, dim, O):
     return np.array([O.fp16_to_f32(int(h)) for h in seg], np.float32)
 
 
-def check_stagewise(O, lay, x, B, g, logits_in=None):
-    """Check every GPU stage against the oracle fed the GPU's inputs."""
+# Expert-group thresholds of the grouped GEMM: every group through the GEMM,
+# every group through the GEMV, or the library's default split.
+PATHS = {"default": 0, "gemm": 1, "gemv": 1 << 30}
+
+
+class gemm_path:
+    """Context manager: run a block with one of PATHS, then restore."""
+
+    def __init__(self, ctx, path):
+        self.ctx, self.path = ctx, path
+
+    def __enter__(self):
+        self.ctx.set_gemm_min_group(PATHS[self.path])
+
+    def __exit__(self, *exc):
+        self.ctx.set_gemm_min_group(0)
+
+
+def check_stagewise(O, lay, x, B, g, logits_in=None, sample=None):
+    """Check every GPU stage against the oracle fed the GPU's inputs (the
+    per-selection projections on `sample` only, if given)."""
     H, D, E, k = lay["hidden"], lay["expert_dim"], lay["experts"], lay["topk"]
     n = B * k
     nbh, nbd = H // 32, D // 32
@@ -98,6 +117,8 @@ def check_stagewise(O, lay, x, B, g, logits_in=None):
     assert np.array_equal(g["list"][:offsets[-1]], lst), "per-expert packing"
     assert g["n_active"][0] == active.size and np.array_equal(g["active"][:active.size], active)
     valid = [i for i in range(n) if not (g["weights"][i] <= 0)]
+    if sample is not None:
+        valid = [i for i in valid if i in set(sample)]
     xq = g["xq"].reshape(B, nbh * 34)
     gate, up = g["gate"].reshape(n, D), g["up"].reshape(n, D)
     act, actq, res = g["act"].reshape(n, D), g["actq"].reshape(n, nbd * 34), g["results"].reshape(n, H)
@@ -148,10 +169,12 @@ def test_moe_decode_gpt_oss_layer(gpu_ctx, O):
           f"vs fp32-activation reference {np.max(np.abs(g['out'] - ref)) / np.max(np.abs(ref)):.2e}")
 
 
+@pytest.mark.parametrize("path", ["default", "gemv"])
 @pytest.mark.parametrize("batch", [32])
-def test_moe_prefill_zipf(gpu_ctx, O, batch):
+def test_moe_prefill_zipf(gpu_ctx, O, batch, path):
     """32 positions per weight pass, router logits injected so expert
-    popularity follows Zipf(1.1): ragged groups of 0..32 rows."""
+    popularity follows Zipf(1.1): ragged groups of 0..32 rows (by default the
+    groups of 9 or more through the grouped GEMM)."""
     from spt import synth
     from spt import workloads as W
 
@@ -159,22 +182,81 @@ def test_moe_prefill_zipf(gpu_ctx, O, batch):
     dl = W.device_layer(gpu_ctx, seed=2, layer=0, shp=shp)
     x = W.x_tokens(2, 0, batch, shp.hidden)
     logits = synth.zipf_logits(synth.stream_key(2, 99), batch, shp.experts, 1.1)
-    g = _run(gpu_ctx, dl.config, dl.layer, x, batch, logits_in=logits)
+    with gemm_path(gpu_ctx, path):
+        g = _run(gpu_ctx, dl.config, dl.layer, x, batch, logits_in=logits)
+    counts = g["counts"]
+    print(f"groups: {np.count_nonzero(counts)} experts, largest {counts.max()}, "
+          f">= 9: {np.count_nonzero(counts >= 9)}")
     lay = W.host_layer(2, 0, shp, experts=np.unique(g["ids"]))
     check_stagewise(O, lay, x, batch, g, logits_in=logits)
 
 
+def test_moe_prefill_hot_expert(gpu_ctx, O):
+    """512 tokens, 25% of them forced to one hot expert and the rest Zipf(1.1)
+    (the long-prompt chunk): groups from 1 to hundreds of rows.  Routing,
+    packing, the Q8_0 stages and the combine are checked on every selection;
+    the projections on a sample holding the hot expert's first and last list
+    tiles and random others."""
+    from spt import synth
+    from spt import workloads as W
+
+    batch = 512
+    shp = W.MoEShape()
+    dl = W.device_layer(gpu_ctx, seed=4, layer=0, shp=shp)
+    x = W.x_tokens(4, 0, batch, shp.hidden)
+    logits = synth.zipf_logits(synth.stream_key(4, 99), batch, shp.experts, 1.1, hot_fraction=0.25, hot_expert=17)
+    g = _run(gpu_ctx, dl.config, dl.layer, x, batch, logits_in=logits)
+    counts, offsets, lst = g["counts"], g["offsets"], g["list"]
+    assert counts[17] >= 128
+    hot = lst[offsets[17]:offsets[18]]
+    rng = np.random.default_rng(4)
+    sample = set(hot[:3].tolist()) | set(hot[60:68].tolist()) | set(hot[-3:].tolist())
+    sample |= set(rng.choice(batch * shp.topk, 24, replace=False).tolist())
+    ids_needed = np.unique(g["ids"][sorted(sample)])
+    lay = W.host_layer(4, 0, shp, experts=ids_needed)
+    check_stagewise(O, lay, x, batch, g, logits_in=logits, sample=sorted(sample))
+
+
+@pytest.mark.parametrize("path", ["default", "gemm", "gemv"])
 @pytest.mark.parametrize("experts,topk", [(1, 1), (4, 2), (7, 7), (8, 2)])
 @pytest.mark.parametrize("bias_type", [-1, 0, 1, 30])
 @pytest.mark.parametrize("mode", ROUTER_MODES)
-def test_moe_reference_fixture(gpu_ctx, O, experts, topk, bias_type, mode):
+def test_moe_reference_fixture(gpu_ctx, O, experts, topk, bias_type, mode, path):
     """moeBatchFixture (hidden 96, expert dim 64) in every router mode, bias
-    type and batch of the reference's batch==sequential test."""
+    type and batch of the reference's batch==sequential test, through the
+    grouped GEMM, the grouped GEMV and the default split."""
     lay = moe_batch_fixture(96, 64, experts, topk, bias_type, mode)
     keep, cfg, lw = device_moe_layer(lay)
-    for batch in (1, 5, 37):
-        x = moe_batch_x(batch, 96, mode)
-        g = _run(gpu_ctx, cfg, lw, x, batch)
-        check_stagewise(O, lay, x, batch, g)
-        want = O.forward_moe_batch(lay, x, batch, q8=True)
-        assert_close(g["out"], want, what=f"{mode} batch {batch}")
+    with gemm_path(gpu_ctx, path):
+        for batch in (1, 5, 37):
+            x = moe_batch_x(batch, 96, mode)
+            g = _run(gpu_ctx, cfg, lw, x, batch)
+            check_stagewise(O, lay, x, batch, g)
+            want = O.forward_moe_batch(lay, x, batch, q8=True)
+            assert_close(g["out"], want, what=f"{mode} batch {batch}")
+
+
+@pytest.mark.parametrize("path", ["gemm", "gemv"])
+@pytest.mark.parametrize("scale", [0, 2, 241, 248, 254, 255])
+def test_moe_special_scales(gpu_ctx, O, scale, path):
+    """moeBatchFixture (hidden 320, expert dim 256: several K segments and row
+    units) with one weight row of each matrix of every expert holding an
+    E8M0 outside the MFMA's exact range in one block (0 and 2: tiny scales;
+    241..254: block sums whose 2^(e-127) scaling overflows fp32 although
+    the result does not; 255: the +Inf scale).  Those rows take the
+    integer-decode fallback; every stage must match the oracle, NaN and Inf
+    positions included."""
+    lay = moe_batch_fixture(320, 256, 4, 2, 0, "normal")
+    for name, rows, nin in (("gate", 256, 320), ("up", 256, 320), ("down", 320, 256)):
+        w = lay[name].reshape(4, rows, nin // 32, 17).copy()
+        w[:, 37, 5, 0] = scale
+        w[:, rows - 1, nin // 32 - 1, 0] = scale
+        lay[name] = w.reshape(-1)
+    keep, cfg, lw = device_moe_layer(lay)
+    with gemm_path(gpu_ctx, path):
+        for batch in (5, 40):
+            x = moe_batch_x(batch, 320, "normal") / 64
+            g = _run(gpu_ctx, cfg, lw, x, batch)
+            check_stagewise(O, lay, x, batch, g)
+            want = O.forward_moe_batch(lay, x, batch, q8=True)
+            assert_close(g["out"], want, what=f"scale {scale} batch {batch}")
