@@ -129,9 +129,11 @@ int spt_ctx_set_cancel_flag(struct spt_ctx *ctx, const volatile int32_t *flag);
 /* Expert groups of at least min_group selections run through the grouped
  * GEMM (bf16 MFMA, up to 64 selections per pass over the expert's weights);
  * smaller groups through the grouped GEMV (4 per pass).  0 restores the
- * default (9).  Results are the same either way within the fp32 tolerance
- * (the per-block sums are exact on both).  No reference counterpart: the
- * reference picks its CPU loop by tile size (forward/mxfp4_batch.go:55-95). */
+ * default policy: groups of 9 or more when the batch holds at least 1024
+ * selections and those groups' GEMM work fills the device.  Results are the
+ * same either way within the fp32 tolerance (the per-block sums are exact on
+ * both).  No reference counterpart: the reference picks its CPU loop by tile
+ * size (forward/mxfp4_batch.go:55-95). */
 int spt_ctx_set_gemm_min_group(struct spt_ctx *ctx, int32_t min_group);
 
 /* Per-kernel timing with HIP events recorded on the context's stream around

@@ -29,7 +29,8 @@ struct spt_ctx {
     std::vector<hipEvent_t> free_events;
     double total_ms[SPT_KERNEL_KINDS] = {};
     int64_t launches[SPT_KERNEL_KINDS] = {};
-    int32_t gemm_min_group = 0;  // 0: the default policy (gemm_min below)
+    int32_t gemm_min_group = 0;  // 0: the default policy (kGemmMinGroup)
+    int n_cu = 0;                // compute units of the device
 };
 
 namespace {
@@ -275,10 +276,14 @@ int copy_tap(spt_ctx *ctx, void *dst, const void *src, size_t bytes) {
     return SPT_OK;
 }
 
-// Smallest expert group that runs through the grouped GEMM: a group of this
-// many selections takes at least three passes of the grouped GEMV over the
-// expert's weights.
+// Default policy for the grouped GEMM (measured on MI355X with GPT-OSS
+// shapes): groups of at least kGemmMinGroup selections (three or more GEMV
+// passes over the expert's weights) go to the GEMM when the batch holds at
+// least kGemmMinSelections selections and their work items fill the device;
+// below that the GEMV's passes are faster (a GEMM item walks the whole input
+// dimension serially, so a few large groups leave most CUs idle).
 constexpr int kGemmMinGroup = 9;
+constexpr int kGemmMinSelections = 1024;
 
 int run_moe(spt_ctx *ctx, const spt_moe_layer *lw, const float *x, float *out, const MoEDims &m,
             const spt_moe_taps *taps) {
@@ -286,8 +291,11 @@ int run_moe(spt_ctx *ctx, const spt_moe_layer *lw, const float *x, float *out, c
     const int64_t nbh = h / 32, nbd = d / 32;
     // An expert's group holds at most n selections: with fewer than the
     // threshold no expert can reach the GEMM, which is then not launched.
-    const int gemm_min = ctx->gemm_min_group > 0 ? ctx->gemm_min_group : kGemmMinGroup;
-    const bool use_gemm = n >= gemm_min;
+    // An explicit threshold (spt_ctx_set_gemm_min_group) applies as given;
+    // the default also needs kGemmMinSelections and a full device of items.
+    const bool forced = ctx->gemm_min_group > 0;
+    const int gemm_min = forced ? ctx->gemm_min_group : kGemmMinGroup;
+    const bool use_gemm = n >= gemm_min && (forced || n >= kGemmMinSelections);
     Carve c;
     size_t o_xc = c.take(B * h), o_xs = c.take(B * nbh * 4), o_xm = c.take(B * nbh * 64);
     size_t o_xb = c.take(use_gemm ? B * nbh * 64 : 0);
@@ -316,6 +324,8 @@ int run_moe(spt_ctx *ctx, const spt_moe_layer *lw, const float *x, float *out, c
     so.active = (int32_t *)(S + o_act_list);
     so.n_active = (int32_t *)(S + o_na);
     so.gemm_min = use_gemm ? gemm_min : INT_MAX;
+    so.gemm_units = (int32_t)((d + 127) / 128);
+    so.gemm_min_items = forced ? 0 : ctx->n_cu;
     so.gv_active = (int32_t *)(S + o_gv);
     so.gv_n = (int32_t *)(S + o_gvn);
     so.gv_pass_off = (int32_t *)(S + o_gvp);
@@ -389,6 +399,7 @@ int run_moe(spt_ctx *ctx, const spt_moe_layer *lw, const float *x, float *out, c
         gg.bias_type[0] = ga.bias_type[0];
         gg.bias_type[1] = ga.bias_type[1];
         gg.btab = xb;
+        gg.tab_rows = B;
         gg.scales = xs;
         gg.codes = xc;
         gg.gm_active = so.gm_active;
@@ -402,7 +413,7 @@ int run_moe(spt_ctx *ctx, const spt_moe_layer *lw, const float *x, float *out, c
         gg.tap[1] = ga.tap[1];
         gg.act_codes = ac;
         gg.act_scales = as;
-        gg.act_mxtab = am;
+        gg.act_mxtab = nullptr;  // read only by the GEMV's down pass
         gg.act_blocks34 = ga.act_blocks34;
         gg.act_btab = ab;
         const int64_t items = gm_tiles * ((d + 127) / 128);
@@ -440,6 +451,7 @@ int run_moe(spt_ctx *ctx, const spt_moe_layer *lw, const float *x, float *out, c
         gd.bias[0] = da.bias[0];
         gd.bias_type[0] = da.bias_type[0];
         gd.btab = ab;
+        gd.tab_rows = n;
         gd.scales = as;
         gd.codes = ac;
         gd.gm_active = so.gm_active;
@@ -529,6 +541,9 @@ int spt_ctx_create(int device, void *hip_stream, spt_ctx **out) {
             return hip_fail(err, "hipSetDevice");
         }
         ctx->stream = (hipStream_t)hip_stream;  // NULL: the device's default stream
+        if (hipDeviceGetAttribute(&ctx->n_cu, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess ||
+            ctx->n_cu <= 0)
+            ctx->n_cu = 256;
     }
     *out = ctx;
     return SPT_OK;

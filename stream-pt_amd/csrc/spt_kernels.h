@@ -28,6 +28,11 @@ struct SelectOut {
     // Experts with count >= gemm_min go to the grouped GEMM, the others to
     // the grouped GEMV, each with its own packed expert list:
     int32_t gemm_min;
+    // ...provided their GEMM work items (token tiles x gemm_units row units)
+    // number at least gemm_min_items (enough to fill the device); otherwise
+    // every expert goes to the GEMV.
+    int32_t gemm_units;
+    int32_t gemm_min_items;
     int32_t *gv_active;    // [E] GEMV experts, ascending
     int32_t *gv_n;
     int32_t *gv_pass_off;  // [E+1] prefix over GEMV experts of ceil(count / kGemvTokens)
@@ -93,7 +98,8 @@ struct MxGemmArgs {
     int nb;
     const void *bias[2];
     int bias_type[2];
-    const uint32_t *btab;    // activation bf16 code tables [*][nb][16 dwords]
+    const uint32_t *btab;    // activation bf16 code tables [tab_rows][nb][16 dwords]
+    int64_t tab_rows;        // rows of btab, scales and codes
     const float *scales;     // activation Q8_0 scales [*][nb]
     const int8_t *codes;     // activation Q8_0 codes [*][nb*32] (special-scale rows)
     const int32_t *gm_active;

@@ -169,10 +169,20 @@ __device__ void pack_lists(int n, int E, const SelectOut &o, const int32_t *s_id
         // kGemmTokens) in ascending expert order
         int pos = 0, na = 0, nv = 0, nm = 0, npass = 0, ntile = 0;
         const uint64_t below = (1ull << tid) - 1ull;
+        // GEMM work items the threshold would give
+        int tiles = 0;
+        for (int e0 = 0; e0 < E; e0 += 64) {
+            const int c = e0 + tid < E ? s_cnt[e0 + tid] : 0;
+            int t = (c > 0 && c >= o.gemm_min) ? (c + kGemmTokens - 1) / kGemmTokens : 0;
+#pragma unroll
+            for (int d = 32; d >= 1; d >>= 1) t += __shfl_xor(t, d);
+            tiles += t;
+        }
+        const bool gemm_on = (int64_t)tiles * o.gemm_units >= (int64_t)o.gemm_min_items;
         for (int e0 = 0; e0 < E; e0 += 64) {
             const int e = e0 + tid;
             const int c = e < E ? s_cnt[e] : 0;
-            const bool big = c > 0 && c >= o.gemm_min;
+            const bool big = gemm_on && c > 0 && c >= o.gemm_min;
             const int np = big ? 0 : (c + kGemvTokens - 1) / kGemvTokens;
             const int ntl = big ? (c + kGemmTokens - 1) / kGemmTokens : 0;
             int incl = c, pincl = np, tincl = ntl;

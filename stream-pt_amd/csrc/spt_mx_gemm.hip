@@ -26,6 +26,8 @@
 // MFMA lane layout (measured on the hardware): lane l holds A row l%16 and B
 // column l%16 at k = 8*(l/16) + 0..7; D lane l, register r is row
 // 4*(l/16) + r, column l%16.
+#include <type_traits>
+
 #include "spt_device.h"
 #include "spt_kernels.h"
 
@@ -36,41 +38,37 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kBM = 256;               // weight rows per work item (gate/up: 128 gate + 128 up)
 constexpr int kBN = kGemmTokens;       // list entries per work item
-constexpr int kSeg = 6;                // 32-element blocks per K segment
-constexpr int kAPieces = 8;            // 16-byte loads per row and segment
-constexpr int kARow = 144;             // LDS bytes per staged row (36 dwords: rows spread over banks)
-constexpr int kBTok = kSeg * 64 + 16;  // LDS bytes per staged token (100 dwords)
-constexpr int kOffE = kBM * kARow;      // E8M0 bytes [row][8]
-constexpr int kOffB = kOffE + kBM * 8;  // bf16 code tables [token][block][64 B]
-constexpr int kOffD = kOffB + kBN * kBTok;  // d_x [token][8]
-constexpr int kStageBytes = kOffD + kBN * 8 * 4;
+constexpr int kSeg = 4;                // 32-element blocks per K segment (68 bytes of a row)
+constexpr int kStages = 3;             // LDS stages; two segments are in flight while one is multiplied
+// A stage: row r's window (the segment's bytes from the 16-byte boundary at
+// or below its first byte, 6 x 16 bytes) in the first 6 of the row's 8 slots
+// of 16 bytes.  (16-byte aligned loads: a load crossing the end of the
+// descriptor's range would read zeros for all its bytes.)
+constexpr int kAPieces = 6;
+constexpr int kASlots = 8;
+constexpr int kARow = 16 * kASlots;
+// B stage: per entry 16 slots of 16 bytes (4 blocks x 4 quarters of the bf16
+// code table); quarter piece p of entry t sits in slot p ^ (t & 15), so the
+// 16 entries of an MFMA fragment read 16 different bank groups.
+constexpr int kOffB = kBM * kARow;
+constexpr int kOffD = kOffB + kBN * kSeg * 64;  // d_x [entry][kSeg]
+constexpr int kStageBytes = kOffD + kBN * kSeg * 4;
 constexpr int kEMin = 4, kEMax = 240;
-// After the K loop the stage buffers hold the special-row values (per wave
-// 2 x 16 rows x 64 tokens) and the gate/up exchange ([token][128 rows]).
-constexpr int kFixBytes = kWaves * 2 * 16 * kBN * 4;
-constexpr int kXTok = 128 * 4 + 16;
-static_assert(kSeg * kMxBlock + 15 <= 16 * kAPieces, "a row's segment fits its loads");
-static_assert(16 * kAPieces <= kARow, "row stride");
-static_assert(kFixBytes + kBN * kXTok <= 2 * kStageBytes, "epilogue areas");
-static_assert(kBM * kAPieces % kThreads == 0 && kBN * kSeg * 4 % kThreads == 0, "stage loads");
-constexpr int kALoads = kBM * kAPieces / kThreads;  // 4
-constexpr int kBLoads = kBN * kSeg * 4 / kThreads;  // 3
+constexpr uint32_t kOOR = 0x80000000u;  // buffer offset past every range: reads zero
+static_assert(kSeg * kMxBlock + 15 <= 16 * kAPieces && kAPieces <= kASlots, "A window");
+static_assert(kBM * kASlots % kThreads == 0 && kBN * kSeg * 4 % kThreads == 0, "stage loads");
+static_assert(kBN * kSeg == 32 * kWaves, "one d_x load of 32 lanes per wave");
+constexpr int kALoads = kBM * kASlots / kThreads;  // 4
+constexpr int kBLoads = kBN * kSeg * 4 / kThreads;  // 2
+// DMA loads per wave and stage (the wait counts below rely on it)
+constexpr int kStageLoads = kALoads + kBLoads + 1;
+static_assert(kStageLoads == 7, "s_waitcnt vmcnt(7) below");
 
-__device__ inline rsrc_t expert_rsrc(const uint8_t *w, uint64_t expert_bytes, int e, uint32_t *le) {
-    // from the 16-byte boundary at or below the matrix's first byte to the
-    // one at or above its end (a 16-byte load crossing the range's end reads
-    // zeros; the bytes up to that boundary share the last byte's page)
-    const uintptr_t mb = reinterpret_cast<uintptr_t>(w + (uint64_t)e * expert_bytes);
-    *le = (uint32_t)(mb & 15u);
-    return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void *>(mb - *le), (short)0,
-                                             (int)(uint32_t)((expert_bytes + *le + 15u) & ~15ull), kRsrcWord3);
-}
 
 // Integer-decode dot of one weight row with one entry's Q8_0 row (the
 // special-scale fallback).
@@ -91,24 +89,174 @@ __device__ float lut_dot(const ByteView &v, uint32_t row_pos, int nb, const int8
     return acc;
 }
 
+typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+
+// Descriptor of expert e's matrix from the 16-byte boundary at or below its
+// first byte to the one at or above its end (a 16-byte load crossing the
+// range's end reads zeros; the bytes up to that boundary share the last
+// byte's page); *le = the matrix's offset in its first 16 bytes.
+__device__ inline u32x4v expert_rsrc(const uint8_t *w, uint64_t expert_bytes, int e, uint32_t *le) {
+    const uintptr_t mb = reinterpret_cast<uintptr_t>(w + (uint64_t)e * expert_bytes);
+    *le = (uint32_t)(mb & 15u);
+    const uint64_t b = mb - *le;
+    return u32x4v{(uint32_t)b, (uint32_t)(b >> 32) & 0xFFFFu, (uint32_t)((expert_bytes + *le + 15u) & ~15ull),
+                  (uint32_t)kRsrcWord3};
+}
+
+// LDS DMA load (buffer -> LDS, no registers): lane l's `bytes` land at LDS
+// address lds + bytes * l.  Issued with inline assembly so that the
+// compiler, which cannot tell which stage an LDS read touches, does not
+// wait for every load in flight before each LDS read; the kernel waits for
+// them itself (s_waitcnt vmcnt in stage order, then a barrier).  Five wait
+// states open each load: M0, the descriptor and the offset may have just
+// been written (by SALU, or by VALU for SGPRs), which an LDS DMA must not see
+// early, and the compiler cannot pad inside inline assembly.
+__device__ inline void dma16(const u32x4v &rs, uint32_t lds, uint32_t voff, uint32_t soff) {
+    asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(rs), "s"(soff), "{m0}"(lds)
+                 : "memory");
+}
+__device__ inline void dma4(const u32x4v &rs, uint32_t lds, uint32_t voff, uint32_t soff) {
+    asm volatile("s_nop 4\n\tbuffer_load_dword %0, %1, %2 offen lds" ::"v"(voff), "s"(rs), "s"(soff), "{m0}"(lds)
+                 : "memory");
+}
+
+__device__ inline u32x4v rsrc_words(const void *base, uint32_t nbytes) {
+    const uint64_t b = reinterpret_cast<uint64_t>(base);
+    return u32x4v{(uint32_t)b, (uint32_t)(b >> 32) & 0xFFFFu, nbytes, (uint32_t)kRsrcWord3};
+}
+
+// Workgroup barrier that leaves the LDS DMA loads in flight: the caller has
+// already waited for what it needs (s_waitcnt in inline assembly, out of
+// sight of the compiler's own wait insertion).
+__device__ inline void stage_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// Four bytes of the stage at byte offset o (any alignment): two aligned
+// dwords and a byte shift (an unaligned LDS dword read returns the same
+// bytes but is far slower).
+__device__ __attribute__((always_inline)) inline uint32_t nibble_word(const uint8_t *st, uint32_t o) {
+    const uint32_t *pw = reinterpret_cast<const uint32_t *>(st + (o & ~3u));
+    return __builtin_amdgcn_alignbyte(pw[1], pw[0], o & 3u);
+}
+
+// One full segment (kSeg blocks) with NTF token fragments, straight-line:
+// the A bytes of all blocks first, the B fragments and d_x one block ahead,
+// then per block its A decode, MFMAs and the FMAs that apply d_x (the two
+// waves of a SIMD overlap one's FMAs with the other's MFMAs).
+template <int NTF>
+__device__ __attribute__((always_inline)) inline void seg_full(const uint8_t *st, const uint32_t (&a_img)[2],
+                                                               const uint32_t (&b_lane)[kSeg], int g, int i16,
+                                                               float (&acc)[2][4][4], uint32_t (&emin)[2],
+                                                               uint32_t (&emax)[2]) {
+    uint32_t eb[kSeg][2], w4[kSeg][2];
+#pragma unroll
+    for (int j = 0; j < kSeg; j++)
+#pragma unroll
+        for (int rf = 0; rf < 2; rf++) {
+            eb[j][rf] = st[a_img[rf] + 17 * j];
+            w4[j][rf] = nibble_word(st, a_img[rf] + 17u * (uint32_t)j + 1u + 4u * (uint32_t)g);
+        }
+    bf16x8 Bv[2][NTF];
+    float dx[2][NTF];
+    auto load_b = [&](int j) {
+#pragma unroll
+        for (int tf = 0; tf < NTF; tf++) {
+            Bv[j & 1][tf] = *reinterpret_cast<const bf16x8 *>(st + kOffB + tf * (16 * kSeg * 64) + b_lane[j]);
+            dx[j & 1][tf] = *reinterpret_cast<const float *>(st + kOffD + ((16 * tf + i16) * kSeg + j) * 4);
+        }
+    };
+    load_b(0);
+#pragma unroll
+    for (int j = 0; j < kSeg; j++) {
+        if (j + 1 < kSeg) load_b(j + 1);
+        v4f D[2][NTF];
+#pragma unroll
+        for (int rf = 0; rf < 2; rf++) {
+            const float sc = __uint_as_float(eb[j][rf] << 23);
+            u32x4 av;
+            av.x = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w4[j][rf], sc, 0));
+            av.y = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w4[j][rf], sc, 1));
+            av.z = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w4[j][rf], sc, 2));
+            av.w = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w4[j][rf], sc, 3));
+            const bf16x8 A = __builtin_bit_cast(bf16x8, av);
+#pragma unroll
+            for (int tf = 0; tf < NTF; tf++)
+                D[rf][tf] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, Bv[j & 1][tf], v4f{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+        }
+#pragma unroll
+        for (int rf = 0; rf < 2; rf++)
+#pragma unroll
+            for (int tf = 0; tf < NTF; tf++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) acc[rf][tf][r] = __builtin_fmaf(D[rf][tf][r], dx[j & 1][tf], acc[rf][tf][r]);
+    }
+#pragma unroll
+    for (int rf = 0; rf < 2; rf++) {
+        emin[rf] = min(emin[rf], min(min(eb[0][rf], eb[1][rf]), min(eb[2][rf], eb[3][rf])));
+        emax[rf] = max(emax[rf], max(max(eb[0][rf], eb[1][rf]), max(eb[2][rf], eb[3][rf])));
+    }
+}
+static_assert(kSeg == 4, "seg_full's exponent reduction");
+
+// The last segment when it holds jn < kSeg blocks.
+template <int NTF>
+__device__ __attribute__((always_inline)) inline void seg_part(const uint8_t *st, const uint32_t (&a_img)[2],
+                                                               const uint32_t (&b_lane)[kSeg], int g, int i16, int jn,
+                                                               float (&acc)[2][4][4], uint32_t (&emin)[2],
+                                                               uint32_t (&emax)[2]) {
+    for (int j = 0; j < jn; j++) {
+        bf16x8 A[2];
+#pragma unroll
+        for (int rf = 0; rf < 2; rf++) {
+            const uint32_t eb = st[a_img[rf] + 17 * j];
+            const uint32_t w4 = nibble_word(st, a_img[rf] + 17u * (uint32_t)j + 1u + 4u * (uint32_t)g);
+            emin[rf] = min(emin[rf], eb);
+            emax[rf] = max(emax[rf], eb);
+            const float sc = __uint_as_float(eb << 23);
+            u32x4 av;
+            av.x = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w4, sc, 0));
+            av.y = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w4, sc, 1));
+            av.z = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w4, sc, 2));
+            av.w = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w4, sc, 3));
+            A[rf] = __builtin_bit_cast(bf16x8, av);
+        }
+#pragma unroll
+        for (int tf = 0; tf < NTF; tf++) {
+            const uint32_t bl = (uint32_t)i16 * (kSeg * 64) + 16u * (uint32_t)((4 * j + g) ^ i16);
+            const bf16x8 B = *reinterpret_cast<const bf16x8 *>(st + kOffB + tf * (16 * kSeg * 64) + bl);
+            const float dx = *reinterpret_cast<const float *>(st + kOffD + ((16 * tf + i16) * kSeg + j) * 4);
+#pragma unroll
+            for (int rf = 0; rf < 2; rf++) {
+                const v4f D = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[rf], B, v4f{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 4; r++) acc[rf][tf][r] = __builtin_fmaf(D[r], dx, acc[rf][tf][r]);
+            }
+        }
+    }
+}
+
 }  // namespace
 
 // Persistent workgroups of eight waves.  Work items are (GEMM expert, unit of
 // output rows, tile of 64 list entries), ordered so the token tiles of one
 // unit are consecutive (they share the unit's weight rows through the
 // caches); workgroup b takes items b, b + G, b + 2G, ...  Gate/up units are
-// 128 output rows (weight rows 0-127 of the item gate, 128-255 up, so the
-// SwiGLU and the Q8_0 of act stay in the workgroup); down units are 256 rows.
-// Wave w multiplies weight rows 32w .. 32w+31 of the item with all 64
-// entries: 2 x 4 MFMA tiles per block.
+// 128 output rows: weight rows 0-127 of the item are gate rows, 128-255 the
+// up rows of the same outputs, and wave w multiplies gate and up rows
+// 16w .. 16w+15, so the SwiGLU is local to the wave; the Q8_0 block of act
+// (32 rows) spans waves 2b and 2b+1.  Down units are 256 rows, wave w rows
+// 32w .. 32w+31.  Every wave takes all 64 entries: 2 x 4 MFMA tiles per block.
 //
-// The K loop runs over segments of kSeg blocks with two LDS stages: while a
-// segment is multiplied, the next one's loads are in flight in registers;
-// they are written to the other stage after the multiply, then one barrier.
+// The K loop runs over segments of kSeg blocks through kStages LDS stages
+// filled by LDS DMA loads (global/buffer -> LDS, no registers): segment s+2
+// is loaded while segment s is multiplied.
 template <int MODE>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void k_mx_gemm(MxGemmArgs a) {
     extern __shared__ __align__(16) uint8_t lds[];
-    __shared__ int s_spec[kBM];  // item tag where the row has a special E8M0
+    __shared__ float s_amax[kWaves][kBN];  // gate/up: per wave and entry, |act| max of its 16 rows (-1: NaN)
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -119,14 +267,22 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
     const int n_slots = *a.gm_n;
     const int total = n_slots > 0 ? a.gm_tile_off[n_slots] * units : 0;
     if ((int)blockIdx.x >= total) return;
-    for (int i = tid; i < kBM; i += kThreads) s_spec[i] = 0;
-    __syncthreads();
 
     const int i16 = lane & 15, g = lane >> 4;
     const int nseg = (nb + kSeg - 1) / kSeg;
-    int tag = 0;
+    // activation tables through buffer descriptors (the per-stage advance is
+    // a scalar offset)
+    const u32x4v rs_b = rsrc_words(a.btab, (uint32_t)(a.tab_rows * (uint64_t)nb * 64u));
+    const u32x4v rs_d = rsrc_words(a.scales, (uint32_t)(a.tab_rows * (uint64_t)nb * 4u));
+    // thread-constant part of the A loads: the piece of the row window
+    const int a_pc = tid & 7;
+    const bool a_pc_ok = a_pc < kAPieces;
+    // per lane: B slot offsets of quarter g of block j for this lane's entry
+    uint32_t b_lane[kSeg];
+#pragma unroll
+    for (int j = 0; j < kSeg; j++) b_lane[j] = (uint32_t)i16 * (kSeg * 64) + 16u * (uint32_t)((4 * j + g) ^ i16);
+
     for (int it = blockIdx.x; it < total; it += gridDim.x) {
-        ++tag;
         // item -> (slot, unit, token tile)
         int lo = 0, hi = n_slots - 1;
         while (lo < hi) {
@@ -143,112 +299,75 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
         const int e = a.gm_active[slot];
         const int begin = a.offsets[e] + tt * kBN;
         const int nt = min(kBN, a.offsets[e + 1] - begin);
+        const int ntf = (nt + 15) >> 4;  // token fragments holding entries
 
-        // weight rows of this item: LDS row r (0..255) -> matrix m, row
         uint32_t le0 = 0, le1 = 0;
-        const rsrc_t rs0 = expert_rsrc(a.w[0], a.expert_bytes, e, &le0);
-        const rsrc_t rs1 = MODE == kGateUp ? expert_rsrc(a.w[1], a.expert_bytes, e, &le1) : rs0;
+        const u32x4v rs0 = expert_rsrc(a.w[0], a.expert_bytes, e, &le0);
+        const u32x4v rs1 = MODE == kGateUp ? expert_rsrc(a.w[1], a.expert_bytes, e, &le1) : rs0;
         if (MODE != kGateUp) le1 = le0;
+        // LDS row r -> matrix row
         auto mrow = [&](int r) { return MODE == kGateUp ? u * (kBM / 2) + (r & (kBM / 2 - 1)) : u * kBM + r; };
 
-        // this thread's stage loads: A pieces k (rows tid/8 + 64k), B pieces,
-        // d_x entry; entries past nt read nothing
+        // this thread's DMA loads: A slots (rows tid/8 + 64k), B slots
+        // (entry (tid + 512k)/16), d_x (entry (32*wave + lane)/4)
         uint32_t a_pos[kALoads];
         bool a_ok[kALoads];
 #pragma unroll
         for (int k = 0; k < kALoads; k++) {
-            const int p = tid + kThreads * k, r = p >> 3;
+            const int r = (tid >> 3) + 64 * k;
             const int row = mrow(r);
-            a_ok[k] = row < a.rows;
-            a_pos[k] = ((k < kALoads / 2 || MODE != kGateUp) ? le0 : le1) + (uint32_t)(a_ok[k] ? row : 0) * row_bytes;
+            a_ok[k] = row < a.rows && a_pc_ok;
+            a_pos[k] = ((MODE == kGateUp && k >= kALoads / 2) ? le1 : le0) + (uint32_t)(row < a.rows ? row : 0) * row_bytes;
         }
-        int64_t b_row[kBLoads];
+        uint32_t b_off[kBLoads];
 #pragma unroll
         for (int k = 0; k < kBLoads; k++) {
-            const int t = (tid + kThreads * k) / (kSeg * 4);
-            int ar = -1;
+            const int q = tid + kThreads * k, t = q >> 4, piece = (q & 15) ^ (t & 15);
+            int ar = 0;  // entries past nt load row 0 (unused)
             if (t < nt) {
                 const int ent = a.list[begin + t];
                 ar = MODE == kGateUp ? ent / a.topk : ent;
             }
-            b_row[k] = ar < 0 ? -1 : (int64_t)ar * nb;
+            b_off[k] = ((uint32_t)ar * (uint32_t)nb + (uint32_t)(piece >> 2)) * 64u + 16u * (uint32_t)(piece & 3);
         }
-        int64_t d_row = -1;
-        if (tid < kBN * kSeg) {
-            const int t = tid / kSeg;
+        uint32_t d_off = 0;
+        {
+            const int idx = 32 * wave + (lane & 31), t = idx / kSeg, j = idx % kSeg;
+            int ar = 0;
             if (t < nt) {
                 const int ent = a.list[begin + t];
-                d_row = (int64_t)(MODE == kGateUp ? ent / a.topk : ent) * nb;
+                ar = MODE == kGateUp ? ent / a.topk : ent;
             }
+            d_off = ((uint32_t)ar * (uint32_t)nb + (uint32_t)j) * 4u;
         }
-
-        u32x4 ra[kALoads], rb[kBLoads];
-        float rd = 0.0f;
-        auto stage_load = [&](int s) {
-            const int b0 = s * kSeg;
+        typedef __attribute__((address_space(3))) uint8_t lds_u8;
+        const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>((lds_u8 *)lds);
+        // seven DMA loads per wave and stage (A x4, B x2, d_x x1)
+        auto issue = [&](int s) {
+            const uint32_t st = lds0 + (uint32_t)(s % kStages) * kStageBytes;
 #pragma unroll
-            for (int k = 0; k < kALoads; k++) {
-                const int pc = tid & 7;
-                const uint32_t off = ((a_pos[k] + (uint32_t)b0 * kMxBlock) & ~15u) + 16u * pc;
-                const rsrc_t rs = (k < kALoads / 2 || MODE != kGateUp) ? rs0 : rs1;
-                ra[k] = a_ok[k] ? __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0))
-                                : u32x4{0u, 0u, 0u, 0u};
-            }
+            for (int k = 0; k < kALoads; k++)
+                dma16((MODE == kGateUp && k >= kALoads / 2) ? rs1 : rs0, st + 16u * (64 * wave + kThreads * k),
+                      a_ok[k] ? ((a_pos[k] + 68u * (uint32_t)s) & ~15u) + 16u * (uint32_t)a_pc : kOOR, 0u);
 #pragma unroll
-            for (int k = 0; k < kBLoads; k++) {
-                const int q = (tid + kThreads * k) % (kSeg * 4), j = q >> 2, sub = q & 3;
-                u32x4 v = {0u, 0u, 0u, 0u};
-                if (b_row[k] >= 0 && b0 + j < nb)
-                    v = *reinterpret_cast<const u32x4 *>(a.btab + ((size_t)(b_row[k] + b0 + j) * 16 + 4 * sub));
-                rb[k] = v;
-            }
-            rd = 0.0f;
-            if (d_row >= 0) {
-                const int j = tid % kSeg;
-                if (b0 + j < nb) rd = a.scales[d_row + b0 + j];
-            }
-        };
-        auto stage_store = [&](int s) {
-            uint8_t *st = lds + (size_t)(s & 1) * kStageBytes;
-            const int b0 = s * kSeg;
-            const int jn = min(kSeg, nb - b0);
-#pragma unroll
-            for (int k = 0; k < kALoads; k++) {
-                const int p = tid + kThreads * k, r = p >> 3, pc = p & 7;
-                *reinterpret_cast<u32x4 *>(st + r * kARow + 16 * pc) = ra[k];
-                // the E8M0 byte of block j sits at lead + 17j of the row's
-                // window; at most one falls in each 16-byte piece
-                const int lead = (int)((a_pos[k] + (uint32_t)b0 * kMxBlock) & 15u);
-                const int num = 16 * pc - lead;
-                const int j = num <= 0 ? 0 : (num + 16) / 17;
-                const int pos = lead + 17 * j - 16 * pc;
-                if (pos < 16 && j < jn) {
-                    const uint32_t w = pos < 4 ? ra[k].x : pos < 8 ? ra[k].y : pos < 12 ? ra[k].z : ra[k].w;
-                    const uint32_t ev = (w >> (8 * (pos & 3))) & 0xFFu;
-                    st[kOffE + r * 8 + j] = (uint8_t)ev;
-                    if (a_ok[k] && (ev < (uint32_t)kEMin || ev > (uint32_t)kEMax)) s_spec[r] = tag;
-                }
-            }
-#pragma unroll
-            for (int k = 0; k < kBLoads; k++) {
-                const int p = tid + kThreads * k, t = p / (kSeg * 4), q = p % (kSeg * 4);
-                *reinterpret_cast<u32x4 *>(st + kOffB + t * kBTok + 64 * (q >> 2) + 16 * (q & 3)) = rb[k];
-            }
-            if (tid < kBN * kSeg) {
-                const int t = tid / kSeg, j = tid % kSeg;
-                *reinterpret_cast<float *>(st + kOffD + (t * 8 + j) * 4) = rd;
-            }
+            for (int k = 0; k < kBLoads; k++)
+                dma16(rs_b, st + kOffB + 16u * (64 * wave + kThreads * k), b_off[k], 256u * (uint32_t)s);
+            if (lane < 32) dma4(rs_d, st + kOffD + 128u * wave, d_off, 16u * (uint32_t)s);
         };
 
-        // this lane's A rows (LDS rows 32*wave + 16*rf + i16) and their
-        // window offsets
-        uint32_t l_pos[2];
+        // this lane's A rows: LDS row and matrix byte position (the window of
+        // segment s starts (pos + 68s) & 15 bytes into the row's LDS slots)
+        uint32_t l_row[2], l_pos[2];
+        bool row_ok[2];
 #pragma unroll
         for (int rf = 0; rf < 2; rf++) {
-            const int r = 32 * wave + 16 * rf + i16;
+            const int r = MODE == kGateUp ? 16 * wave + (kBM / 2) * rf + i16 : 32 * wave + 16 * rf + i16;
             const int row = mrow(r);
-            l_pos[rf] = ((MODE == kGateUp && r >= kBM / 2) ? le1 : le0) + (uint32_t)(row < a.rows ? row : 0) * row_bytes;
+            row_ok[rf] = row < a.rows;
+            l_row[rf] = (uint32_t)r * kARow;
+            l_pos[rf] = ((MODE == kGateUp && rf == 1) ? le1 : le0) + (uint32_t)(row_ok[rf] ? row : 0) * row_bytes;
         }
+
         float acc[2][4][4];
 #pragma unroll
         for (int rf = 0; rf < 2; rf++)
@@ -256,74 +375,44 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
             for (int tf = 0; tf < 4; tf++)
 #pragma unroll
                 for (int r = 0; r < 4; r++) acc[rf][tf][r] = 0.0f;
+        uint32_t emin[2] = {255u, 255u}, emax[2] = {0u, 0u};
 
-        stage_load(0);
-        stage_store(0);
-        __syncthreads();
-        for (int s = 0; s < nseg; s++) {
-            if (s + 1 < nseg) stage_load(s + 1);
-            const uint8_t *st = lds + (size_t)(s & 1) * kStageBytes;
-            const int b0 = s * kSeg;
-            const int jn = min(kSeg, nb - b0);
-            // per row fragment: E8M0 bytes of the segment, and for blocks
-            // j = jj + 4m the dword offset (jj) + 68m and byte shift of this
-            // lane's four nibble bytes (1 + 4g .. 4 + 4g of the block)
-            u32x2 ev[2];
-            uint32_t aoff[2][4], ash[2][4];
+        // The K loop, instantiated per number of token fragments (so the
+        // accumulators stay in place through it).
+        auto kloop = [&](auto ntf_c) {
+            constexpr int NTF = decltype(ntf_c)::value;
+            issue(0);
+            if (nseg > 1) issue(1);
+            for (int s = 0; s < nseg; s++) {
+                // this wave's loads of segment s have landed (those of s+1
+                // may still fly); after the barrier every wave's have, and
+                // every wave is done with segment s-1, whose stage segment
+                // s+2 reuses
+                if (s + 1 < nseg)
+                    asm volatile("s_waitcnt vmcnt(7) lgkmcnt(0)" ::: "memory");
+                else
+                    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+                stage_barrier();
+                if (s + 2 < nseg) issue(s + 2);
+                const uint8_t *st = lds + (size_t)(s % kStages) * kStageBytes;
+                const int jn = min(kSeg, nb - kSeg * s);
+                uint32_t a_img[2];
 #pragma unroll
-            for (int rf = 0; rf < 2; rf++) {
-                const int r = 32 * wave + 16 * rf + i16;
-                ev[rf] = *reinterpret_cast<const u32x2 *>(st + kOffE + r * 8);
-                const uint32_t lead = (l_pos[rf] + (uint32_t)b0 * kMxBlock) & 15u;
-#pragma unroll
-                for (int jj = 0; jj < 4; jj++) {
-                    const uint32_t o = lead + 1u + 4u * (uint32_t)g + 17u * (uint32_t)jj;
-                    aoff[rf][jj] = (uint32_t)r * kARow + (o & ~3u);
-                    ash[rf][jj] = o & 3u;
-                }
+                for (int rf = 0; rf < 2; rf++) a_img[rf] = l_row[rf] + ((l_pos[rf] + 68u * (uint32_t)s) & 15u);
+                if (jn == kSeg)
+                    seg_full<NTF>(st, a_img, b_lane, g, i16, acc, emin, emax);
+                else
+                    seg_part<NTF>(st, a_img, b_lane, g, i16, jn, acc, emin, emax);
             }
-#pragma unroll
-            for (int j = 0; j < kSeg; j++) {
-                if (j >= jn) break;
-                const int jj = j & 3, m = j >> 2;
-                bf16x8 A[2];
-#pragma unroll
-                for (int rf = 0; rf < 2; rf++) {
-                    const uint32_t *pw = reinterpret_cast<const uint32_t *>(st + aoff[rf][jj] + 68 * m);
-                    const uint32_t w4 = __builtin_amdgcn_alignbyte(pw[1], pw[0], ash[rf][jj]);
-                    const uint32_t eb = ((j < 4 ? ev[rf].x : ev[rf].y) >> (8 * (j & 3))) & 0xFFu;
-                    const float sc = __uint_as_float(eb << 23);
-                    u32x4 av;
-                    av.x = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w4, sc, 0));
-                    av.y = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w4, sc, 1));
-                    av.z = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w4, sc, 2));
-                    av.w = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w4, sc, 3));
-                    A[rf] = __builtin_bit_cast(bf16x8, av);
-                }
-                bf16x8 B[4];
-                float dx[4];
-#pragma unroll
-                for (int tf = 0; tf < 4; tf++) {
-                    const int t = 16 * tf + i16;
-                    B[tf] = *reinterpret_cast<const bf16x8 *>(st + kOffB + t * kBTok + 64 * j + 16 * g);
-                    dx[tf] = *reinterpret_cast<const float *>(st + kOffD + (t * 8 + j) * 4);
-                }
-                v4f D[2][4];
-#pragma unroll
-                for (int rf = 0; rf < 2; rf++)
-#pragma unroll
-                    for (int tf = 0; tf < 4; tf++)
-                        D[rf][tf] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[rf], B[tf], v4f{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
-#pragma unroll
-                for (int rf = 0; rf < 2; rf++)
-#pragma unroll
-                    for (int tf = 0; tf < 4; tf++)
-#pragma unroll
-                        for (int r = 0; r < 4; r++) acc[rf][tf][r] = __builtin_fmaf(D[rf][tf][r], dx[tf], acc[rf][tf][r]);
-            }
-            if (s + 1 < nseg) stage_store(s + 1);
-            __syncthreads();
-        }
+        };
+        if (ntf == 4)
+            kloop(std::integral_constant<int, 4>{});
+        else if (ntf == 3)
+            kloop(std::integral_constant<int, 3>{});
+        else if (ntf == 2)
+            kloop(std::integral_constant<int, 2>{});
+        else
+            kloop(std::integral_constant<int, 1>{});
 
         // entries of this lane's token columns
         int ent[4];
@@ -333,42 +422,33 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
             ent[tf] = t < nt ? a.list[begin + t] : -1;
         }
 
-        // rows with special E8M0 bytes: the integer decode, one token per
-        // lane, through LDS into the accumulators
-        {
-            const bool mine = lane < 32 && s_spec[32 * wave + lane] == tag;
-            const uint64_t sm = __ballot(mine);
-            if (sm) {
-                float *fix = reinterpret_cast<float *>(lds) + wave * 2 * 16 * kBN;
+        // rows with an E8M0 outside [kEMin, kEMax]: the integer decode, one
+        // entry per lane, moved into the accumulators by lane shuffles
+#pragma unroll
+        for (int rf = 0; rf < 2; rf++) {
+            const bool sp = row_ok[rf] && (emin[rf] < (uint32_t)kEMin || emax[rf] > (uint32_t)kEMax);
+            const uint32_t rows16 = (uint32_t)__ballot(sp) & 0xFFFFu;  // lanes 0..15 hold rows 0..15
+            if (rows16) {
                 int ar = -1;
                 if (lane < nt) {
                     const int en = a.list[begin + lane];
                     ar = MODE == kGateUp ? en / a.topk : en;
                 }
-                for (int rr = 0; rr < 32; rr++) {
-                    if (!((sm >> rr) & 1ull)) continue;
-                    const int r = 32 * wave + rr;
-                    const bool up = MODE == kGateUp && r >= kBM / 2;
-                    const ByteView cv = make_view((up ? a.w[1] : a.w[0]) + (uint64_t)e * a.expert_bytes, a.expert_bytes);
+                const int rbase = MODE == kGateUp ? 16 * wave + (kBM / 2) * rf : 32 * wave + 16 * rf;
+                const ByteView cv = make_view(((MODE == kGateUp && rf == 1) ? a.w[1] : a.w[0]) + (uint64_t)e * a.expert_bytes,
+                                              a.expert_bytes);
+                for (int i = 0; i < 16; i++) {
+                    if (!((rows16 >> i) & 1u)) continue;
                     float v = 0.0f;
                     if (ar >= 0)
-                        v = lut_dot(cv, (uint32_t)mrow(r) * row_bytes, nb, a.codes + (size_t)ar * nb * 32,
+                        v = lut_dot(cv, (uint32_t)mrow(rbase + i) * row_bytes, nb, a.codes + (size_t)ar * nb * 32,
                                     a.scales + (size_t)ar * nb);
-                    fix[rr * kBN + lane] = v;
-                }
-                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
-                __builtin_amdgcn_wave_barrier();
-                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
 #pragma unroll
-                for (int rf = 0; rf < 2; rf++)
-#pragma unroll
-                    for (int r = 0; r < 4; r++) {
-                        const int rr = 16 * rf + 4 * g + r;
-                        if ((sm >> rr) & 1ull) {
-#pragma unroll
-                            for (int tf = 0; tf < 4; tf++) acc[rf][tf][r] = fix[rr * kBN + 16 * tf + i16];
-                        }
+                    for (int tf = 0; tf < 4; tf++) {
+                        const float fv = __shfl(v, 16 * tf + i16);
+                        if (g == (i >> 2)) acc[rf][tf][i & 3] = fv;
                     }
+                }
             }
         }
 
@@ -389,132 +469,103 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
                     *reinterpret_cast<v4f *>(a.out + (size_t)ent[tf] * a.rows + row) = o;
                 }
             }
+            // every wave is done with the stages before the next item's loads
+            stage_barrier();
         } else {
-            // gate (waves 0-3) and up (waves 4-7) rows of output rows
-            // u*128 + 32*(wave&3) + 16*rf + 4g + r; up values go to the gate
-            // waves through LDS
-            const int w4 = wave & 3;
-            const bool is_up = wave >= 4;
-            float *xch = reinterpret_cast<float *>(lds + kFixBytes);
-            float val[2][4][4];
+            // output rows u*128 + 16*wave + 4g + r: gate (rf 0), up (rf 1)
+            const int row = u * (kBM / 2) + 16 * wave + 4 * g;
+            const bool rok = row < a.rows;
+            float bg[4], bu[4];
 #pragma unroll
-            for (int rf = 0; rf < 2; rf++) {
-                const int row = u * (kBM / 2) + 32 * w4 + 16 * rf + 4 * g;
-                float bsum[4];
-#pragma unroll
-                for (int r = 0; r < 4; r++)
-                    bsum[r] = row < a.rows ? bias_at(a.bias[is_up ? 1 : 0], a.bias_type[is_up ? 1 : 0], (uint64_t)e * a.rows + row + r) : 0.0f;
-#pragma unroll
-                for (int tf = 0; tf < 4; tf++)
-#pragma unroll
-                    for (int r = 0; r < 4; r++) val[rf][tf][r] = acc[rf][tf][r] + bsum[r];
+            for (int r = 0; r < 4; r++) {
+                bg[r] = rok ? bias_at(a.bias[0], a.bias_type[0], (uint64_t)e * a.rows + row + r) : 0.0f;
+                bu[r] = rok ? bias_at(a.bias[1], a.bias_type[1], (uint64_t)e * a.rows + row + r) : 0.0f;
             }
-            if (is_up) {
+            float act[4][4];
 #pragma unroll
-                for (int rf = 0; rf < 2; rf++)
+            for (int tf = 0; tf < 4; tf++) {
+                float amax = 0.0f;
+                bool nan = false;
+                v4f gv, uv, av;
 #pragma unroll
-                    for (int tf = 0; tf < 4; tf++) {
-                        const int t = 16 * tf + i16;
-                        const int lr = 32 * w4 + 16 * rf + 4 * g;
-                        *reinterpret_cast<v4f *>(reinterpret_cast<uint8_t *>(xch) + t * kXTok + lr * 4) =
-                            v4f{val[rf][tf][0], val[rf][tf][1], val[rf][tf][2], val[rf][tf][3]};
-                    }
+                for (int r = 0; r < 4; r++) {
+                    gv[r] = acc[0][tf][r] + bg[r];
+                    uv[r] = acc[1][tf][r] + bu[r];
+                    av[r] = swiglu(gv[r], uv[r]);
+                    act[tf][r] = av[r];
+                    const float m = __builtin_fabsf(av[r]);
+                    nan |= m != m;
+                    amax = m > amax ? m : amax;
+                }
+                if (ent[tf] >= 0 && rok) {
+                    const size_t o = (size_t)ent[tf] * a.rows + row;
+                    if (a.tap[0]) *reinterpret_cast<v4f *>(a.tap[0] + o) = gv;
+                    if (a.tap[1]) *reinterpret_cast<v4f *>(a.tap[1] + o) = uv;
+                    if (a.out) *reinterpret_cast<v4f *>(a.out + o) = av;
+                }
+                // the wave's 16 rows of the entry: lanes i16 + 16g
+                amax = fmaxf(amax, __shfl_xor(amax, 16));
+                amax = fmaxf(amax, __shfl_xor(amax, 32));
+                const bool nan_any = ((__ballot(nan) >> i16) & 0x0001000100010001ull) != 0;
+                if (g == 0) s_amax[wave][16 * tf + i16] = nan_any ? -1.0f : amax;
             }
-            __syncthreads();
-            if (!is_up) {
-                const int blk_row = u * (kBM / 2) + 32 * w4;  // first output row of this wave's Q8_0 block
-                const bool blk_ok = blk_row < a.rows;
-                const int nbo = a.rows / 32;
+            // every wave is also done with the stages before the next item's loads
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+            stage_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+            const int blk_row = u * (kBM / 2) + 32 * (wave >> 1);  // first row of this wave pair's Q8_0 block
+            const int half = wave & 1;                             // elements 16*half .. 16*half+15 of it
+            const int nbo = a.rows / 32;
 #pragma unroll
-                for (int tf = 0; tf < 4; tf++) {
-                    const int t = 16 * tf + i16;
-                    float act[2][4];
-                    float amax = 0.0f;
-                    bool nan = false;
+            for (int tf = 0; tf < 4; tf++) {
+                if (ent[tf] < 0 || blk_row >= a.rows) continue;
+                const float m0 = s_amax[wave][16 * tf + i16], m1 = s_amax[wave ^ 1][16 * tf + i16];
+                const bool nan_any = m0 < 0.0f || m1 < 0.0f;
+                const float d = nan_any ? __builtin_nanf("") : fmaxf(m0, m1) / 127.0f;
+                const float id = (d != 0.0f) ? 1.0f / d : 0.0f;
+                const uint16_t dh = f32_to_f16_bits(d);
+                int q[4];
 #pragma unroll
-                    for (int rf = 0; rf < 2; rf++) {
-                        const int lr = 32 * w4 + 16 * rf + 4 * g;
-                        const v4f uv = *reinterpret_cast<const v4f *>(reinterpret_cast<const uint8_t *>(xch) + t * kXTok + lr * 4);
-#pragma unroll
-                        for (int r = 0; r < 4; r++) {
-                            const float v = swiglu(val[rf][tf][r], uv[r]);
-                            act[rf][r] = v;
-                            const float av = __builtin_fabsf(v);
-                            nan |= av != av;
-                            amax = av > amax ? av : amax;
-                        }
-                        const int row = blk_row + 16 * rf + 4 * g;
-                        if (ent[tf] >= 0 && row < a.rows) {
-                            const size_t o = (size_t)ent[tf] * a.rows + row;
-                            if (a.tap[0]) *reinterpret_cast<v4f *>(a.tap[0] + o) = v4f{val[rf][tf][0], val[rf][tf][1], val[rf][tf][2], val[rf][tf][3]};
-                            if (a.tap[1]) *reinterpret_cast<v4f *>(a.tap[1] + o) = uv;
-                            if (a.out) *reinterpret_cast<v4f *>(a.out + o) = v4f{act[rf][0], act[rf][1], act[rf][2], act[rf][3]};
-                        }
-                    }
-                    // Q8_0 of the 32-element block (rows 4g+r and 16+4g+r of
-                    // the four lanes i16, i16+16, i16+32, i16+48)
-                    amax = fmaxf(amax, __shfl_xor(amax, 16));
-                    amax = fmaxf(amax, __shfl_xor(amax, 32));
-                    const uint64_t nm = __ballot(nan);
-                    const bool nan_any = ((nm >> i16) & 0x0001000100010001ull) != 0;
-                    const float d = nan_any ? __builtin_nanf("") : amax / 127.0f;
-                    const float id = (d != 0.0f) ? 1.0f / d : 0.0f;
-                    const uint16_t dh = f32_to_f16_bits(d);
-                    int q[2][4];
-#pragma unroll
-                    for (int rf = 0; rf < 2; rf++)
-#pragma unroll
-                        for (int r = 0; r < 4; r++) {
-                            const float rq = __builtin_roundf(act[rf][r] * id);
-                            q[rf][r] = (rq != rq) ? 0 : (rq > 127.0f ? 127 : (rq < -127.0f ? -127 : (int)rq));
-                        }
-                    if (ent[tf] >= 0 && blk_ok) {
-                        const size_t blk = (size_t)ent[tf] * nbo + blk_row / 32;
-#pragma unroll
-                        for (int rf = 0; rf < 2; rf++) {
-                            const uint32_t cw = (uint32_t)(q[rf][0] & 0xff) | ((uint32_t)(q[rf][1] & 0xff) << 8) |
-                                                ((uint32_t)(q[rf][2] & 0xff) << 16) | ((uint32_t)(q[rf][3] & 0xff) << 24);
-                            if (a.act_codes) *reinterpret_cast<uint32_t *>(a.act_codes + blk * 32 + 16 * rf + 4 * g) = cw;
-                            if (a.act_blocks34) {
-#pragma unroll
-                                for (int r = 0; r < 4; r++) a.act_blocks34[blk * kQ80Block + 2 + 16 * rf + 4 * g + r] = (uint8_t)q[rf][r];
-                            }
-                        }
-                        if (g == 0) {
-                            if (a.act_scales) a.act_scales[blk] = f16_bits_to_f32(dh);
-                            if (a.act_blocks34) {
-                                a.act_blocks34[blk * kQ80Block] = (uint8_t)(dh & 0xff);
-                                a.act_blocks34[blk * kQ80Block + 1] = (uint8_t)(dh >> 8);
-                            }
-                        }
-                        if (a.act_mxtab) {
-                            // nibble position 2*el' + h of elements (4g+r, 16+4g+r): 8g + 2r + {0,1}
-                            u32x2 hw, lw;
-                            hw.x = e4m3_small(q[0][0] >> 4) | (e4m3_small(q[1][0] >> 4) << 8) | (e4m3_small(q[0][1] >> 4) << 16) | (e4m3_small(q[1][1] >> 4) << 24);
-                            hw.y = e4m3_small(q[0][2] >> 4) | (e4m3_small(q[1][2] >> 4) << 8) | (e4m3_small(q[0][3] >> 4) << 16) | (e4m3_small(q[1][3] >> 4) << 24);
-                            lw.x = e4m3_small(q[0][0] & 15) | (e4m3_small(q[1][0] & 15) << 8) | (e4m3_small(q[0][1] & 15) << 16) | (e4m3_small(q[1][1] & 15) << 24);
-                            lw.y = e4m3_small(q[0][2] & 15) | (e4m3_small(q[1][2] & 15) << 8) | (e4m3_small(q[0][3] & 15) << 16) | (e4m3_small(q[1][3] & 15) << 24);
-                            *reinterpret_cast<u32x2 *>(a.act_mxtab + blk * 64 + 8 * g) = hw;
-                            *reinterpret_cast<u32x2 *>(a.act_mxtab + blk * 64 + 32 + 8 * g) = lw;
-                        }
-                        if (a.act_btab) {
-                            const u32x4 bw = {bf16_code_pair(q[0][0], q[1][0]), bf16_code_pair(q[0][1], q[1][1]),
-                                              bf16_code_pair(q[0][2], q[1][2]), bf16_code_pair(q[0][3], q[1][3])};
-                            *reinterpret_cast<u32x4 *>(a.act_btab + blk * 16 + 4 * g) = bw;
-                        }
+                for (int r = 0; r < 4; r++) {
+                    const float rq = __builtin_roundf(act[tf][r] * id);
+                    q[r] = (rq != rq) ? 0 : (rq > 127.0f ? 127 : (rq < -127.0f ? -127 : (int)rq));
+                }
+                const size_t blk = (size_t)ent[tf] * nbo + blk_row / 32;
+                const int el = 16 * half + 4 * g;  // element of q[0]
+                if (a.act_codes)
+                    *reinterpret_cast<uint32_t *>(a.act_codes + blk * 32 + el) =
+                        (uint32_t)(q[0] & 0xff) | ((uint32_t)(q[1] & 0xff) << 8) | ((uint32_t)(q[2] & 0xff) << 16) |
+                        ((uint32_t)(q[3] & 0xff) << 24);
+                if (half == 0 && g == 0) {
+                    if (a.act_scales) a.act_scales[blk] = f16_bits_to_f32(dh);
+                    if (a.act_blocks34) {
+                        a.act_blocks34[blk * kQ80Block] = (uint8_t)(dh & 0xff);
+                        a.act_blocks34[blk * kQ80Block + 1] = (uint8_t)(dh >> 8);
                     }
                 }
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    // element 16*half + 4g + r: nibble position 2*(4g + r) + half
+                    const int p = 2 * (4 * g + r) + half;
+                    if (a.act_mxtab) {
+                        a.act_mxtab[blk * 64 + p] = (uint8_t)e4m3_small(q[r] >> 4);
+                        a.act_mxtab[blk * 64 + 32 + p] = (uint8_t)e4m3_small(q[r] & 15);
+                    }
+                    if (a.act_btab)
+                        reinterpret_cast<uint16_t *>(a.act_btab + blk * 16)[2 * (4 * g + r) + half] =
+                            (uint16_t)(__float_as_uint((float)q[r]) >> 16);
+                    if (a.act_blocks34) a.act_blocks34[blk * kQ80Block + 2 + el + r] = (uint8_t)q[r];
+                }
             }
+            // the partner wave has read this wave's s_amax before the next item writes it
+            stage_barrier();
         }
-        // every wave is done with the epilogue areas before the next item's
-        // first stage is written over them
-        __syncthreads();
     }
 }
 
 hipError_t launch_mx_gemm(hipStream_t s, GemvMode mode, const MxGemmArgs &a, int max_items) {
     if (max_items <= 0 || a.rows <= 0 || a.nb <= 0) return hipSuccess;
-    constexpr size_t lds = 2 * (size_t)kStageBytes;
+    constexpr size_t lds = (size_t)kStages * kStageBytes;
     static const hipError_t attr = [] {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_mx_gemm<kGateUp>),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);

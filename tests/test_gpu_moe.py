@@ -169,12 +169,12 @@ def test_moe_decode_gpt_oss_layer(gpu_ctx, O):
           f"vs fp32-activation reference {np.max(np.abs(g['out'] - ref)) / np.max(np.abs(ref)):.2e}")
 
 
-@pytest.mark.parametrize("path", ["default", "gemv"])
+@pytest.mark.parametrize("path", ["default", "gemm", "gemv"])
 @pytest.mark.parametrize("batch", [32])
 def test_moe_prefill_zipf(gpu_ctx, O, batch, path):
     """32 positions per weight pass, router logits injected so expert
-    popularity follows Zipf(1.1): ragged groups of 0..32 rows (by default the
-    groups of 9 or more through the grouped GEMM)."""
+    popularity follows Zipf(1.1): ragged groups of 0..32 rows, through the
+    default split (at 128 selections: all GEMV), all GEMM and all GEMV."""
     from spt import synth
     from spt import workloads as W
 
@@ -193,7 +193,8 @@ def test_moe_prefill_zipf(gpu_ctx, O, batch, path):
 
 def test_moe_prefill_hot_expert(gpu_ctx, O):
     """512 tokens, 25% of them forced to one hot expert and the rest Zipf(1.1)
-    (the long-prompt chunk): groups from 1 to hundreds of rows.  Routing,
+    (the long-prompt chunk): groups from 1 to hundreds of rows (by default
+    the groups of 9 or more through the grouped GEMM).  Routing,
     packing, the Q8_0 stages and the combine are checked on every selection;
     the projections on a sample holding the hot expert's first and last list
     tiles and random others."""
