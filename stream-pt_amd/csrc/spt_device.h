@@ -337,6 +337,33 @@ __device__ inline int q8_quantize_lane(float v, int lane, uint16_t *dbits) {
     return (r != r) ? 0 : (r > 127.0f ? 127 : (r < -127.0f ? -127 : (int)r));
 }
 
+// Largest value over each half-wave (32 lanes) of non-negative non-NaN
+// floats given as bit patterns (which order like the values): DPP lane ^ 15,
+// ^ 7, ^ 1, ^ 2 within rows of 16, then a swizzle for lane ^ 16.
+__device__ __attribute__((always_inline)) inline uint32_t max32_bits(uint32_t m) {
+    m = max(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x140, 0xF, 0xF, false));
+    m = max(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x141, 0xF, 0xF, false));
+    m = max(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0xB1, 0xF, 0xF, false));
+    m = max(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x4E, 0xF, 0xF, false));
+    m = max(m, (uint32_t)__builtin_amdgcn_ds_swizzle((int)m, 0x401F));
+    return m;
+}
+
+// Q8_0 of a 32-element block held one element per lane by each half-wave:
+// the arithmetic of q8_quantize_lane (scale amax / 127, a NaN anywhere in
+// the block makes the scale NaN), with the reductions done per half-wave.
+__device__ __attribute__((always_inline)) inline int q8_quantize_half(float v, int lane, uint16_t *dbits) {
+    const float a = __builtin_fabsf(v);
+    const uint64_t nanm = __ballot(a != a);
+    const bool nan_any = ((lane < 32 ? nanm : nanm >> 32) & 0xFFFFFFFFull) != 0;
+    const float m = __uint_as_float(max32_bits(a == a ? __float_as_uint(a) : 0u));
+    const float d = nan_any ? __builtin_nanf("") : m / 127.0f;
+    const float id = (d != 0.0f) ? 1.0f / d : 0.0f;
+    *dbits = f32_to_f16_bits(d);
+    const float r = __builtin_roundf(v * id);
+    return (r != r) ? 0 : (r > 127.0f ? 127 : (r < -127.0f ? -127 : (int)r));
+}
+
 // Lane i (< 32) of a wavefront stores element i of Q8_0 block `blk` (code q)
 // into every requested layout of write_q8_block; lane 0 also stores the scale.
 __device__ inline void write_q8_lane(int q, uint16_t dh, int lane, size_t blk, int8_t *codes,

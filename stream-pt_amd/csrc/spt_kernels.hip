@@ -15,7 +15,8 @@ constexpr int kWG = 256;
 constexpr int kRowsPerWG = 16;
 
 // ---------------------------------------------------------------------------
-// Q8_0 quantization: one thread per block of 32.
+// Q8_0 quantization: one half-wave per block of 32, one element per lane
+// (coalesced loads; the block's amax by DPP and a swizzle).
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(kWG) void k_quantize(const float *__restrict__ x, int64_t nblocks,
                                                   int8_t *__restrict__ codes,
@@ -24,20 +25,18 @@ __global__ __launch_bounds__(kWG) void k_quantize(const float *__restrict__ x, i
                                                   uint8_t *__restrict__ mxtab,
                                                   uint8_t *__restrict__ blocks34,
                                                   uint32_t *__restrict__ btab) {
-    int64_t b = (int64_t)blockIdx.x * kWG + threadIdx.x;
-    if (b >= nblocks) return;
-    float v[32];
-#pragma unroll
-    for (int i = 0; i < 32; i++) v[i] = x[b * 32 + i];
-    uint32_t w[8];
+    const int tid = threadIdx.x, lane = tid & 63, i = tid & 31;
+    const int64_t b = (int64_t)blockIdx.x * (kWG / 32) + (tid >> 5);
+    const bool ok = b < nblocks;
+    const float v = ok ? x[b * 32 + i] : 0.0f;
     uint16_t dh;
-    q8_quantize32(v, w, &dh);
-    write_q8_block(w, dh, (size_t)b, codes, scales, mxtab, blocks34, btab);
+    const int q = q8_quantize_half(v, lane, &dh);  // every lane takes part (cross-lane steps)
+    if (ok) write_q8_lane(q, dh, i, (size_t)b, codes, scales, mxtab, blocks34, btab);
     if (sumq) {
-        int32_t s = 0;
+        int s = q;
 #pragma unroll
-        for (int k = 0; k < 8; k++) s = __builtin_amdgcn_sdot4((int)w[k], 0x01010101, s, false);
-        sumq[b] = s;
+        for (int off = 16; off >= 1; off >>= 1) s += __shfl_xor(s, off, 32);
+        if (ok && i == 0) sumq[b] = s;
     }
 }
 
@@ -45,7 +44,7 @@ hipError_t launch_quantize(hipStream_t s, const float *x, int64_t nblocks, int8_
                            float *scales, int32_t *sumq, uint8_t *mxtab, uint8_t *blocks34,
                            uint32_t *btab) {
     if (nblocks <= 0) return hipSuccess;
-    dim3 grid((unsigned)((nblocks + kWG - 1) / kWG));
+    dim3 grid((unsigned)((nblocks + kWG / 32 - 1) / (kWG / 32)));
     hipLaunchKernelGGL(k_quantize, grid, dim3(kWG), 0, s, x, nblocks, codes, scales, sumq, mxtab, blocks34, btab);
     return hipGetLastError();
 }
@@ -72,51 +71,81 @@ __device__ inline float router_reduce(float a, int lane) {
     return (p + p1) + (p2 + p3);
 }
 
+// Largest of the wave's 64 values (every lane gets it); NaN operands lose
+// (v_max_f32 returns the other operand), so the result is NaN only when all
+// are.  DPP within rows of 16 (lane ^ 1, ^ 2, half-row and row mirrors), then
+// the four row results through readlane.
+__device__ __attribute__((always_inline)) inline float wave_max(float v) {
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false)));
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false)));
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false)));
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false)));
+    const int b = __builtin_bit_cast(int, v);
+    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0));
+    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16));
+    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32));
+    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
+    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+
 // selectMoEBatch (forward/moe_batch.go:305-342) for one token by one
 // wavefront: k rounds of a strict '>' scan where the lowest index wins ties,
-// NaN and -Inf never win and picked experts are excluded (lane L owns experts
-// L, L+64, ...; a per-lane bit mask marks the picked ones); a round with
-// nothing selectable falls back to Index = round, logit 0.  Then the softmax
+// NaN and -Inf never win and picked experts are excluded.  Lane L owns
+// experts L, L+64, ...; excluded experts (picked, or past E) hold NaN.  A
+// round takes the largest value m (NaN candidates lose), and if m > -Inf the
+// lowest expert holding a value equal to m (ballots by slot; -0 and +0 tie,
+// as under '>'); otherwise nothing is selectable and the round falls back to
+// Index = round, logit 0.  Then the softmax
 // over the k logits: w = f32(exp(f64(l - max))) (lane r computes rank r's),
 // summed in f32 in rank order, scaled by 1/sum when sum > 0.  Results go to
 // LDS (s_ids/s_w, the token's k slots) and to global ids/weights.
-__device__ void select_token(const float *lg, int E, int k, int32_t *ids, float *weights,
-                             int32_t *s_ids, float *s_w) {
-    const int lane = threadIdx.x & 63;
+struct TokenLogits {
     float v[kMaxExperts / 64];
+};
+
+// Lane L's logits of a token (experts L, L+64, ...; NaN past E).
+__device__ inline TokenLogits load_token_logits(const float *lg, int E) {
+    const int lane = threadIdx.x & 63;
+    TokenLogits tl;
 #pragma unroll
     for (int i = 0; i < kMaxExperts / 64; i++) {
         const int ex = lane + 64 * i;
-        v[i] = ex < E ? lg[ex] : -__builtin_inff();
+        tl.v[i] = ex < E ? lg[ex] : __builtin_nanf("");
     }
-    uint32_t taken = 0;
+    return tl;
+}
+
+__device__ void select_token(TokenLogits tl, int E, int k, int32_t *ids, float *weights,
+                             int32_t *s_ids, float *s_w) {
+    const int lane = threadIdx.x & 63;
+    const float qnan = __builtin_nanf("");
+    float *v = tl.v;
+    const int nslot = (E + 63) / 64;
     int my_id = 0;
     float my_val = 0.0f;
     for (int r = 0; r < k; r++) {
-        float bv = -__builtin_inff();
-        int bi = -1;
+        float lm = qnan;
 #pragma unroll
-        for (int i = 0; i < kMaxExperts / 64; i++) {
-            if (!((taken >> i) & 1u) && v[i] > bv) {
-                bv = v[i];
-                bi = lane + 64 * i;
+        for (int i = 0; i < kMaxExperts / 64; i++) lm = fmaxf(lm, v[i]);
+        const float m = wave_max(lm);
+        int bi = r;
+        float bv = 0.0f;
+        if (m > -__builtin_inff()) {
+            bv = m;
+#pragma unroll
+            for (int i = 0; i < kMaxExperts / 64; i++) {
+                if (i >= nslot) break;
+                const uint64_t hit = __ballot(v[i] == m);
+                if (hit) {
+                    bi = 64 * i + __builtin_ctzll(hit);
+                    break;
+                }
             }
         }
+        // exclude the pick (in the fallback, expert `round`)
 #pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) {
-            const float ov = __shfl_xor(bv, off);
-            const int oi = __shfl_xor(bi, off);
-            const bool take = oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi));
-            if (take) {
-                bv = ov;
-                bi = oi;
-            }
-        }
-        if (bi < 0) {
-            bi = r;
-            bv = 0.0f;
-        }
-        if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
+        for (int i = 0; i < kMaxExperts / 64; i++)
+            if (bi == lane + 64 * i) v[i] = qnan;
         if (lane == r) {
             my_id = bi;
             my_val = bv;
@@ -125,12 +154,12 @@ __device__ void select_token(const float *lg, int E, int k, int32_t *ids, float 
     // max over ranks in order (NaN never replaces: strict '>')
     float mx = -__builtin_inff();
     for (int r = 0; r < k; r++) {
-        const float l = __shfl(my_val, r);
+        const float l = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_val), r));
         if (l > mx) mx = l;
     }
     const float e = lane < k ? static_cast<float>(exp(static_cast<double>(my_val - mx))) : 0.0f;
     float sum = 0.0f;
-    for (int r = 0; r < k; r++) sum += __shfl(e, r);
+    for (int r = 0; r < k; r++) sum += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, e), r));
     if (lane < k) {
         const float w = sum > 0.0f ? e * (1.0f / sum) : e;
         s_ids[lane] = my_id;
@@ -139,6 +168,21 @@ __device__ void select_token(const float *lg, int E, int k, int32_t *ids, float 
         weights[lane] = w;
     }
 }
+
+// Inclusive prefix sum over the 64 lanes of a wavefront: Hillis-Steele by
+// DPP row shifts within rows of 16, then the row totals carried by the row
+// broadcasts (lane 15 to the next row, lane 31 to rows 2-3).
+__device__ __attribute__((always_inline)) inline int wave_incl_scan(int x) {
+    x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, true);  // row_shr:1
+    x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, true);  // row_shr:2
+    x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, true);  // row_shr:4
+    x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, true);  // row_shr:8
+    x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xA, 0xF, false); // row_bcast:15 -> rows 1, 3
+    x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xC, 0xF, false); // row_bcast:31 -> rows 2, 3
+    return x;
+}
+
+__device__ __attribute__((always_inline)) inline int lane63(int x) { return __builtin_amdgcn_readlane(x, 63); }
 
 // Per-expert lists (forward/moe_batch.go:142-159) for n = batch*k selections
 // held in LDS (s_ids/s_w), by one workgroup of kSelWG threads.  Selections
@@ -173,10 +217,7 @@ __device__ void pack_lists(int n, int E, const SelectOut &o, const int32_t *s_id
         int tiles = 0;
         for (int e0 = 0; e0 < E; e0 += 64) {
             const int c = e0 + tid < E ? s_cnt[e0 + tid] : 0;
-            int t = (c > 0 && c >= o.gemm_min) ? (c + kGemmTokens - 1) / kGemmTokens : 0;
-#pragma unroll
-            for (int d = 32; d >= 1; d >>= 1) t += __shfl_xor(t, d);
-            tiles += t;
+            tiles += lane63(wave_incl_scan((c > 0 && c >= o.gemm_min) ? (c + kGemmTokens - 1) / kGemmTokens : 0));
         }
         const bool gemm_on = (int64_t)tiles * o.gemm_units >= (int64_t)o.gemm_min_items;
         for (int e0 = 0; e0 < E; e0 += 64) {
@@ -185,16 +226,7 @@ __device__ void pack_lists(int n, int E, const SelectOut &o, const int32_t *s_id
             const bool big = gemm_on && c > 0 && c >= o.gemm_min;
             const int np = big ? 0 : (c + kGemvTokens - 1) / kGemvTokens;
             const int ntl = big ? (c + kGemmTokens - 1) / kGemmTokens : 0;
-            int incl = c, pincl = np, tincl = ntl;
-#pragma unroll
-            for (int d = 1; d < 64; d <<= 1) {
-                const int up = __shfl_up(incl, d), pup = __shfl_up(pincl, d), tup = __shfl_up(tincl, d);
-                if (tid >= d) {
-                    incl += up;
-                    pincl += pup;
-                    tincl += tup;
-                }
-            }
+            const int incl = wave_incl_scan(c), pincl = wave_incl_scan(np), tincl = wave_incl_scan(ntl);
             const uint64_t act = __ballot(c > 0), actv = __ballot(c > 0 && !big), actm = __ballot(big);
             if (e < E) {
                 s_off[e] = pos + incl - c;
@@ -212,9 +244,9 @@ __device__ void pack_lists(int n, int E, const SelectOut &o, const int32_t *s_id
                     o.gm_tile_off[r] = ntile + tincl - ntl;
                 }
             }
-            pos += __shfl(incl, 63);
-            npass += __shfl(pincl, 63);
-            ntile += __shfl(tincl, 63);
+            pos += lane63(incl);
+            npass += lane63(pincl);
+            ntile += lane63(tincl);
             na += __builtin_popcountll(act);
             nv += __builtin_popcountll(actv);
             nm += __builtin_popcountll(actm);
@@ -261,8 +293,8 @@ static size_t select_lds(int n, int E) {
 
 // Router logits: one workgroup per (4 experts, 1 token); wave w computes the
 // logit of expert 4*blockIdx.x + w for token blockIdx.y (16 chunk loads in
-// flight per lane).  With q set, workgroup (0, t) also quantizes token t's
-// row of x to Q8_0.
+// flight per lane).  With q set, the workgroups of token t also quantize its
+// row of x to Q8_0, eight blocks each (a half-wave per block).
 __global__ __launch_bounds__(kWG) void k_route(const float *__restrict__ router,
                                                const void *bias, int bias_type,
                                                const float *__restrict__ x, int H, int E,
@@ -271,15 +303,14 @@ __global__ __launch_bounds__(kWG) void k_route(const float *__restrict__ router,
     const int e = blockIdx.x * 4 + wave;
     const int t = blockIdx.y;
     const float *xt = x + (size_t)t * H;
-    if (blockIdx.x == 0 && (q.codes || q.blocks34)) {
-        for (int b = tid; b < H / 32; b += kWG) {
-            float v[32];
-#pragma unroll
-            for (int i = 0; i < 32; i++) v[i] = xt[b * 32 + i];
-            uint32_t w[8];
+    if (q.codes || q.blocks34) {
+        const int nbh = H / 32;
+        for (int b0 = blockIdx.x * (kWG / 32); b0 < nbh; b0 += gridDim.x * (kWG / 32)) {
+            const int b = b0 + (tid >> 5), i = tid & 31;
+            const float v = b < nbh ? xt[b * 32 + i] : 0.0f;
             uint16_t dh;
-            q8_quantize32(v, w, &dh);
-            write_q8_block(w, dh, (size_t)t * (H / 32) + b, q.codes, q.scales, q.mxtab, q.blocks34, q.btab);
+            const int qv = q8_quantize_half(v, lane, &dh);  // every lane takes part
+            if (b < nbh) write_q8_lane(qv, dh, i, (size_t)t * nbh + b, q.codes, q.scales, q.mxtab, q.blocks34, q.btab);
         }
     }
     if (e >= E) return;
@@ -318,9 +349,16 @@ __global__ __launch_bounds__(kSelWG) void k_select(const float *__restrict__ log
     int32_t *s_run = s_off + E + 1;
     uint32_t *s_bits = reinterpret_cast<uint32_t *>(s_run + E);
     const int wave = threadIdx.x >> 6;
-    for (int t = wave; t < batch; t += kSelWG / 64)
-        select_token(logits + (size_t)t * E, E, topk, o.ids + t * topk, o.weights + t * topk,
-                     s_ids + t * topk, s_w + t * topk);
+    // each wave takes tokens wave, wave + 16, ...; the next token's logits
+    // are loaded while the current one is selected
+    constexpr int kStride = kSelWG / 64;
+    TokenLogits next{};
+    if (wave < batch) next = load_token_logits(logits + (size_t)wave * E, E);
+    for (int t = wave; t < batch; t += kStride) {
+        const TokenLogits cur = next;
+        if (t + kStride < batch) next = load_token_logits(logits + (size_t)(t + kStride) * E, E);
+        select_token(cur, E, topk, o.ids + t * topk, o.weights + t * topk, s_ids + t * topk, s_w + t * topk);
+    }
     __syncthreads();
     pack_lists(n, E, o, s_ids, s_w, s_cnt, s_off, s_run, s_bits);
 }
