@@ -29,7 +29,13 @@ for p in (os.path.join(ROOT, "stream-pt_amd"), ROOT):
         sys.path.insert(0, p)
 
 HBM_PEAK_GBPS = 8000.0
+BF16_DENSE_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+INT8_DENSE_TOPS = 5000.0     # MI355X dense int8 MFMA
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "k_mx_mfma_decode_b64_36layers.md")
+MFMA_PROFILE = os.path.join(ROOT, "profiles", "k_mx_gemm_prefill_b512_hot.md")
+# grouped-GEMM policy of the library's default (spt_abi.hip: kGemmMinGroup,
+# kGemmMinSelections; select: items must fill the device)
+GEMM_MIN_GROUP, GEMM_MIN_SELECTIONS = 9, 1024
 
 
 def measured_traffic(batch, layers, seed):
@@ -44,6 +50,20 @@ def measured_traffic(batch, layers, seed):
                 if line.startswith("traffic_bytes_per_launch k_mx_mfma<0> B=64:"):
                     return float(line.split(":", 1)[1])
     except OSError:
+        pass
+    return None
+
+
+def measured_mfma_util(workload):
+    """MFMA busy fraction of the grouped GEMM kernels from the committed
+    rocprofv3 counter pass (SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE x
+    SIMDs)), for the workload that pass ran, else None."""
+    try:
+        with open(MFMA_PROFILE) as f:
+            for line in f:
+                if line.startswith(f"mfma_util {workload}:"):
+                    return json.loads(line.split(":", 1)[1])
+    except (OSError, ValueError):
         pass
     return None
 
@@ -63,6 +83,9 @@ def parse():
     ap.add_argument("--seed", type=int, default=3)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the prefill workloads")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="only the prefill workloads (one layer resident; for counter passes)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run a 1 GiB elementwise copy kernel three times (known "
                          "traffic for scaling hardware byte counters)")
@@ -108,6 +131,11 @@ def main():
         del src, dst
     ctx = spt.Context(0, stream.cuda_stream)
     shp = W.MoEShape()
+    if args.prefill_only:
+        layer0 = W.device_layer(ctx, args.seed, 0, shp)
+        print(json.dumps({"prefill": prefill(args, ctx, layer0, shp, W, stream)}), flush=True)
+        ctx.close()
+        return
     L = args.layers
     t0 = time.time()
     layers = [W.device_layer(ctx, args.seed, l, shp) for l in range(L)]
@@ -194,6 +222,7 @@ def main():
         "bytes_per_launch": head["gate_up_bytes_per_launch"],
         "avg_launch_us": round(head["gate_up_avg_us"], 2),
     }
+    pre = None if args.no_prefill else prefill(args, ctx, layers[0], shp, W, stream)
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(args, shp, W)
@@ -223,9 +252,118 @@ def main():
                               if k != "kernel_ms_per_step"} for b, r in results.items()},
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "prefill": pre,
     }
     print(json.dumps(line), flush=True)
     ctx.close()
+
+
+def prefill(args, ctx, dl, shp, W, stream, reps=20):
+    """The batched-prefill workloads, one MoE layer each (router logits
+    injected so expert popularity follows Zipf(1.1)):
+      zipf_b32:  32 positions per weight pass;
+      hot_b512:  a 512-token prompt chunk, 25% of the tokens forced to one
+                 hot expert, plus the layer's Q4_0 attention projections
+                 (Q, K, V, O) at B = 512.
+    Per workload: tokens/s of the layer, per-kernel durations (HIP events on
+    the library's stream), the weight bytes of the touched experts over the
+    layer time, and for the grouped GEMM its algorithmic multiply-adds
+    (selections of GEMM experts x 3 x hidden x expert dim) over its kernel
+    time against the dense bf16 MFMA peak it runs on and the int8 peak."""
+    import numpy as np
+    import torch
+
+    import spt
+    from spt import synth
+
+    H, D, E, k = shp.hidden, shp.expert_dim, shp.experts, shp.topk
+    out = {}
+    for name, B, hot, seed in (("zipf_b32", 32, 0.0, 2), ("hot_b512", 512, 0.25, 4)):
+        logits = torch.from_numpy(synth.zipf_logits(synth.stream_key(seed, 99), B, E, 1.1,
+                                                    hot_fraction=hot, hot_expert=17)).cuda()
+        x = torch.from_numpy(W.x_tokens(seed, 0, B, H)).cuda()
+        y = torch.empty(B * H, dtype=torch.float32, device="cuda")
+        counts = torch.zeros(E, dtype=torch.int32, device="cuda")
+        taps = spt.make_taps(logits_in=logits, counts=counts)
+        ctx.forward_moe_batch(dl.config, dl.layer, x, y, B, taps)
+        torch.cuda.synchronize()
+        c = counts.cpu().numpy()
+        distinct = int(np.count_nonzero(c))
+        n = B * k
+        big = c[c >= GEMM_MIN_GROUP]
+        gemm_on = n >= GEMM_MIN_SELECTIONS and int(np.sum((big + 63) // 64)) * ((D + 127) // 128) >= 256
+        gemm_sel = int(big.sum()) if gemm_on else 0
+        for _ in range(3):
+            ctx.forward_moe_batch(dl.config, dl.layer, x, y, B, taps)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            ctx.forward_moe_batch(dl.config, dl.layer, x, y, B, taps)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / reps
+        ctx.enable_timing(True)
+        ctx.read_timing()
+        for _ in range(reps):
+            ctx.forward_moe_batch(dl.config, dl.layer, x, y, B, taps)
+        kt = ctx.read_timing()
+        ctx.enable_timing(False)
+        kus = {kk: round(v[0] / reps * 1e3, 1) for kk, v in kt.items() if v[1]}
+        wbytes = distinct * (2 * shp.gate_bytes + shp.down_bytes)
+        res = {
+            "batch": B, "ms_per_layer": round(ms, 4), "tokens_per_s": round(B / (ms / 1e3), 1),
+            "distinct_experts": distinct, "largest_group": int(c.max()),
+            "weight_gb": round(wbytes / 1e9, 4), "weight_gbps": round(wbytes / (ms / 1e3) / 1e9, 1),
+            "kernel_us": kus, "gemm_experts": int(len(big)) if gemm_on else 0, "gemm_selections": gemm_sel,
+        }
+        gemm_us = kus.get("gate_up_gemm", 0.0) + kus.get("down_gemm", 0.0)
+        if gemm_sel and gemm_us > 0:
+            macs = gemm_sel * 3 * H * D
+            tops = 2 * macs / (gemm_us * 1e-6) / 1e12
+            res["gemm"] = {"macs": macs, "us": round(gemm_us, 1), "tops": round(tops, 2),
+                           "frac_bf16_dense": round(tops / BF16_DENSE_TFLOPS, 4),
+                           "frac_int8_dense": round(tops / INT8_DENSE_TOPS, 4),
+                           "mfma_util_measured": measured_mfma_util(name)}
+        if name == "hot_b512":
+            res["q40_attention"] = q40_projections(ctx, B, W, stream, reps)
+        out[name] = res
+        log(f"prefill {name}: {json.dumps(res)}")
+    # the dense Q4_0 projections alone (GEMV at B=1, small GEMM at B=32)
+    out["q40_attention"] = {str(B): q40_projections(ctx, B, W, stream, reps) for B in (1, 32)}
+    log(f"prefill q40: {json.dumps(out['q40_attention'])}")
+    return out
+
+
+def q40_projections(ctx, B, W, stream, reps):
+    """Q4_0 x Q8_0 attention projections of one layer (Q 2880->4096,
+    K/V 2880->512, O 4096->2880; fp16 scales |N(0,0.01)|, uniform nibbles)
+    for B tokens: microseconds per projection and in total."""
+    import torch
+
+    import spt
+    from spt import synth
+
+    res, total = {}, 0.0
+    for i, (name, din, dout) in enumerate(W.q40_projection_shapes()):
+        wb = torch.from_numpy(synth.q40_bytes(synth.stream_key(40 + i, dout), dout, din)).cuda()
+        t = spt.Tensor.make(name, spt.TYPE_Q4_0, [din, dout], wb.data_ptr(), wb.numel())
+        xq = torch.from_numpy(synth.normal(synth.stream_key(50 + i, B), B * din)).cuda()
+        yq = torch.empty(B * dout, dtype=torch.float32, device="cuda")
+        for _ in range(3):
+            ctx.mul_q40_batch_into(t, xq, yq, B)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            ctx.mul_q40_batch_into(t, xq, yq, B)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) / reps * 1e3
+        res[name] = round(us, 1)
+        total += us
+    res["total_us"] = round(total, 1)
+    return res
 
 
 def cpu_baseline(args, shp, W):

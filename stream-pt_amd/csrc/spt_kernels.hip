@@ -395,14 +395,32 @@ __global__ __launch_bounds__(kWG) void k_q40_gemv(Q40Args a) {
     const uint32_t row_pos = (uint32_t)(row_ok ? r : 0) * (uint32_t)(nb * kQ40Block);
     const ByteView view = make_view(a.w, a.nbytes);
 
-    for (int c0 = 0; c0 < a.ntok; c0 += NT) {
+    // token passes of NT tokens: workgroup (x, y) takes passes y, y + G, ...
+    for (int c0 = blockIdx.y * NT; c0 < a.ntok; c0 += gridDim.y * NT) {
         const int nt = min(NT, a.ntok - c0);
-        for (int t = 0; t < nt; t++) {
-            const uint32_t *src = reinterpret_cast<const uint32_t *>(a.codes + (size_t)(c0 + t) * nb * 32);
-            for (int i = tid; i < words; i += kWG) s_codes[t * words + i] = src[i];
-            for (int i = tid; i < nb; i += kWG) {
-                s_scales[t * nb + i] = a.scales[(size_t)(c0 + t) * nb + i];
-                s_sumq[t * nb + i] = a.sumq[(size_t)(c0 + t) * nb + i];
+        {
+            // the pass's codes (consecutive tokens: one contiguous run),
+            // scales and code sums; every load issued before the stores
+            typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+            const u4 *src = reinterpret_cast<const u4 *>(a.codes + (size_t)c0 * nb * 32);
+            const int n16 = nt * words / 4;
+            constexpr int kU = 8;
+            for (int i0 = 0; i0 < n16; i0 += kU * kWG) {
+                u4 v[kU];
+#pragma unroll
+                for (int u = 0; u < kU; u++) {
+                    const int i = i0 + u * kWG + tid;
+                    if (i < n16) v[u] = src[i];
+                }
+#pragma unroll
+                for (int u = 0; u < kU; u++) {
+                    const int i = i0 + u * kWG + tid;
+                    if (i < n16) reinterpret_cast<u4 *>(s_codes)[i] = v[u];
+                }
+            }
+            for (int i = tid; i < nt * nb; i += kWG) {
+                s_scales[i] = a.scales[(size_t)c0 * nb + i];
+                s_sumq[i] = a.sumq[(size_t)c0 * nb + i];
             }
         }
         __syncthreads();
@@ -459,8 +477,12 @@ template <int MAXP>
 static hipError_t launch_q40_maxp(hipStream_t s, const Q40Args &a) {
     constexpr int NT = 8;
     size_t lds = (size_t)NT * a.nb * (32 + 4 + 4);
-    hipLaunchKernelGGL((k_q40_gemv<MAXP, NT>), dim3((a.rows + kRowsPerWG - 1) / kRowsPerWG), dim3(kWG),
-                       lds, s, a);
+    // row tiles x token passes, up to about four workgroups per CU
+    const int tiles = (a.rows + kRowsPerWG - 1) / kRowsPerWG;
+    const int passes = (a.ntok + NT - 1) / NT;
+    int gy = (1024 + tiles - 1) / tiles;
+    gy = gy < 1 ? 1 : (gy > passes ? passes : gy);
+    hipLaunchKernelGGL((k_q40_gemv<MAXP, NT>), dim3(tiles, gy), dim3(kWG), lds, s, a);
     return hipGetLastError();
 }
 
