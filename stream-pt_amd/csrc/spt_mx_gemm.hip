@@ -43,16 +43,19 @@ constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kBM = 256;               // weight rows per work item (gate/up: 128 gate + 128 up)
 constexpr int kBN = kGemmTokens;       // list entries per work item
-constexpr int kSeg = 4;                // 32-element blocks per K segment (68 bytes of a row)
-constexpr int kStages = 3;             // LDS stages; two segments are in flight while one is multiplied
+constexpr int kSeg = 8;                // 32-element blocks per K segment (136 bytes of a row)
+constexpr int kStages = 2;             // LDS stages; the next segment is in flight while one is multiplied
 // A stage: row r's window (the segment's bytes from the 16-byte boundary at
-// or below its first byte, 6 x 16 bytes) in the first 6 of the row's 8 slots
-// of 16 bytes.  (16-byte aligned loads: a load crossing the end of the
-// descriptor's range would read zeros for all its bytes.)
-constexpr int kAPieces = 6;
-constexpr int kASlots = 8;
+// or below its first byte) in 10 slots of 16 bytes (16-byte aligned loads:
+// a load crossing the end of the descriptor's range would read zeros for all
+// its bytes).  The 64 lanes of a DMA load fill 64 consecutive slots, so a
+// stage's 256 x 10 slots take 40 loads per workgroup, five per wave; loads
+// 0-19 hold rows 0-127.
+constexpr int kAPieces = 10;
+constexpr int kASlots = kAPieces;
 constexpr int kARow = 16 * kASlots;
-// B stage: per entry 16 slots of 16 bytes (4 blocks x 4 quarters of the bf16
+constexpr int kAInstr = kBM * kASlots / 64;
+// B stage: per entry 32 slots of 16 bytes (8 blocks x 4 quarters of the bf16
 // code table); quarter piece p of entry t sits in slot p ^ (t & 15), so the
 // 16 entries of an MFMA fragment read 16 different bank groups.
 constexpr int kOffB = kBM * kARow;
@@ -60,14 +63,12 @@ constexpr int kOffD = kOffB + kBN * kSeg * 64;  // d_x [entry][kSeg]
 constexpr int kStageBytes = kOffD + kBN * kSeg * 4;
 constexpr int kEMin = 4, kEMax = 240;
 constexpr uint32_t kOOR = 0x80000000u;  // buffer offset past every range: reads zero
-static_assert(kSeg * kMxBlock + 15 <= 16 * kAPieces && kAPieces <= kASlots, "A window");
-static_assert(kBM * kASlots % kThreads == 0 && kBN * kSeg * 4 % kThreads == 0, "stage loads");
-static_assert(kBN * kSeg == 32 * kWaves, "one d_x load of 32 lanes per wave");
-constexpr int kALoads = kBM * kASlots / kThreads;  // 4
-constexpr int kBLoads = kBN * kSeg * 4 / kThreads;  // 2
-// DMA loads per wave and stage (the wait counts below rely on it)
-constexpr int kStageLoads = kALoads + kBLoads + 1;
-static_assert(kStageLoads == 7, "s_waitcnt vmcnt(7) below");
+static_assert(kSeg * kMxBlock + 15 <= 16 * kAPieces, "A window");
+static_assert(kAInstr % kWaves == 0 && kBN * kSeg * 4 % kThreads == 0, "stage loads");
+static_assert(kBM / 2 * kASlots % 64 == 0, "gate rows fill whole A loads");
+static_assert(kBN * kSeg == 64 * kWaves, "one d_x load per wave");
+constexpr int kALoads = kAInstr / kWaves;           // 5
+constexpr int kBLoads = kBN * kSeg * 4 / kThreads;  // 4
 
 
 // Integer-decode dot of one weight row with one entry's Q8_0 row (the
@@ -194,12 +195,14 @@ __device__ __attribute__((always_inline)) inline void seg_full(const uint8_t *st
                 for (int r = 0; r < 4; r++) acc[rf][tf][r] = __builtin_fmaf(D[rf][tf][r], dx[j & 1][tf], acc[rf][tf][r]);
     }
 #pragma unroll
-    for (int rf = 0; rf < 2; rf++) {
-        emin[rf] = min(emin[rf], min(min(eb[0][rf], eb[1][rf]), min(eb[2][rf], eb[3][rf])));
-        emax[rf] = max(emax[rf], max(max(eb[0][rf], eb[1][rf]), max(eb[2][rf], eb[3][rf])));
-    }
+    for (int rf = 0; rf < 2; rf++)
+#pragma unroll
+        for (int j = 0; j < kSeg; j += 2) {
+            emin[rf] = min(emin[rf], min(eb[j][rf], eb[j + 1][rf]));
+            emax[rf] = max(emax[rf], max(eb[j][rf], eb[j + 1][rf]));
+        }
 }
-static_assert(kSeg == 4, "seg_full's exponent reduction");
+static_assert(kSeg % 2 == 0, "seg_full's exponent reduction");
 
 // The last segment when it holds jn < kSeg blocks.
 template <int NTF>
@@ -251,7 +254,7 @@ __device__ __attribute__((always_inline)) inline void seg_part(const uint8_t *st
 // 32w .. 32w+31.  Every wave takes all 64 entries: 2 x 4 MFMA tiles per block.
 //
 // The K loop runs over segments of kSeg blocks through kStages LDS stages
-// filled by LDS DMA loads (global/buffer -> LDS, no registers): segment s+2
+// filled by LDS DMA loads (global/buffer -> LDS, no registers): segment s+1
 // is loaded while segment s is multiplied.
 template <int MODE>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void k_mx_gemm(MxGemmArgs a) {
@@ -274,9 +277,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
     // a scalar offset)
     const u32x4v rs_b = rsrc_words(a.btab, (uint32_t)(a.tab_rows * (uint64_t)nb * 64u));
     const u32x4v rs_d = rsrc_words(a.scales, (uint32_t)(a.tab_rows * (uint64_t)nb * 4u));
-    // thread-constant part of the A loads: the piece of the row window
-    const int a_pc = tid & 7;
-    const bool a_pc_ok = a_pc < kAPieces;
     // per lane: B slot offsets of quarter g of block j for this lane's entry
     uint32_t b_lane[kSeg];
 #pragma unroll
@@ -308,21 +308,23 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
         // LDS row r -> matrix row
         auto mrow = [&](int r) { return MODE == kGateUp ? u * (kBM / 2) + (r & (kBM / 2 - 1)) : u * kBM + r; };
 
-        // this thread's DMA loads: A slots (rows tid/8 + 64k), B slots
-        // (entry (tid + 512k)/16), d_x (entry (32*wave + lane)/4)
+        // this thread's DMA loads: A load i = wave + 8k fills slots 64i..64i+63
+        // (slot q: row q / 10, piece q % 10), B slots (entry (tid + 512k)/32),
+        // d_x (entry (64*wave + lane)/8)
         uint32_t a_pos[kALoads];
         bool a_ok[kALoads];
 #pragma unroll
         for (int k = 0; k < kALoads; k++) {
-            const int r = (tid >> 3) + 64 * k;
+            const int q = 64 * (wave + kWaves * k) + lane, r = q / kASlots, pc = q - r * kASlots;
             const int row = mrow(r);
-            a_ok[k] = row < a.rows && a_pc_ok;
-            a_pos[k] = ((MODE == kGateUp && k >= kALoads / 2) ? le1 : le0) + (uint32_t)(row < a.rows ? row : 0) * row_bytes;
+            a_ok[k] = row < a.rows;
+            a_pos[k] = ((MODE == kGateUp && r >= kBM / 2) ? le1 : le0) + (uint32_t)(a_ok[k] ? row : 0) * row_bytes +
+                       16u * (uint32_t)pc;
         }
         uint32_t b_off[kBLoads];
 #pragma unroll
         for (int k = 0; k < kBLoads; k++) {
-            const int q = tid + kThreads * k, t = q >> 4, piece = (q & 15) ^ (t & 15);
+            const int q = tid + kThreads * k, t = q >> 5, piece = (q & 31) ^ (t & 15);
             int ar = 0;  // entries past nt load row 0 (unused)
             if (t < nt) {
                 const int ent = a.list[begin + t];
@@ -332,7 +334,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
         }
         uint32_t d_off = 0;
         {
-            const int idx = 32 * wave + (lane & 31), t = idx / kSeg, j = idx % kSeg;
+            const int idx = 64 * wave + lane, t = idx / kSeg, j = idx % kSeg;
             int ar = 0;
             if (t < nt) {
                 const int ent = a.list[begin + t];
@@ -342,17 +344,23 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
         }
         typedef __attribute__((address_space(3))) uint8_t lds_u8;
         const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>((lds_u8 *)lds);
-        // seven DMA loads per wave and stage (A x4, B x2, d_x x1)
+        // ten DMA loads per wave and stage (A x5, B x4, d_x x1).  The A
+        // window of segment s starts at the 16-byte boundary at or below
+        // the row's byte pos + 136s (a_pos holds pos + 16 * piece).
         auto issue = [&](int s) {
             const uint32_t st = lds0 + (uint32_t)(s % kStages) * kStageBytes;
 #pragma unroll
-            for (int k = 0; k < kALoads; k++)
-                dma16((MODE == kGateUp && k >= kALoads / 2) ? rs1 : rs0, st + 16u * (64 * wave + kThreads * k),
-                      a_ok[k] ? ((a_pos[k] + 68u * (uint32_t)s) & ~15u) + 16u * (uint32_t)a_pc : kOOR, 0u);
+            for (int k = 0; k < kALoads; k++) {
+                const int i = wave + kWaves * k;
+                const uint32_t pos = a_pos[k] + (uint32_t)(kSeg * kMxBlock) * (uint32_t)s;
+                // (pos - 16*piece) rounded down to 16, plus 16*piece
+                dma16((MODE == kGateUp && i >= kAInstr / 2) ? rs1 : rs0, st + 16u * 64u * (uint32_t)i,
+                      a_ok[k] ? (pos & ~15u) : kOOR, 0u);
+            }
 #pragma unroll
             for (int k = 0; k < kBLoads; k++)
-                dma16(rs_b, st + kOffB + 16u * (64 * wave + kThreads * k), b_off[k], 256u * (uint32_t)s);
-            if (lane < 32) dma4(rs_d, st + kOffD + 128u * wave, d_off, 16u * (uint32_t)s);
+                dma16(rs_b, st + kOffB + 16u * (64 * wave + kThreads * k), b_off[k], (uint32_t)(kSeg * 64) * (uint32_t)s);
+            dma4(rs_d, st + kOffD + 256u * wave, d_off, (uint32_t)(kSeg * 4) * (uint32_t)s);
         };
 
         // this lane's A rows: LDS row and matrix byte position (the window of
@@ -382,23 +390,19 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
         auto kloop = [&](auto ntf_c) {
             constexpr int NTF = decltype(ntf_c)::value;
             issue(0);
-            if (nseg > 1) issue(1);
             for (int s = 0; s < nseg; s++) {
-                // this wave's loads of segment s have landed (those of s+1
-                // may still fly); after the barrier every wave's have, and
-                // every wave is done with segment s-1, whose stage segment
-                // s+2 reuses
-                if (s + 1 < nseg)
-                    asm volatile("s_waitcnt vmcnt(7) lgkmcnt(0)" ::: "memory");
-                else
-                    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+                // this wave's loads of segment s have landed; after the
+                // barrier every wave's have, and every wave is done with
+                // segment s-1, whose stage segment s+1 reuses
+                asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
                 stage_barrier();
-                if (s + 2 < nseg) issue(s + 2);
+                if (s + 1 < nseg) issue(s + 1);
                 const uint8_t *st = lds + (size_t)(s % kStages) * kStageBytes;
                 const int jn = min(kSeg, nb - kSeg * s);
                 uint32_t a_img[2];
 #pragma unroll
-                for (int rf = 0; rf < 2; rf++) a_img[rf] = l_row[rf] + ((l_pos[rf] + 68u * (uint32_t)s) & 15u);
+                for (int rf = 0; rf < 2; rf++)
+                    a_img[rf] = l_row[rf] + ((l_pos[rf] + (uint32_t)(kSeg * kMxBlock) * (uint32_t)s) & 15u);
                 if (jn == kSeg)
                     seg_full<NTF>(st, a_img, b_lane, g, i16, acc, emin, emax);
                 else
