@@ -62,6 +62,7 @@ constexpr int kOffB = kBM * kARow;
 constexpr int kOffD = kOffB + kBN * kSeg * 64;  // d_x [entry][kSeg]
 constexpr int kStageBytes = kOffD + kBN * kSeg * 4;
 constexpr int kEMin = 4, kEMax = 240;
+constexpr int kXcds = 8;  // accelerator complex dies of an MI355X
 constexpr uint32_t kOOR = 0x80000000u;  // buffer offset past every range: reads zero
 static_assert(kSeg * kMxBlock + 15 <= 16 * kAPieces, "A window");
 static_assert(kAInstr % kWaves == 0 && kBN * kSeg * 4 % kThreads == 0, "stage loads");
@@ -269,7 +270,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
     const int units = (a.rows + unit_rows - 1) / unit_rows;
     const int n_slots = *a.gm_n;
     const int total = n_slots > 0 ? a.gm_tile_off[n_slots] * units : 0;
-    if ((int)blockIdx.x >= total) return;
+    // Workgroup b runs on XCD b % 8 (round-robin dispatch), each XCD with its
+    // own L2: number the workgroups XCD-major so consecutive items (the token
+    // tiles of one unit, which read the same weight rows) run on one XCD.
+    const int G = gridDim.x;
+    const int vb = (G % kXcds == 0) ? ((int)blockIdx.x % kXcds) * (G / kXcds) + (int)blockIdx.x / kXcds : (int)blockIdx.x;
+    if (vb >= total) return;
 
     const int i16 = lane & 15, g = lane >> 4;
     const int nseg = (nb + kSeg - 1) / kSeg;
@@ -282,7 +288,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
 #pragma unroll
     for (int j = 0; j < kSeg; j++) b_lane[j] = (uint32_t)i16 * (kSeg * 64) + 16u * (uint32_t)((4 * j + g) ^ i16);
 
-    for (int it = blockIdx.x; it < total; it += gridDim.x) {
+    for (int it = vb; it < total; it += G) {
         // item -> (slot, unit, token tile)
         int lo = 0, hi = n_slots - 1;
         while (lo < hi) {
