@@ -143,7 +143,14 @@ hipError_t launch_select(hipStream_t s, const float *logits, int batch, int expe
 hipError_t launch_mx_mfma(hipStream_t s, GemvMode mode, const MxMfmaArgs &a, int slots);
 // max_items: upper bound of the GEMM work items (0: nothing to launch).
 hipError_t launch_mx_gemm(hipStream_t s, GemvMode mode, const MxGemmArgs &a, int max_items);
+// Q4_0 x Q8_0 for a batch: the int8-MFMA GEMM (spt_q40_gemm.hip) from
+// kQ40GemmMinTokens tokens and kQ40GemmMinRows output rows (narrower
+// projections give it too few 64-row tiles to fill the device), else the
+// GEMV.
+constexpr int kQ40GemmMinTokens = 64;
+constexpr int kQ40GemmMinRows = 1024;
 hipError_t launch_q40_gemv(hipStream_t s, const Q40Args &a);
+hipError_t launch_q40_gemm(hipStream_t s, const Q40Args &a);
 hipError_t launch_combine(hipStream_t s, const float *results, const float *weights, int batch,
                           int topk, int hidden, float *out);
 hipError_t launch_block_sums_mx(hipStream_t s, const uint8_t *w, uint64_t nbytes, int rows, int nb,

@@ -488,6 +488,7 @@ static hipError_t launch_q40_maxp(hipStream_t s, const Q40Args &a) {
 
 hipError_t launch_q40_gemv(hipStream_t s, const Q40Args &a) {
     if (a.rows <= 0 || a.ntok <= 0) return hipSuccess;
+    if (a.ntok >= kQ40GemmMinTokens && a.rows >= kQ40GemmMinRows) return launch_q40_gemm(s, a);
     const int per_lane = (a.nb + 15) / 16;
     if (per_lane <= 1) return launch_q40_maxp<1>(s, a);
     if (per_lane <= 2) return launch_q40_maxp<2>(s, a);

@@ -1,0 +1,281 @@
+// spt_q40_gemm.hip -- Q4_0 x Q8_0 GEMM for large batches on the gfx950 int8
+// MFMA (v_mfma_i32_16x16x32_i8).
+//
+// forward.MulQ40BatchInto (forward/q40.go:40-103) for batches large enough
+// that the projection is a contraction: y[t][row] = sum_b float(isum) *
+// (d_w * d_x), with isum = sum (n - 8) * q the exact int32 block sum.  One
+// MFMA per 16 rows x 16 tokens x one block of 32: A = the weight nibbles n
+// (0..15, exact as int8), B = the Q8_0 codes, D = sum n * q exactly, so
+// isum = D - 8 * sum(q) with the per-block code sums of the quantizer; then
+// acc = fma(float(isum), d_w * d_x, acc), the GEMV's arithmetic per block.
+// K order inside a block: lane group g of the MFMA (k = 8g .. 8g+7) takes
+// nibble bytes 2+4g .. 5+4g of the block: low nibbles are elements 4g..4g+3,
+// high nibbles 16+4g..16+4g+3, matched by code dwords g and 4+g.
+// MFMA lane layout (measured on the hardware): lane l holds A row l%16 and
+// B column l%16 at k = 8*(l/16) + 0..7 (byte i of the 64-bit operand is
+// k offset i); D lane l, register r is row 4*(l/16) + r, column l%16.
+#include <type_traits>
+
+#include "spt_device.h"
+#include "spt_kernels.h"
+
+namespace spt {
+
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+constexpr int kWaves = 4;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kTR = 16 * kWaves;  // rows per workgroup (16 per wave)
+constexpr int kTN = 64;           // tokens per workgroup (4 fragments)
+constexpr int kSeg = 8;           // blocks per K segment (144 bytes of a row)
+constexpr int kAPieces = 10;      // 16-byte loads per row window (144 + 15 <= 160)
+constexpr int kARow = 176;        // LDS bytes per staged row (44 dwords: rows over distinct banks)
+constexpr int kBTok = kSeg * 32 + 16;  // LDS bytes per staged token (68 dwords)
+constexpr int kOffB = kTR * kARow;
+constexpr int kOffD = kOffB + kTN * kBTok;  // d_x [token][kSeg]
+constexpr int kOffS = kOffD + kTN * kSeg * 4;  // code sums [token][kSeg]
+constexpr int kStageBytes = kOffS + kTN * kSeg * 4;
+static_assert(kSeg * kQ40Block + 15 <= 16 * kAPieces && 16 * kAPieces <= kARow, "A window");
+constexpr int kALoads = (kTR * kAPieces + kThreads - 1) / kThreads;  // 3
+constexpr int kBLoads = kTN * kSeg * 2 / kThreads;                    // 4 (16 pieces of 16 B per token)
+constexpr int kSLoads = 2 * kTN * kSeg / kThreads;                    // 4 (d_x and sums, one dword each)
+static_assert(kTN * kSeg * 2 % kThreads == 0 && 2 * kTN * kSeg % kThreads == 0, "stage loads");
+
+// Four bytes of the stage at byte offset o (o even: Q4_0 rows are 2-byte
+// aligned): two aligned dwords and a byte shift.
+__device__ __attribute__((always_inline)) inline uint32_t word_at(const uint8_t *st, uint32_t o) {
+    const uint32_t *pw = reinterpret_cast<const uint32_t *>(st + (o & ~3u));
+    return __builtin_amdgcn_alignbyte(pw[1], pw[0], o & 3u);
+}
+
+// Blocks [j0, j1) of a stage (JN = j1 - j0 known when the segment is full)
+// for NTF token fragments: each block's LDS reads are issued one block ahead
+// of its MFMAs.
+struct Q40Lane {
+    uint32_t alead;     // LDS offset of this lane's nibble word of block 0
+    uint32_t dlead[4];  // LDS offsets of the D rows' fp16 scales of block 0
+    int i16, g;
+};
+
+template <int NTF, int JN>
+__device__ __attribute__((always_inline)) inline void q40_blocks(const uint8_t *st, const Q40Lane &L, int jn,
+                                                                 float (&acc)[4][4]) {
+    struct Blk {
+        uint32_t w4;
+        uint32_t dwb[4];
+        uint32_t bq[NTF][2];
+        float dx[NTF];
+        int s8[NTF];
+    };
+    auto fetch = [&](int j, Blk &b) {
+        b.w4 = word_at(st, L.alead + (uint32_t)j * kQ40Block);
+#pragma unroll
+        for (int r = 0; r < 4; r++) b.dwb[r] = *reinterpret_cast<const uint16_t *>(st + L.dlead[r] + (uint32_t)j * kQ40Block);
+#pragma unroll
+        for (int tf = 0; tf < NTF; tf++) {
+            const int t = 16 * tf + L.i16;
+            const uint32_t *bq = reinterpret_cast<const uint32_t *>(st + kOffB + t * kBTok + 32 * j);
+            b.bq[tf][0] = bq[L.g];
+            b.bq[tf][1] = bq[4 + L.g];
+            b.dx[tf] = *reinterpret_cast<const float *>(st + kOffD + 4 * (t * kSeg + j));
+            b.s8[tf] = 8 * *reinterpret_cast<const int32_t *>(st + kOffS + 4 * (t * kSeg + j));
+        }
+    };
+    auto run = [&](const Blk &b) {
+        const long A = (long)(b.w4 & 0x0F0F0F0Fu) | ((long)((b.w4 >> 4) & 0x0F0F0F0Fu) << 32);
+        float dw[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) dw[r] = f16_bits_to_f32(b.dwb[r]);
+        v4i D[NTF];
+#pragma unroll
+        for (int tf = 0; tf < NTF; tf++)
+            D[tf] = __builtin_amdgcn_mfma_i32_16x16x32_i8(A, (long)b.bq[tf][0] | ((long)b.bq[tf][1] << 32), v4i{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+        for (int tf = 0; tf < NTF; tf++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) acc[tf][r] = __builtin_fmaf((float)(D[tf][r] - b.s8[tf]), dw[r] * b.dx[tf], acc[tf][r]);
+    };
+    if constexpr (JN > 0) {
+        Blk cur, nxt;
+        fetch(0, cur);
+#pragma unroll
+        for (int j = 0; j < JN; j++) {
+            if (j + 1 < JN) fetch(j + 1, nxt);
+            run(cur);
+            cur = nxt;
+        }
+    } else {
+        for (int j = 0; j < jn; j++) {
+            Blk b;
+            fetch(j, b);
+            run(b);
+        }
+    }
+}
+
+}  // namespace
+
+// Workgroup (x, y): rows 64x .. 64x+63, tokens 64y .. 64y+63.  Wave w takes
+// rows 16w .. 16w+15 with all 64 tokens (four MFMA fragments per block).
+// The K loop runs over segments of kSeg blocks with two LDS stages: while a
+// segment is multiplied, the next one's loads are in flight in registers.
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void k_q40_gemm(Q40Args a) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int i16 = lane & 15, g = lane >> 4;
+    const int nb = a.nb;
+    const uint32_t row_bytes = (uint32_t)nb * kQ40Block;
+    const int r0 = blockIdx.x * kTR, t0 = blockIdx.y * kTN;
+    const int nt = min(kTN, a.ntok - t0);
+    const int ntf = (nt + 15) >> 4;
+    const int nseg = (nb + kSeg - 1) / kSeg;
+
+    // the matrix from the 16-byte boundary at or below its first byte
+    const uintptr_t wb = reinterpret_cast<uintptr_t>(a.w);
+    const uint32_t le = (uint32_t)(wb & 15u);
+    const rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void *>(wb - le), (short)0,
+                                                        (int)(uint32_t)((a.nbytes + le + 15u) & ~15ull), kRsrcWord3);
+
+    // this thread's stage loads: A pieces (row p/10, piece p%10), B pieces
+    // (token q/16, piece q%16), d_x and code sums (one dword each)
+    uint32_t a_pos[kALoads];
+    int a_r[kALoads], a_pc[kALoads];
+    bool a_ok[kALoads];
+#pragma unroll
+    for (int k = 0; k < kALoads; k++) {
+        const int p = tid + kThreads * k;
+        a_r[k] = p / kAPieces;
+        a_pc[k] = p - a_r[k] * kAPieces;
+        const int row = r0 + a_r[k];
+        a_ok[k] = p < kTR * kAPieces && row < a.rows;
+        a_pos[k] = le + (uint32_t)(a_ok[k] ? row : 0) * row_bytes;
+    }
+    u32x4 ra[kALoads], rb[kBLoads];
+    uint32_t rsx[kSLoads];
+    auto stage_load = [&](int s) {
+        const int b0 = s * kSeg;
+#pragma unroll
+        for (int k = 0; k < kALoads; k++) {
+            const uint32_t off = ((a_pos[k] + (uint32_t)b0 * kQ40Block) & ~15u) + 16u * (uint32_t)a_pc[k];
+            ra[k] = a_ok[k] ? __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0))
+                            : u32x4{0u, 0u, 0u, 0u};
+        }
+#pragma unroll
+        for (int k = 0; k < kBLoads; k++) {
+            const int q = tid + kThreads * k, t = q >> 4, pc = q & 15;
+            const int b = b0 + (pc >> 1);
+            u32x4 v = {0u, 0u, 0u, 0u};
+            if (t < nt && b < nb)
+                v = *reinterpret_cast<const u32x4 *>(a.codes + ((size_t)(t0 + t) * nb + b) * 32 + 16 * (pc & 1));
+            rb[k] = v;
+        }
+#pragma unroll
+        for (int k = 0; k < kSLoads; k++) {
+            const int q = tid + kThreads * k, which = q / (kTN * kSeg), e = q % (kTN * kSeg);
+            const int t = e / kSeg, b = b0 + e % kSeg;
+            uint32_t v = 0u;
+            if (t < nt && b < nb) {
+                const size_t o = (size_t)(t0 + t) * nb + b;
+                v = which == 0 ? __float_as_uint(a.scales[o]) : (uint32_t)a.sumq[o];
+            }
+            rsx[k] = v;
+        }
+    };
+    auto stage_store = [&](int s) {
+        uint8_t *st = lds + (size_t)(s & 1) * kStageBytes;
+#pragma unroll
+        for (int k = 0; k < kALoads; k++)
+            if (tid + kThreads * k < kTR * kAPieces) *reinterpret_cast<u32x4 *>(st + a_r[k] * kARow + 16 * a_pc[k]) = ra[k];
+#pragma unroll
+        for (int k = 0; k < kBLoads; k++) {
+            const int q = tid + kThreads * k, t = q >> 4, pc = q & 15;
+            *reinterpret_cast<u32x4 *>(st + kOffB + t * kBTok + 16 * pc) = rb[k];
+        }
+#pragma unroll
+        for (int k = 0; k < kSLoads; k++) {
+            const int q = tid + kThreads * k, which = q / (kTN * kSeg), e = q % (kTN * kSeg);
+            *reinterpret_cast<uint32_t *>(st + (which == 0 ? kOffD : kOffS) + 4 * e) = rsx[k];
+        }
+    };
+
+    // this lane's A row (MFMA layout: row i16) and D rows (4g .. 4g+3)
+    const int arow = 16 * wave + i16;
+    const uint32_t apos = le + (uint32_t)(r0 + arow < a.rows ? r0 + arow : 0) * row_bytes;
+    uint32_t dpos[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const int row = r0 + 16 * wave + 4 * g + r;
+        dpos[r] = le + (uint32_t)(row < a.rows ? row : 0) * row_bytes;
+    }
+    float acc[4][4];
+#pragma unroll
+    for (int tf = 0; tf < 4; tf++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) acc[tf][r] = 0.0f;
+
+    // The K loop, instantiated per number of token fragments.
+    auto kloop = [&](auto ntf_c) {
+        constexpr int NTF = decltype(ntf_c)::value;
+        stage_load(0);
+        stage_store(0);
+        __syncthreads();
+        for (int s = 0; s < nseg; s++) {
+            if (s + 1 < nseg) stage_load(s + 1);
+            const uint8_t *st = lds + (size_t)(s & 1) * kStageBytes;
+            const int b0 = s * kSeg, jn = min(kSeg, nb - b0);
+            // window offsets of this segment: A row (nibble bytes 2+4g..5+4g
+            // of block j at lead + 18j + 2 + 4g), and the D rows' scales
+            Q40Lane L;
+            L.alead = (uint32_t)arow * kARow + ((apos + (uint32_t)b0 * kQ40Block) & 15u) + 2u + 4u * (uint32_t)g;
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+                L.dlead[r] = (uint32_t)(16 * wave + 4 * g + r) * kARow + ((dpos[r] + (uint32_t)b0 * kQ40Block) & 15u);
+            L.i16 = i16;
+            L.g = g;
+            if (jn == kSeg)
+                q40_blocks<NTF, kSeg>(st, L, jn, acc);
+            else
+                q40_blocks<NTF, 0>(st, L, jn, acc);
+            if (s + 1 < nseg) stage_store(s + 1);
+            __syncthreads();
+        }
+    };
+    if (ntf == 4)
+        kloop(std::integral_constant<int, 4>{});
+    else if (ntf == 3)
+        kloop(std::integral_constant<int, 3>{});
+    else if (ntf == 2)
+        kloop(std::integral_constant<int, 2>{});
+    else
+        kloop(std::integral_constant<int, 1>{});
+
+    // y[t][row]: rows 4g .. 4g+3 of the wave's 16 for token 16tf + i16
+    const int row = r0 + 16 * wave + 4 * g;
+#pragma unroll
+    for (int tf = 0; tf < 4; tf++) {
+        const int t = 16 * tf + i16;
+        if (t >= nt) continue;
+        float *yp = a.y + (size_t)(t0 + t) * a.rows + row;
+        if (row + 3 < a.rows && ((reinterpret_cast<uintptr_t>(yp) & 15u) == 0)) {
+            *reinterpret_cast<v4f *>(yp) = v4f{acc[tf][0], acc[tf][1], acc[tf][2], acc[tf][3]};
+        } else {
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+                if (row + r < a.rows) yp[r] = acc[tf][r];
+        }
+    }
+}
+
+hipError_t launch_q40_gemm(hipStream_t s, const Q40Args &a) {
+    if (a.rows <= 0 || a.ntok <= 0 || a.nb <= 0) return hipSuccess;
+    dim3 grid((a.rows + kTR - 1) / kTR, (a.ntok + kTN - 1) / kTN);
+    hipLaunchKernelGGL(k_q40_gemm, grid, dim3(kThreads), 2 * (size_t)kStageBytes, s, a);
+    return hipGetLastError();
+}
+
+}  // namespace spt

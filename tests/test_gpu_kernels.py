@@ -173,8 +173,15 @@ def test_mxfp4_expert_gemv_odd_half_bias(gpu_ctx, O, bias_type):
     assert_close(y.cpu().numpy(), want, what="odd-count 2-byte bias")
 
 
-@pytest.mark.parametrize("input_dim,output_dim", [(2880, 4096), (2880, 512), (4096, 2880), (32, 17)])
-@pytest.mark.parametrize("batch", [1, 32])
+@pytest.mark.parametrize("input_dim,output_dim,batch", [
+    (2880, 4096, 1), (2880, 512, 1), (4096, 2880, 1), (32, 17, 1),
+    (2880, 4096, 32), (2880, 512, 32), (4096, 2880, 32), (32, 17, 32),
+    # the int8-MFMA GEMM (64 tokens and up): full and ragged token tiles,
+    # row counts off the 64-row tile and the 4-row stores, inputs shorter
+    # than one 8-block segment and off its multiple
+    (2880, 4096, 100), (2880, 512, 64), (4096, 2880, 70), (32, 17, 64), (96, 70, 129),
+    (288, 4, 65), (2880, 512, 512),
+])
 def test_q40_gemv(gpu_ctx, O, input_dim, output_dim, batch):
     import torch
 
