@@ -86,6 +86,8 @@ def parse():
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill workloads")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the prefill workloads (one layer resident; for counter passes)")
+    ap.add_argument("--no-lm-head", action="store_true", help="skip the Q8_0 LM head")
+    ap.add_argument("--lm-head-only", action="store_true", help="only the Q8_0 LM head (for profiles)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run a 1 GiB elementwise copy kernel three times (known "
                          "traffic for scaling hardware byte counters)")
@@ -131,6 +133,10 @@ def main():
         del src, dst
     ctx = spt.Context(0, stream.cuda_stream)
     shp = W.MoEShape()
+    if args.lm_head_only:
+        print(json.dumps({"lm_head": lm_head(ctx, stream)}), flush=True)
+        ctx.close()
+        return
     if args.prefill_only:
         layer0 = W.device_layer(ctx, args.seed, 0, shp)
         print(json.dumps({"prefill": prefill(args, ctx, layer0, shp, W, stream)}), flush=True)
@@ -223,6 +229,7 @@ def main():
         "avg_launch_us": round(head["gate_up_avg_us"], 2),
     }
     pre = None if args.no_prefill else prefill(args, ctx, layers[0], shp, W, stream)
+    lmh = None if args.no_lm_head else lm_head(ctx, stream)
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(args, shp, W)
@@ -253,6 +260,7 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
         "prefill": pre,
+        "lm_head": lmh,
     }
     print(json.dumps(line), flush=True)
     ctx.close()
@@ -363,6 +371,43 @@ def q40_projections(ctx, B, W, stream, reps):
         res[name] = round(us, 1)
         total += us
     res["total_us"] = round(total, 1)
+    return res
+
+
+def lm_head(ctx, stream, reps=20, rows=201088, input_dim=2880):
+    """The GPT-OSS LM head, 201088 x 2880 Q8_0 (615 MB; fp16 scales
+    |N(0,0.01)|, uniform int8 codes) times one fp32 token: MulQ80Into (all
+    logits) and MulQ80Argmax (best token only).  Kernel microseconds from HIP
+    events on the library's stream; algorithmic bytes = the matrix once + x
+    (+ the fp32 logits for MulQ80Into), over 8 TB/s."""
+    import torch
+
+    import spt
+    from spt import synth
+
+    wb = torch.from_numpy(synth.q80_bytes(synth.stream_key(60, 0), rows, input_dim)).cuda()
+    t = spt.Tensor.make("output.weight", spt.TYPE_Q8_0, [input_dim, rows], wb.data_ptr(), wb.numel())
+    x = torch.from_numpy(synth.normal(synth.stream_key(61, 0), input_dim)).cuda()
+    y = torch.empty(rows, dtype=torch.float32, device="cuda")
+    for _ in range(3):
+        ctx.mul_q80_into(t, x, y)
+        ctx.mul_q80_argmax(t, x)
+    torch.cuda.synchronize()
+    res = {"rows": rows, "input": input_dim, "matrix_bytes": wb.numel()}
+    for name, call, extra in (("into", lambda: ctx.mul_q80_into(t, x, y), rows * 4),
+                              ("argmax", lambda: ctx.mul_q80_argmax(t, x), 0)):
+        ctx.enable_timing(True)
+        ctx.read_timing()
+        for _ in range(reps):
+            call()
+        kt = ctx.read_timing()
+        ctx.enable_timing(False)
+        us = kt["q80"][0] / kt["q80"][1] * 1e3
+        nbytes = wb.numel() + input_dim * 4 + extra
+        gbps = nbytes / (us * 1e-6) / 1e9
+        res[name] = {"us": round(us, 1), "gbps": round(gbps, 1), "frac_hbm": round(gbps / HBM_PEAK_GBPS, 4)}
+    log(f"lm_head: {json.dumps(res)}")
+    del wb
     return res
 
 

@@ -148,7 +148,8 @@ enum {
     SPT_KERNEL_SELECT = 6,   /* top-k + softmax + per-expert packing          */
     SPT_KERNEL_GATE_UP_GEMM = 7, /* grouped gate/up GEMM (large groups)       */
     SPT_KERNEL_DOWN_GEMM = 8,    /* grouped down GEMM (large groups)          */
-    SPT_KERNEL_KINDS = 9
+    SPT_KERNEL_Q80 = 9,      /* Q8_0 LM head (GEMV or argmax)                 */
+    SPT_KERNEL_KINDS = 10
 };
 int spt_ctx_enable_timing(struct spt_ctx *ctx, int enable);
 /* Synchronise, then write the summed milliseconds and launch counts of each
@@ -186,6 +187,22 @@ int spt_mul_q40_batch_into(struct spt_ctx *ctx, const spt_tensor *w, const float
 /* Host-slice form of MulQ40BatchInto for a cgo caller holding Go slices. */
 int spt_mul_q40_batch_into_host(struct spt_ctx *ctx, const spt_tensor *w, const float *x_host,
                                 int64_t x_len, float *y_host, int64_t y_len, int64_t batch);
+
+/* forward.MulQ80Into (forward/q80.go:107-148): y = W x for a Q8_0 [in, out]
+ * matrix (the LM head) with fp32 activations, as the reference computes it
+ * (no Q8_0 of x): every row in quantQ80AVX2's order (forward/
+ * quant_amd64.go:92-116), so y matches the reference's bits.  in <= 4096;
+ * x and y must not overlap (the reference does not check; on the device an
+ * overlap is a race). */
+int spt_mul_q80_into(struct spt_ctx *ctx, const spt_tensor *w, const float *x_dev, int64_t x_len,
+                     float *y_dev, int64_t y_len);
+
+/* forward.MulQ80Argmax (forward/q80.go:20-105): the largest logit of W x and
+ * the lowest row holding it, without storing the logits.  NaN logits never
+ * win, -0 equals +0, and when no logit exceeds -Inf the result is row 0 with
+ * -Inf, as in the reference.  Synchronises; the outputs are host values. */
+int spt_mul_q80_argmax(struct spt_ctx *ctx, const spt_tensor *w, const float *x_dev, int64_t x_len,
+                       int64_t *best_token, float *best_logit);
 
 /* forward.mulMoEBatchExpert (forward/mxfp4_batch.go:29-53) for one expert of
  * an MXFP4 [in, out, experts] tensor with consecutive (not gathered) rows:

@@ -71,6 +71,11 @@ def lib():
             getattr(L, n).restype = C.c_float
         L.so_mul_q40_f32.argtypes = [u8p, f32p, f32p, C.c_int, C.c_int, C.c_int, C.c_int]
         L.so_mul_q40_f32.restype = None
+        L.so_mul_q80_f32.argtypes = [u8p, f32p, f32p, C.c_int, C.c_int, C.c_int]
+        L.so_mul_q80_f32.restype = None
+        L.so_mul_q80_argmax.argtypes = [u8p, f32p, C.c_int, C.c_int, C.c_int, C.c_int,
+                                        C.POINTER(C.c_int64), C.POINTER(C.c_float)]
+        L.so_mul_q80_argmax.restype = None
         L.so_route.argtypes = [f32p, C.c_void_p, f32p, C.c_int, C.c_int, C.c_int, f32p]
         L.so_route.restype = None
         L.so_select.argtypes = [f32p, C.c_int, C.c_int, i32p, f32p]
@@ -157,6 +162,23 @@ def mul_q40_f32(w, x, input_dim, output_dim, batch, threads=1):
     y = np.empty(batch * output_dim, np.float32)
     lib().so_mul_q40_f32(w, x, y, input_dim, output_dim, batch, threads)
     return y
+
+
+def mul_q80_f32(w, x, input_dim, output_dim, threads=1):
+    """MulQ80Into numerics: y[row] = quantQ80AVX2(row, x)."""
+    w, x = _c(w, np.uint8), _c(x, np.float32)
+    y = np.empty(output_dim, np.float32)
+    lib().so_mul_q80_f32(w, x, y, input_dim, output_dim, threads)
+    return y
+
+
+def mul_q80_argmax(w, x, input_dim, output_dim, workers=1, window_rows=0):
+    """MulQ80Argmax: (best_token, best_logit) with the reference's worker and
+    window merge (window_rows 0: one window)."""
+    w, x = _c(w, np.uint8), _c(x, np.float32)
+    tok, logit = C.c_int64(), C.c_float()
+    lib().so_mul_q80_argmax(w, x, input_dim, output_dim, workers, window_rows, C.byref(tok), C.byref(logit))
+    return tok.value, np.float32(logit.value)
 
 
 def route(router, bias, x, batch, hidden, experts):

@@ -350,6 +350,59 @@ void so_mul_q40_f32(const uint8_t *w, const float *x, float *y, int input, int o
     }
 }
 
+/* forward/q80.go:107-148 (MulQ80Into numerics): every row by quantQ80AVX2;
+ * the pair form the reference runs (quantQ80PairAVX2, quant_amd64.go:19-47)
+ * keeps each row's four chains and reduction, so the bits are the same.
+ * Rows are split over threads; partitioning does not change the bits. */
+void so_mul_q80_f32(const uint8_t *w, const float *x, float *y, int input, int output, int threads) {
+    int nb = input / 32;
+    size_t row_bytes = (size_t)nb * Q80_BLOCK;
+    if (threads < 1) threads = 1;
+#pragma omp parallel for schedule(static) num_threads(threads)
+    for (int row = 0; row < output; row++) y[row] = so_dot_q80_f32(w + (size_t)row * row_bytes, x, nb);
+}
+
+/* forward/q80.go:20-105 (MulQ80Argmax): rows in windows of window_rows rows
+ * (WithTensorChunks), each window split over min(workers, rows) workers as
+ * in workers_quant.go:42-55.  A worker scans its rows in order from (its
+ * first row, -Inf) and keeps strict maxima (q80.go:64-82); after each window
+ * the workers' results merge into the running best, which starts at
+ * (0, -Inf), by a larger logit or an equal logit with a lower token
+ * (q80.go:93-99).  Workers run one after another here; the result does not
+ * depend on their timing. */
+void so_mul_q80_argmax(const uint8_t *w, const float *x, int input, int output, int workers,
+                       int window_rows, int64_t *token, float *logit) {
+    int nb = input / 32;
+    size_t row_bytes = (size_t)nb * Q80_BLOCK;
+    if (window_rows < 1 || window_rows > output) window_rows = output;
+    if (workers < 1) workers = 1;
+    if (workers > window_rows) workers = window_rows;
+    int64_t best_t = 0;
+    float best_l = -INFINITY;
+    for (int first = 0; first < output; first += window_rows) {
+        int rows = output - first < window_rows ? output - first : window_rows;
+        int active = workers < rows ? workers : rows;
+        for (int wk = 0; wk < active; wk++) {
+            int begin = (int)((int64_t)wk * rows / active), end = (int)((int64_t)(wk + 1) * rows / active);
+            int64_t lt = first + begin;
+            float ll = -INFINITY;
+            for (int r = begin; r < end; r++) {
+                float v = so_dot_q80_f32(w + (size_t)(first + r) * row_bytes, x, nb);
+                if (v > ll) {
+                    ll = v;
+                    lt = first + r;
+                }
+            }
+            if (ll > best_l || (ll == best_l && lt < best_t)) {
+                best_l = ll;
+                best_t = lt;
+            }
+        }
+    }
+    *token = best_t;
+    *logit = best_l;
+}
+
 /* ------------------------------------------------------------------------- */
 /* Router, selection, SwiGLU, grouping                                        */
 /* ------------------------------------------------------------------------- */

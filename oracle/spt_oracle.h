@@ -62,6 +62,11 @@ float so_dot_f32_scalar(const float *w, const float *x, int n);
 void so_mul_q40_f32(const uint8_t *w, const float *x, float *y,
                     int input, int output, int batch, int threads);
 
+/* MulQ80Into / MulQ80Argmax (the LM head): rows by quantQ80AVX2. */
+void so_mul_q80_f32(const uint8_t *w, const float *x, float *y, int input, int output, int threads);
+void so_mul_q80_argmax(const uint8_t *w, const float *x, int input, int output, int workers,
+                       int window_rows, int64_t *token, float *logit);
+
 void  so_route(const float *router, const float *bias, const float *x,
                int batch, int hidden, int experts, float *logits);
 void  so_select(const float *logits, int experts, int k,

@@ -177,6 +177,35 @@ int q40_shape(const spt_tensor *t, int64_t *in, int64_t *out, int64_t *row_bytes
     return SPT_OK;
 }
 
+// q80Shape (forward/q80.go:150-171), plus this library's limits: the
+// input fits the kernel's x staging (kQ80MaxBlocks blocks), the rows are
+// 2-byte aligned and the matrix below 4 GiB.
+int q80_shape(const spt_tensor *t, int64_t *in, int64_t *out) {
+    if (t->type != SPT_TYPE_Q8_0)
+        return fail(SPT_ERR_INVALID, "\"%s\": GGML type %u instead of Q8_0 (8)", tname(t), t->type);
+    if (t->n_dims != 2) return fail(SPT_ERR_INVALID, "\"%s\": expected 2D matrix", tname(t));
+    uint64_t i = t->shape[0], o = t->shape[1];
+    if (i == 0 || o == 0 || i % 32 != 0)
+        return fail(SPT_ERR_INVALID, "\"%s\": invalid Q8_0 shape [%llu %llu]", tname(t), (unsigned long long)i,
+                    (unsigned long long)o);
+    if (i > (uint64_t)INT64_MAX || o > (uint64_t)INT64_MAX || i / 32 > (uint64_t)INT64_MAX / 34)
+        return fail(SPT_ERR_INVALID, "\"%s\": matrix dimensions exceed platform limits", tname(t));
+    uint64_t bytes = i / 32 * 34;
+    if (o > UINT64_MAX / bytes || t->nbytes == 0 || t->nbytes != o * bytes)
+        return fail(SPT_ERR_INVALID, "\"%s\": invalid byte range", tname(t));
+    if (!t->data) return fail(SPT_ERR_INVALID, "\"%s\": tensor is not resident (nil data)", tname(t));
+    if (i > (uint64_t)spt::kQ80MaxBlocks * 32)
+        return fail(SPT_ERR_INVALID, "\"%s\": Q8_0 input dimension %llu exceeds the supported %d", tname(t),
+                    (unsigned long long)i, spt::kQ80MaxBlocks * 32);
+    if ((uintptr_t)t->data & 1)
+        return fail(SPT_ERR_INVALID, "\"%s\": Q8_0 data must be 2-byte aligned", tname(t));
+    if (t->nbytes > 0xFFFFFF00ull || o > (uint64_t)INT_MAX)
+        return fail(SPT_ERR_INVALID, "\"%s\": tensor larger than 4 GiB is not supported", tname(t));
+    *in = (int64_t)i;
+    *out = (int64_t)o;
+    return SPT_OK;
+}
+
 // validateMoEBatchExpert (forward/mxfp4_batch.go:17-27).
 int validate_expert(const spt_tensor *t, int64_t input, int64_t output, int64_t experts) {
     if (t->type != SPT_TYPE_MXFP4 || t->n_dims != 3 || t->shape[0] != (uint64_t)input ||
@@ -730,6 +759,72 @@ int spt_mul_q40_batch_into_host(spt_ctx *ctx, const spt_tensor *w, const float *
     (void)hipFree(xd);
     (void)hipFree(yd);
     return rc;
+}
+
+int spt_mul_q80_into(spt_ctx *ctx, const spt_tensor *w, const float *x_dev, int64_t x_len, float *y_dev,
+                     int64_t y_len) {
+    int rc;
+    if ((rc = check_ctx(ctx))) return rc;
+    if (!w) return fail(SPT_ERR_INVALID, "nil context or reader");
+    if ((rc = check_cancel(ctx))) return rc;
+    int64_t in, out;
+    if ((rc = q80_shape(w, &in, &out))) return rc;
+    if (x_len != in || y_len != out)
+        return fail(SPT_ERR_INVALID, "\"%s\": expected input/output lengths %lld/%lld, got %lld/%lld", tname(w),
+                    (long long)in, (long long)out, (long long)x_len, (long long)y_len);
+    if (!x_dev || !y_dev) return fail(SPT_ERR_INVALID, "nil input or output");
+    if (ranges_overlap(x_dev, (uint64_t)x_len * 4, y_dev, (uint64_t)y_len * 4))
+        return fail(SPT_ERR_INVALID, "input and output must not overlap");
+    if ((rc = check_device(ctx))) return rc;
+    spt::Q80Args a{};
+    a.w = (const uint8_t *)w->data;
+    a.nbytes = w->nbytes;
+    a.rows = (int)out;
+    a.nb = (int)(in / 32);
+    a.x = x_dev;
+    a.y = y_dev;
+    SPT_HIP(timed(ctx, SPT_KERNEL_Q80, [&] { return spt::launch_q80_rows(ctx->stream, a, ctx->n_cu); }));
+    return SPT_OK;
+}
+
+int spt_mul_q80_argmax(spt_ctx *ctx, const spt_tensor *w, const float *x_dev, int64_t x_len, int64_t *best_token,
+                       float *best_logit) {
+    int rc;
+    if ((rc = check_ctx(ctx))) return rc;
+    if (!w) return fail(SPT_ERR_INVALID, "nil reader");
+    if ((rc = check_cancel(ctx))) return rc;
+    int64_t in, out;
+    if ((rc = q80_shape(w, &in, &out))) return rc;
+    if (x_len != in)
+        return fail(SPT_ERR_INVALID, "\"%s\": expected %lld input elements, got %lld", tname(w), (long long)in,
+                    (long long)x_len);
+    if (!x_dev || !best_token || !best_logit) return fail(SPT_ERR_INVALID, "nil input or output");
+    if ((rc = check_device(ctx))) return rc;
+    const int waves = spt::q80_grid_waves((int)out, (int)(in / 32), ctx->n_cu);
+    Carve c;
+    const size_t o_v = c.take((size_t)waves * 4), o_i = c.take((size_t)waves * 4), o_out = c.take(8);
+    char *S;
+    if ((rc = scratch(ctx, c.off, &S))) return rc;
+    spt::Q80Args a{};
+    a.w = (const uint8_t *)w->data;
+    a.nbytes = w->nbytes;
+    a.rows = (int)out;
+    a.nb = (int)(in / 32);
+    a.x = x_dev;
+    a.part_v = (float *)(S + o_v);
+    a.part_i = (int32_t *)(S + o_i);
+    a.out_v = (float *)(S + o_out);
+    a.out_i = (int32_t *)(S + o_out + 4);
+    SPT_HIP(timed(ctx, SPT_KERNEL_Q80, [&] { return spt::launch_q80_rows(ctx->stream, a, ctx->n_cu); }));
+    struct {
+        float v;
+        int32_t i;
+    } res;
+    SPT_HIP(hipMemcpyAsync(&res, S + o_out, sizeof res, hipMemcpyDeviceToHost, ctx->stream));
+    SPT_HIP(hipStreamSynchronize(ctx->stream));
+    *best_token = res.i;
+    *best_logit = res.v;
+    return SPT_OK;
 }
 
 int spt_mul_mxfp4_expert(spt_ctx *ctx, const spt_tensor *w, const spt_tensor *bias, int32_t expert,

@@ -27,6 +27,31 @@ constexpr int kRsrcWord3 = 0x00020000;
 
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
 
+// Raw buffer descriptor as four dwords (for inline assembly).
+typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+
+// LDS DMA load (buffer -> LDS, no registers): lane l's `bytes` land at LDS
+// address lds + bytes * l.  Issued with inline assembly so that the
+// compiler, which cannot tell which stage an LDS read touches, does not
+// wait for every load in flight before each LDS read; the kernel waits for
+// them itself (s_waitcnt vmcnt in stage order).  Five wait
+// states open each load: M0, the descriptor and the offset may have just
+// been written (by SALU, or by VALU for SGPRs), which an LDS DMA must not see
+// early, and the compiler cannot pad inside inline assembly.
+__device__ inline void dma16(const u32x4v &rs, uint32_t lds, uint32_t voff, uint32_t soff) {
+    asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(rs), "s"(soff), "{m0}"(lds)
+                 : "memory");
+}
+__device__ inline void dma4(const u32x4v &rs, uint32_t lds, uint32_t voff, uint32_t soff) {
+    asm volatile("s_nop 4\n\tbuffer_load_dword %0, %1, %2 offen lds" ::"v"(voff), "s"(rs), "s"(soff), "{m0}"(lds)
+                 : "memory");
+}
+
+__device__ inline u32x4v rsrc_words(const void *base, uint32_t nbytes) {
+    const uint64_t b = reinterpret_cast<uint64_t>(base);
+    return u32x4v{(uint32_t)b, (uint32_t)(b >> 32) & 0xFFFFu, nbytes, (uint32_t)kRsrcWord3};
+}
+
 // A bounds-checked view of `nbytes` bytes at `p`: the descriptor base is p
 // rounded down to 4 bytes and `lead` (0..3) is p's offset inside it, so every
 // dword load stays aligned; dwords wholly past the end read as zero.

@@ -129,6 +129,25 @@ struct Q40Args {
     float *y;
 };
 
+// Q8_0 [in, out] x fp32 x (the LM head, spt_q80_head.hip): y = W x, or with
+// part_v set the argmax of W x -- per-wave (logit, row) into part_v / part_i
+// (q80_grid_waves entries), merged into *out_v / *out_i.
+constexpr int kQ80MaxBlocks = 128;  // input <= 4096
+struct Q80Args {
+    const uint8_t *w;
+    uint64_t nbytes;
+    int rows;
+    int nb;
+    const float *x;
+    float *y;
+    float *part_v;
+    int32_t *part_i;
+    float *out_v;
+    int32_t *out_i;
+    int rows_per_chunk;  // set by the launcher
+    int chunks;
+};
+
 hipError_t launch_quantize(hipStream_t s, const float *x, int64_t nblocks, int8_t *codes,
                            float *scales, int32_t *sumq, uint8_t *mxtab, uint8_t *blocks34,
                            uint32_t *btab);
@@ -151,6 +170,8 @@ constexpr int kQ40GemmMinTokens = 64;
 constexpr int kQ40GemmMinRows = 1024;
 hipError_t launch_q40_gemv(hipStream_t s, const Q40Args &a);
 hipError_t launch_q40_gemm(hipStream_t s, const Q40Args &a);
+int q80_grid_waves(int rows, int nb, int n_cu);
+hipError_t launch_q80_rows(hipStream_t s, const Q80Args &a, int n_cu);
 hipError_t launch_combine(hipStream_t s, const float *results, const float *weights, int batch,
                           int topk, int hidden, float *out);
 hipError_t launch_block_sums_mx(hipStream_t s, const uint8_t *w, uint64_t nbytes, int rows, int nb,

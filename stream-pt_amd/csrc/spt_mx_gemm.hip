@@ -91,7 +91,6 @@ __device__ float lut_dot(const ByteView &v, uint32_t row_pos, int nb, const int8
     return acc;
 }
 
-typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
 
 // Descriptor of expert e's matrix from the 16-byte boundary at or below its
 // first byte to the one at or above its end (a 16-byte load crossing the
@@ -103,28 +102,6 @@ __device__ inline u32x4v expert_rsrc(const uint8_t *w, uint64_t expert_bytes, in
     const uint64_t b = mb - *le;
     return u32x4v{(uint32_t)b, (uint32_t)(b >> 32) & 0xFFFFu, (uint32_t)((expert_bytes + *le + 15u) & ~15ull),
                   (uint32_t)kRsrcWord3};
-}
-
-// LDS DMA load (buffer -> LDS, no registers): lane l's `bytes` land at LDS
-// address lds + bytes * l.  Issued with inline assembly so that the
-// compiler, which cannot tell which stage an LDS read touches, does not
-// wait for every load in flight before each LDS read; the kernel waits for
-// them itself (s_waitcnt vmcnt in stage order, then a barrier).  Five wait
-// states open each load: M0, the descriptor and the offset may have just
-// been written (by SALU, or by VALU for SGPRs), which an LDS DMA must not see
-// early, and the compiler cannot pad inside inline assembly.
-__device__ inline void dma16(const u32x4v &rs, uint32_t lds, uint32_t voff, uint32_t soff) {
-    asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(rs), "s"(soff), "{m0}"(lds)
-                 : "memory");
-}
-__device__ inline void dma4(const u32x4v &rs, uint32_t lds, uint32_t voff, uint32_t soff) {
-    asm volatile("s_nop 4\n\tbuffer_load_dword %0, %1, %2 offen lds" ::"v"(voff), "s"(rs), "s"(soff), "{m0}"(lds)
-                 : "memory");
-}
-
-__device__ inline u32x4v rsrc_words(const void *base, uint32_t nbytes) {
-    const uint64_t b = reinterpret_cast<uint64_t>(base);
-    return u32x4v{(uint32_t)b, (uint32_t)(b >> 32) & 0xFFFFu, nbytes, (uint32_t)kRsrcWord3};
 }
 
 // Workgroup barrier that leaves the LDS DMA loads in flight: the caller has

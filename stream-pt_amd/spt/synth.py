@@ -83,6 +83,22 @@ def q40_bytes(key: int, rows: int, input_dim: int, scale_std: float = 0.01) -> n
     return out.reshape(-1)
 
 
+def q80_bytes(key: int, rows: int, input_dim: int, scale_std: float = 0.01) -> np.ndarray:
+    """Q8_0 matrix [rows][input/32 blocks of 34 B]: fp16 scale |N(0, std)|,
+    uniform int8 codes.  Drawn from numpy's PCG64 seeded with the key (fast
+    enough for a 615 MB LM head), so also a pure function of the key."""
+    nb = rows * (input_dim // 32)
+    rng = np.random.Generator(np.random.PCG64(key))
+    out = np.empty((nb, 34), np.uint8)
+    step = 1 << 22
+    for b0 in range(0, nb, step):
+        n = min(step, nb - b0)
+        d = np.abs(rng.standard_normal(n, dtype=np.float32) * np.float32(scale_std)).astype(np.float16)
+        out[b0:b0 + n, 0:2] = d.view(np.uint8).reshape(n, 2)
+        out[b0:b0 + n, 2:] = rng.integers(0, 256, size=(n, 32), dtype=np.uint8)
+    return out.reshape(-1)
+
+
 def zipf_logits(key: int, batch: int, experts: int, s: float = 1.1,
                 hot_fraction: float = 0.0, hot_expert: int = 0) -> np.ndarray:
     """Router logits under which top-k selection samples experts without

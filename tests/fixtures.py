@@ -3,8 +3,23 @@ formulas (the reference writes them to a temp file; here they are arrays).
 
 moe_batch_fixture: tests/testdata/forward/moe_batch_test.go:20-111
 moe_batch_x:       tests/testdata/forward/moe_batch_test.go:134-139
+quant_optimization_fixture:
+                   tests/testdata/forward/quant_optimization_test.go:25-56
 """
 import numpy as np
+
+def quant_optimization_fixture(typ, input_dim, output_dim):
+    """Q4_0 (typ 2) or Q8_0 (typ 8) [input, output] bytes: block g's fp16
+    scale cycles through eight values (normal, negative, subnormal, the
+    largest finite, -0), byte j of its payload is (13g + 7(j+2)) & 0xFF."""
+    bb = 18 if typ == 2 else 34
+    nblk = input_dim // 32 * output_dim
+    scales = np.array([0x3C00, 0xB800, 0x3400, 0x0001, 0x03FF, 0x0400, 0x7BFF, 0x8000], np.uint16)
+    data = np.zeros((nblk, bb), np.uint8)
+    data[:, 0:2] = scales[np.arange(nblk) % 8].view(np.uint8).reshape(nblk, 2)
+    data[:, 2:] = ((np.arange(nblk)[:, None] * 13 + np.arange(2, bb)[None, :] * 7) & 0xFF).astype(np.uint8)
+    return data.reshape(-1)
+
 
 ROUTER_MODES = ("normal", "ties", "nonfinite", "mixed-nan", "infinite", "underflow", "clamp")
 

@@ -164,6 +164,49 @@ def test_q40_validation(vctx):
     assert b"overlap" in spt.lib().spt_last_error()
 
 
+def _q80(inp=64, out=3, nbytes=None, shape=None, typ=None):
+    return spt.Tensor.make("output.weight", spt.TYPE_Q8_0 if typ is None else typ,
+                           [inp, out] if shape is None else shape, 0x40000000,
+                           inp // 32 * 34 * out if nbytes is None else nbytes)
+
+
+def test_q80_validation(vctx):
+    """q80Shape (forward/q80.go:150-171) and the length checks of MulQ80Into
+    / MulQ80Argmax (q80.go:37-39,114-116); TestQuantOptimizationQ80ShapeOverflow
+    (quant_optimization_test.go:368-374)."""
+    L = spt.lib()
+    tok, logit = C.c_int64(), C.c_float()
+
+    def into(w, xl, yl, x=X, y=OUT):
+        return L.spt_mul_q80_into(vctx.handle, C.byref(w), x, xl, y, yl)
+
+    def argmax(w, xl):
+        return L.spt_mul_q80_argmax(vctx.handle, C.byref(w), X, xl, C.byref(tok), C.byref(logit))
+
+    assert into(_q80(), 64, 3) == spt.ERR_DEVICE
+    assert argmax(_q80(), 64) == spt.ERR_DEVICE
+    bad = [
+        (_q80(typ=spt.TYPE_Q4_0), b"instead of Q8_0 (8)"),
+        (_q80(shape=[64]), b"expected 2D matrix"),
+        (_q80(inp=48, nbytes=34 * 3), b"invalid Q8_0 shape"),
+        (_q80(shape=[32, 2 ** 64 - 1], nbytes=34), b"exceed platform limits"),
+        (_q80(nbytes=205), b"byte range"),
+        (_q80(inp=4128, out=1), b"exceeds the supported 4096"),
+    ]
+    for w, msg in bad:
+        xl = w.shape[0] if w.n_dims >= 1 else 64
+        for rc in (into(w, xl, 3), argmax(w, xl)):
+            assert rc == spt.ERR_INVALID
+            assert msg in L.spt_last_error(), L.spt_last_error()
+    assert into(_q80(), 63, 3) == spt.ERR_INVALID
+    assert b"expected input/output lengths 64/3, got 63/3" in L.spt_last_error()
+    assert into(_q80(), 64, 1) == spt.ERR_INVALID
+    assert argmax(_q80(), 32) == spt.ERR_INVALID
+    assert b"expected 64 input elements, got 32" in L.spt_last_error()
+    assert into(_q80(), 64, 3, x=X, y=X + 8) == spt.ERR_INVALID
+    assert b"overlap" in L.spt_last_error()
+
+
 def test_quantize_validation(vctx):
     L = spt.lib()
     assert L.spt_quantize_q8_0(vctx.handle, X, 33, OUT) == spt.ERR_INVALID

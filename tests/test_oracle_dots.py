@@ -17,6 +17,8 @@ import math
 import numpy as np
 import pytest
 
+from fixtures import quant_optimization_fixture
+
 LEVELS64 = np.array([0, .5, 1, 1.5, 2, 3, 4, 6, 0, -.5, -1, -1.5, -2, -3, -4, -6], np.float64)
 
 
@@ -152,21 +154,11 @@ def test_quant_float16_scales(O, typ):
             assert got == want, hex(s)
 
 
-def _quant_fixture(typ, input_dim, output_dim):
-    bb = 18 if typ == 2 else 34
-    nblk = input_dim // 32 * output_dim
-    scales = np.array([0x3C00, 0xB800, 0x3400, 0x0001, 0x03FF, 0x0400, 0x7BFF, 0x8000], np.uint16)
-    data = np.zeros((nblk, bb), np.uint8)
-    data[:, 0:2] = scales[np.arange(nblk) % 8].view(np.uint8).reshape(nblk, 2)
-    data[:, 2:] = ((np.arange(nblk)[:, None] * 13 + np.arange(2, bb)[None, :] * 7) & 0xFF).astype(np.uint8)
-    return data.reshape(-1)
-
-
 @pytest.mark.parametrize("typ", [2, 8])
 @pytest.mark.parametrize("input_dim", [32, 96, 512])
 def test_quant_numerics(O, typ, input_dim):
     output_dim = 17
-    data = _quant_fixture(typ, input_dim, output_dim)
+    data = quant_optimization_fixture(typ, input_dim, output_dim)
     x = ((np.arange(input_dim) % 23) - 11).astype(np.float32) / 32
     bb = 18 if typ == 2 else 34
     rb = input_dim // 32 * bb
