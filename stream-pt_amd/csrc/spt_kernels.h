@@ -144,8 +144,6 @@ struct Q80Args {
     int32_t *part_i;
     float *out_v;
     int32_t *out_i;
-    int rows_per_chunk;  // set by the launcher
-    int chunks;
 };
 
 hipError_t launch_quantize(hipStream_t s, const float *x, int64_t nblocks, int8_t *codes,

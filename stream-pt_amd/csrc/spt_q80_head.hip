@@ -6,18 +6,19 @@
 // block, c_e = fma(float(q_e) * d, x[32b + e], c_e) over the blocks in order
 // -- and ends with t_s = ((c_s + c_{8+s}) + c_{16+s}) + c_{24+s},
 // p_i = t_i + t_{i+4}, y = (p_0 + p_1) + (p_2 + p_3) (quantQ80AVX2 and
-// quantSumAVX2, forward/quant_amd64.go:92-116).  Here a half-wave takes a
-// row, lane e owning chain e, so every row's bits equal the reference's.
+// quantSumAVX2, forward/quant_amd64.go:92-116).  Here 8 lanes take a row,
+// lane j owning chains 4j .. 4j+3 (per block: two code pairs, one fp16 scale
+// and one float4 of x), so every row's bits equal the reference's.
 // float(q) * d is exact (at most 8 x 11 significant bits, never subnormal);
 // v_fma_mix_f32(q, d, -0.0) forms it from the fp16 bits in one instruction
 // (adding -0.0 leaves every product, -0.0 included, unchanged).
 //
-// Memory: the matrix is read once, in chunks of whole consecutive rows (as
-// many as fit in kChunkBytes) that a wave loads into its own LDS buffers by
-// LDS DMA, kBufs - 1 chunks in flight while one is multiplied; x is staged
-// once per workgroup in LDS.  Waves take chunks w, w + W, w + 2W, ... of the
-// grid's W waves.  The argmax form keeps each wave's best (logit, row) and a
-// one-workgroup pass merges them.
+// Memory: the matrix is read once.  A wave takes tiles of 8 consecutive
+// rows (tiles w, w + W, ... of the grid's W waves) and walks each tile's K
+// in segments of kSeg blocks; a segment's 8 row windows are loaded into the
+// wave's own LDS stage by LDS DMA, kBufs - 1 segments in flight while one is
+// multiplied.  x is staged once per workgroup in LDS.  The argmax form keeps
+// each wave's best (logit, row) and a one-workgroup pass merges them.
 #include "spt_device.h"
 #include "spt_kernels.h"
 
@@ -27,12 +28,17 @@ namespace {
 
 constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;
-constexpr int kChunkInstr = 6;                    // 1 KiB LDS DMA loads per chunk
-constexpr int kChunkBytes = 1024 * kChunkInstr;   // two rows of 2880 inputs (2 x 3060 + 15)
-constexpr int kBufs = 3;
-constexpr uint32_t kOOR = 0xFFFFFFF0u;            // an offset past every descriptor's range
-constexpr int kUnroll = 8;
-constexpr int kMaxChunkRows = 64;                 // a chunk's y values fit one store (one per lane)
+constexpr int kTileRows = 8;                                          // 8 lanes per row
+constexpr int kSeg = 9;                                               // blocks per K segment (90 = 10 x 9)
+constexpr int kPieces = (15 + kSeg * kQ80Block + 15) / 16;            // 16-byte loads per row window
+constexpr int kSlot = 16 * kPieces;                                   // LDS bytes per row in a stage
+constexpr int kSegInstr = (kTileRows * kPieces + 63) / 64;            // LDS DMA loads per segment
+constexpr int kStageBytes = 1024 * kSegInstr;
+constexpr int kBufs = 4;
+constexpr int kGroup = 3;                                             // blocks per LDS read group
+constexpr uint32_t kOOR = 0xFFFFFFF0u;                                // past every descriptor's range
+static_assert(kSeg % kGroup == 0, "segment of whole groups");
+static_assert(kBufs - 1 <= 3, "the store count of the wait covers three units");
 
 // float(q) * fp16(dbits) exactly.
 __device__ __attribute__((always_inline)) inline float q80_weight(int q, uint32_t dbits, float neg_zero) {
@@ -50,6 +56,45 @@ __device__ __attribute__((always_inline)) inline void argmax_take(float v, int i
     }
 }
 
+// One block of a lane's four chains: codes 4j, 4j+1 in qa, 4j+2, 4j+3 in qb.
+__device__ __attribute__((always_inline)) inline void q80_block(uint32_t qa, uint32_t qb, uint32_t d, float4 x,
+                                                                float nz, float (&c)[4]) {
+    c[0] = __builtin_fmaf(q80_weight((int)(int8_t)(qa & 0xFFu), d, nz), x.x, c[0]);
+    c[1] = __builtin_fmaf(q80_weight((int)(int8_t)(qa >> 8), d, nz), x.y, c[1]);
+    c[2] = __builtin_fmaf(q80_weight((int)(int8_t)(qb & 0xFFu), d, nz), x.z, c[2]);
+    c[3] = __builtin_fmaf(q80_weight((int)(int8_t)(qb >> 8), d, nz), x.w, c[3]);
+}
+
+struct Q80Grp {
+    uint32_t qa[kGroup], qb[kGroup], d[kGroup];
+    float4 x[kGroup];
+};
+
+// A full segment: kSeg / kGroup groups, each group's LDS reads issued while
+// the previous group is multiplied (two register sets, no copies).
+__device__ __attribute__((always_inline)) inline void q80_segment(const uint16_t *qp, const uint16_t *dp,
+                                                                  const float4 *xp, float nz, float (&c)[4]) {
+    constexpr int kNG = kSeg / kGroup;
+    Q80Grp g[2];
+    auto fetch = [&](int gi, Q80Grp &t) {
+#pragma unroll
+        for (int k = 0; k < kGroup; k++) {
+            const int b = kGroup * gi + k;
+            t.qa[k] = qp[(kQ80Block / 2) * b];
+            t.qb[k] = qp[(kQ80Block / 2) * b + 1];
+            t.d[k] = dp[(kQ80Block / 2) * b];
+            t.x[k] = xp[8 * b];
+        }
+    };
+    fetch(0, g[0]);
+#pragma unroll
+    for (int gi = 0; gi < kNG; gi++) {
+        if (gi + 1 < kNG) fetch(gi + 1, g[(gi + 1) & 1]);
+#pragma unroll
+        for (int k = 0; k < kGroup; k++) q80_block(g[gi & 1].qa[k], g[gi & 1].qb[k], g[gi & 1].d[k], g[gi & 1].x[k], nz, c);
+    }
+}
+
 }  // namespace
 
 template <bool ARGMAX>
@@ -58,108 +103,137 @@ __global__ __launch_bounds__(kThreads) void k_q80_rows(Q80Args a) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wl = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int gw = blockIdx.x * kWaves + wl, nw = gridDim.x * kWaves;
-    const int half = lane >> 5, e = lane & 31;
-    const int nb = a.nb;
+    const int rg = lane >> 3, j = lane & 7;  // row of the tile, chain quad
+    const int nb = a.nb, rows = a.rows;
     const uint32_t rb = (uint32_t)nb * kQ80Block;
-    const int R = a.rows_per_chunk;
+    const int nseg = (nb + kSeg - 1) / kSeg;
+    const int tiles = (rows + kTileRows - 1) / kTileRows;
+    const int units = gw < tiles ? ((tiles - gw + nw - 1) / nw) * nseg : 0;
 
     // x for the workgroup: x[32b + e] at 128b + 4e
     float *xs = reinterpret_cast<float *>(lds);
     for (int i = tid; i < 32 * nb; i += kThreads) xs[i] = a.x[i];
-    uint8_t *bufs = lds + 128 * nb + wl * (kBufs * kChunkBytes);
+    uint8_t *stages = lds + 128 * nb + wl * (kBufs * kStageBytes);
 
     typedef __attribute__((address_space(3))) uint8_t lds_u8;
-    const uint32_t buf0 = (uint32_t)reinterpret_cast<uintptr_t>((lds_u8 *)bufs);
+    const uint32_t st0 = (uint32_t)reinterpret_cast<uintptr_t>((lds_u8 *)stages);
     const uintptr_t wb = reinterpret_cast<uintptr_t>(a.w);
     const uint32_t le = (uint32_t)(wb & 15u);
     const u32x4v rs = rsrc_words(reinterpret_cast<const void *>(wb - le), (uint32_t)((a.nbytes + le + 15u) & ~15ull));
-    const int mine = gw < a.chunks ? (a.chunks - gw + nw - 1) / nw : 0;
 
-    // chunk c's rows [c*R, c*R + R) as 16-byte pieces from the boundary at
-    // or below their first byte; pieces at or past the rows' end are not read
-    auto issue = [&](int i) {
-        const int c = gw + i * nw;
-        const uint32_t start = le + (uint32_t)c * (uint32_t)R * rb;
-        const uint32_t end = le + (uint32_t)min((uint64_t)(c + 1) * (uint64_t)R * rb, a.nbytes);
-        const uint32_t base = start & ~15u;
-        const uint32_t buf = buf0 + (uint32_t)(i % kBufs) * kChunkBytes;
+    // this lane's pieces: load i covers piece (64i + lane) % kPieces of row
+    // (64i + lane) / kPieces of the tile
+    int prow[kSegInstr], pk[kSegInstr];
 #pragma unroll
-        for (int k = 0; k < kChunkInstr; k++) {
-            const uint32_t off = base + 16u * (uint32_t)(64 * k + lane);
-            dma16(rs, buf + 1024u * (uint32_t)k, off < end ? off : kOOR, 0u);
+    for (int i = 0; i < kSegInstr; i++) {
+        const int p = 64 * i + lane;
+        prow[i] = p / kPieces;
+        pk[i] = p - prow[i] * kPieces;
+    }
+    // Units are (tile, segment) pairs in order: segment sg of tile t, the
+    // tiles gw, gw + nw, ...  A row's window starts at the 16-byte boundary
+    // at or below its segment's first byte; pieces past the segment's end
+    // are not read.  The issue position runs kBufs - 1 units ahead.
+    int it = gw, isg = 0, iu = 0;
+    auto issue = [&]() {
+        const int t = it, sg = isg;
+        const uint32_t seg0 = (uint32_t)(kSeg * kQ80Block) * (uint32_t)sg;
+        const uint32_t seg1 = min(seg0 + (uint32_t)(kSeg * kQ80Block), rb);
+        const uint32_t st = st0 + (uint32_t)(iu % kBufs) * kStageBytes;
+        if (++isg == nseg) {
+            isg = 0;
+            it += nw;
+        }
+        iu++;
+#pragma unroll
+        for (int i = 0; i < kSegInstr; i++) {
+            const int row = kTileRows * t + prow[i];
+            const uint32_t rpos = le + (uint32_t)row * rb;
+            const uint32_t off = ((rpos + seg0) & ~15u) + 16u * (uint32_t)pk[i];
+            const bool ok = prow[i] < kTileRows && row < rows && off < rpos + seg1;
+            dma16(rs, st + 1024u * (uint32_t)i, ok ? off : kOOR, 0u);
         }
     };
-    for (int i = 0; i < kBufs - 1 && i < mine; i++) issue(i);
+    for (int u = 0; u < kBufs - 1 && u < units; u++) issue();
     __syncthreads();  // x staged
 
     const float nz = -0.0f;
     float best_v = -__builtin_inff();
     int best_i = 0;
-    for (int i = 0; i < mine; i++) {
-        // Wait for chunk i.  Memory operations complete in issue order for
-        // the counter, so the wait names how many may stay outstanding:
-        // the later chunks' loads and, for y, the one store of each earlier
-        // chunk that was issued after chunk i's loads (chunks i-2 and i-1).
-        if (i + kBufs - 1 < mine) {
-            issue(i + kBufs - 1);
-            constexpr int kLater = (kBufs - 1) * kChunkInstr;
-            static_assert(kBufs == 3, "the store counts below assume two chunks in flight");
-            if (ARGMAX || i == 0)
-                asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kLater) : "memory");
-            else if (i == 1)
-                asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kLater + 1) : "memory");
-            else
-                asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kLater + 2) : "memory");
+    float c[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // chains 4j .. 4j+3 of row rg
+    // y of MulQ80Into: lane 8k + r collects row r of the wave's tile 8m + k
+    // (m counting groups of eight tiles); one store per eight tiles
+    float yv = 0.0f;
+    int yrow = -1;
+    int t = gw, sg = 0, ti = 0;
+    for (int u = 0; u < units; u++) {
+        // Wait for unit u: with the kBufs - 1 later units' loads issued, at
+        // most that many loads may stay outstanding.  Loads complete in
+        // issue order, so this holds whether or not stores issued in between
+        // have completed.
+        if (u + kBufs - 1 < units) {
+            issue();
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"((kBufs - 1) * kSegInstr) : "memory");
         } else {
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         }
-        const int c = gw + i * nw;
-        const int r0 = c * R, nr = min(R, a.rows - r0);
-        const uint8_t *cb = bufs + (i % kBufs) * kChunkBytes + ((le + (uint32_t)r0 * rb) & 15u);
-        float yv = 0.0f;  // lane j: row r0 + j
-        for (int p = 0; p < nr; p += 2) {
-            const int rr = p + half;
-            const uint8_t *rowp = cb + (rr < nr ? rr : p) * rb;
-            const int8_t *qp = reinterpret_cast<const int8_t *>(rowp + 2 + e);
-            const uint16_t *dp = reinterpret_cast<const uint16_t *>(rowp);
-            const float *xp = xs + e;
-            float acc = 0.0f;
-            int b = 0;
-            for (; b + kUnroll <= nb; b += kUnroll) {
+        const int row = kTileRows * t + rg;
+        const int b0 = kSeg * sg, jn = min(kSeg, nb - b0);
+        const uint8_t *rowp = stages + (u % kBufs) * kStageBytes + kSlot * rg +
+                              ((le + (uint32_t)row * rb + (uint32_t)(b0 * kQ80Block)) & 15u);
+        const uint16_t *qp = reinterpret_cast<const uint16_t *>(rowp + 2 + 4 * j);
+        const uint16_t *dp = reinterpret_cast<const uint16_t *>(rowp);
+        const float4 *xp = reinterpret_cast<const float4 *>(xs + 32 * b0) + j;
+        if (jn == kSeg) {
+            q80_segment(qp, dp, xp, nz, c);
+        } else {
+            for (int b = 0; b < jn; b++)
+                q80_block(qp[(kQ80Block / 2) * b], qp[(kQ80Block / 2) * b + 1], dp[(kQ80Block / 2) * b], xp[8 * b],
+                          nz, c);
+        }
+        if (sg == nseg - 1) {
+            // t_{4m+k} at lane m < 2 of the row: chains 4m+k + 8, 16, 24 sit
+            // in lanes m + 2, 4, 6; p_k = t_k + t_{k+4} (lanes 0 and 1)
+            float pk4[4];
 #pragma unroll
-                for (int j = 0; j < kUnroll; j++) {
-                    const float w = q80_weight(qp[kQ80Block * (b + j)], dp[(kQ80Block / 2) * (b + j)], nz);
-                    acc = __builtin_fmaf(w, xp[32 * (b + j)], acc);
+            for (int k = 0; k < 4; k++) {
+                const float tk = ((c[k] + __shfl_down(c[k], 2, 8)) + __shfl_down(c[k], 4, 8)) + __shfl_down(c[k], 6, 8);
+                pk4[k] = tk + __shfl_down(tk, 1, 8);
+                c[k] = 0.0f;
+            }
+            const float y = (pk4[0] + pk4[1]) + (pk4[2] + pk4[3]);
+            if constexpr (ARGMAX) {
+                // lane 8r keeps the best of row r across the wave's tiles
+                if (j == 0 && row < rows) argmax_take(y, row, best_v, best_i);
+            } else {
+#pragma unroll
+                for (int r = 0; r < kTileRows; r++) {
+                    const float yr =
+                        __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, y), 8 * r));
+                    const bool mine_r = lane == 8 * (ti & 7) + r;
+                    yv = mine_r ? yr : yv;
+                    yrow = mine_r ? kTileRows * t + r : yrow;
+                }
+                if ((ti & 7) == 7 || u + 1 == units) {
+                    if (yrow >= 0 && yrow < rows) a.y[yrow] = yv;
+                    yrow = -1;
                 }
             }
-            for (; b < nb; b++) {
-                const float w = q80_weight(qp[kQ80Block * b], dp[(kQ80Block / 2) * b], nz);
-                acc = __builtin_fmaf(w, xp[32 * b], acc);
-            }
-            // chains e, e+8, e+16, e+24 -> t_e (e < 8); then the pairwise sum
-            const float c8 = __shfl_down(acc, 8, 32), c16 = __shfl_down(acc, 16, 32), c24 = __shfl_down(acc, 24, 32);
-            const float t = ((acc + c8) + c16) + c24;
-            const float pr = t + __shfl_down(t, 4, 32);
-            const float qd = pr + __shfl_down(pr, 1, 32);
-            const float y = qd + __shfl_down(qd, 2, 32);
-            const float y0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, y), 0));
-            const float y1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, y), 32));
-            if constexpr (ARGMAX) {
-                argmax_take(y0, r0 + p, best_v, best_i);
-                if (p + 1 < nr) argmax_take(y1, r0 + p + 1, best_v, best_i);
-            } else {
-                yv = lane == p ? y0 : yv;
-                yv = lane == p + 1 ? y1 : yv;
-            }
+            ti++;
+            t += nw;
         }
-        if constexpr (!ARGMAX) {
-            if (lane < nr) a.y[r0 + lane] = yv;
-        }
+        if (++sg == nseg) sg = 0;
     }
     if constexpr (ARGMAX) {
+        float bv = -__builtin_inff();
+        int bi = 0;
+#pragma unroll
+        for (int r = 0; r < kTileRows; r++)
+            argmax_take(__builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, best_v), 8 * r)),
+                        __builtin_amdgcn_readlane(best_i, 8 * r), bv, bi);
         if (lane == 0) {
-            a.part_v[gw] = best_v;
-            a.part_i[gw] = best_i;
+            a.part_v[gw] = bv;
+            a.part_i[gw] = bi;
         }
     }
 }
@@ -191,24 +265,16 @@ __global__ __launch_bounds__(1024) void k_q80_argmax_merge(const float *part_v, 
     }
 }
 
-static int q80_rows_per_chunk(int nb) {
-    const int rb = nb * kQ80Block;
-    return min(kMaxChunkRows, (kChunkBytes - 15) / rb);
-}
-
 int q80_grid_waves(int rows, int nb, int n_cu) {
-    const int chunks = (rows + q80_rows_per_chunk(nb) - 1) / q80_rows_per_chunk(nb);
-    const int wgs = min((chunks + kWaves - 1) / kWaves, max(n_cu, 1));
+    (void)nb;
+    const int tiles = (rows + kTileRows - 1) / kTileRows;
+    const int wgs = min((tiles + kWaves - 1) / kWaves, max(n_cu, 1));
     return wgs * kWaves;
 }
 
-hipError_t launch_q80_rows(hipStream_t s, const Q80Args &a0, int n_cu) {
-    if (a0.nb < 1 || a0.nb > kQ80MaxBlocks || a0.rows < 1) return hipErrorInvalidValue;
-    Q80Args a = a0;
-    a.rows_per_chunk = q80_rows_per_chunk(a.nb);
-    a.chunks = (a.rows + a.rows_per_chunk - 1) / a.rows_per_chunk;
-    const int waves = q80_grid_waves(a.rows, a.nb, n_cu);
-    constexpr size_t kMaxLds = (size_t)128 * kQ80MaxBlocks + (size_t)kWaves * kBufs * kChunkBytes;
+hipError_t launch_q80_rows(hipStream_t s, const Q80Args &a, int n_cu) {
+    if (a.nb < 1 || a.nb > kQ80MaxBlocks || a.rows < 1) return hipErrorInvalidValue;
+    constexpr size_t kMaxLds = (size_t)128 * kQ80MaxBlocks + (size_t)kWaves * kBufs * kStageBytes;
     static_assert(kMaxLds <= 160 * 1024, "LDS");
     static const hipError_t attr = [] {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_q80_rows<false>),
@@ -219,7 +285,8 @@ hipError_t launch_q80_rows(hipStream_t s, const Q80Args &a0, int n_cu) {
         return e;
     }();
     if (attr != hipSuccess) return attr;
-    const size_t lds = (size_t)128 * a.nb + (size_t)kWaves * kBufs * kChunkBytes;
+    const int waves = q80_grid_waves(a.rows, a.nb, n_cu);
+    const size_t lds = (size_t)128 * a.nb + (size_t)kWaves * kBufs * kStageBytes;
     if (a.part_v) {
         hipLaunchKernelGGL(k_q80_rows<true>, dim3(waves / kWaves), dim3(kThreads), lds, s, a);
         hipError_t err = hipGetLastError();
