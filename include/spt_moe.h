@@ -204,6 +204,13 @@ int spt_mul_q80_into(struct spt_ctx *ctx, const spt_tensor *w, const float *x_de
 int spt_mul_q80_argmax(struct spt_ctx *ctx, const spt_tensor *w, const float *x_dev, int64_t x_len,
                        int64_t *best_token, float *best_logit);
 
+/* Host-slice forms of MulQ80Into / MulQ80Argmax for a cgo caller holding Go
+ * slices (forward/engine.go:223,228 pass the final hidden state). */
+int spt_mul_q80_into_host(struct spt_ctx *ctx, const spt_tensor *w, const float *x_host, int64_t x_len,
+                          float *y_host, int64_t y_len);
+int spt_mul_q80_argmax_host(struct spt_ctx *ctx, const spt_tensor *w, const float *x_host,
+                            int64_t x_len, int64_t *best_token, float *best_logit);
+
 /* forward.mulMoEBatchExpert (forward/mxfp4_batch.go:29-53) for one expert of
  * an MXFP4 [in, out, experts] tensor with consecutive (not gathered) rows:
  * y[t*out + row] = dot(W_e[row], x[t*in:]) + bias_e[row], t < batch.

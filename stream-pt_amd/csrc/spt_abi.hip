@@ -827,6 +827,54 @@ int spt_mul_q80_argmax(spt_ctx *ctx, const spt_tensor *w, const float *x_dev, in
     return SPT_OK;
 }
 
+int spt_mul_q80_into_host(spt_ctx *ctx, const spt_tensor *w, const float *x_host, int64_t x_len, float *y_host,
+                          int64_t y_len) {
+    int rc;
+    if ((rc = check_ctx(ctx))) return rc;
+    if (!w) return fail(SPT_ERR_INVALID, "nil context or reader");
+    int64_t in, out;
+    if ((rc = q80_shape(w, &in, &out))) return rc;
+    if (x_len != in || y_len != out)
+        return fail(SPT_ERR_INVALID, "\"%s\": expected input/output lengths %lld/%lld, got %lld/%lld", tname(w),
+                    (long long)in, (long long)out, (long long)x_len, (long long)y_len);
+    if (!x_host || !y_host) return fail(SPT_ERR_INVALID, "nil input or output");
+    if ((rc = check_device(ctx))) return rc;
+    void *xd = nullptr, *yd = nullptr;
+    if ((rc = spt_alloc(ctx, (uint64_t)x_len * 4, &xd))) return rc;
+    if ((rc = spt_alloc(ctx, (uint64_t)y_len * 4, &yd))) {
+        (void)hipFree(xd);
+        return rc;
+    }
+    rc = spt_copy_h2d(ctx, xd, x_host, (uint64_t)x_len * 4);
+    if (!rc) rc = spt_mul_q80_into(ctx, w, (const float *)xd, x_len, (float *)yd, y_len);
+    if (!rc) rc = spt_copy_d2h(ctx, y_host, yd, (uint64_t)y_len * 4);
+    (void)hipStreamSynchronize(ctx->stream);
+    (void)hipFree(xd);
+    (void)hipFree(yd);
+    return rc;
+}
+
+int spt_mul_q80_argmax_host(spt_ctx *ctx, const spt_tensor *w, const float *x_host, int64_t x_len,
+                            int64_t *best_token, float *best_logit) {
+    int rc;
+    if ((rc = check_ctx(ctx))) return rc;
+    if (!w) return fail(SPT_ERR_INVALID, "nil reader");
+    int64_t in, out;
+    if ((rc = q80_shape(w, &in, &out))) return rc;
+    if (x_len != in)
+        return fail(SPT_ERR_INVALID, "\"%s\": expected %lld input elements, got %lld", tname(w), (long long)in,
+                    (long long)x_len);
+    if (!x_host || !best_token || !best_logit) return fail(SPT_ERR_INVALID, "nil input or output");
+    if ((rc = check_device(ctx))) return rc;
+    void *xd = nullptr;
+    if ((rc = spt_alloc(ctx, (uint64_t)x_len * 4, &xd))) return rc;
+    rc = spt_copy_h2d(ctx, xd, x_host, (uint64_t)x_len * 4);
+    if (!rc) rc = spt_mul_q80_argmax(ctx, w, (const float *)xd, x_len, best_token, best_logit);
+    (void)hipStreamSynchronize(ctx->stream);
+    (void)hipFree(xd);
+    return rc;
+}
+
 int spt_mul_mxfp4_expert(spt_ctx *ctx, const spt_tensor *w, const spt_tensor *bias, int32_t expert,
                          const float *x_dev, int64_t x_len, float *y_dev, int64_t y_len, int64_t batch) {
     int rc;

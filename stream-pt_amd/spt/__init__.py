@@ -30,7 +30,7 @@ EXPORTED = (
     "spt_forward_moe", "spt_forward_moe_batch", "spt_forward_moe_batch_ex",
     "spt_forward_moe_batch_host", "spt_block_sums", "spt_synth_mxfp4",
     "spt_ctx_enable_timing", "spt_ctx_read_timing", "spt_ctx_set_gemm_min_group",
-    "spt_mul_q80_into", "spt_mul_q80_argmax",
+    "spt_mul_q80_into", "spt_mul_q80_argmax", "spt_mul_q80_into_host", "spt_mul_q80_argmax_host",
 )
 KERNEL_KINDS = ("quantize", "route", "gate_up", "down", "combine", "q40", "select", "gate_up_gemm", "down_gemm",
                 "q80")
@@ -113,6 +113,8 @@ def lib():
         "spt_mul_q40_batch_into_host": ([vp, T, vp, i64, vp, i64, i64], C.c_int),
         "spt_mul_q80_into": ([vp, T, vp, i64, vp, i64], C.c_int),
         "spt_mul_q80_argmax": ([vp, T, vp, i64, C.POINTER(C.c_int64), C.POINTER(C.c_float)], C.c_int),
+        "spt_mul_q80_into_host": ([vp, T, vp, i64, vp, i64], C.c_int),
+        "spt_mul_q80_argmax_host": ([vp, T, vp, i64, C.POINTER(C.c_int64), C.POINTER(C.c_float)], C.c_int),
         "spt_mul_mxfp4_expert": ([vp, T, T, i32, vp, i64, vp, i64, i64], C.c_int),
         "spt_route_moe_batch": ([vp, T, T, vp, i64, vp], C.c_int),
         "spt_forward_moe": ([vp, C.POINTER(MoEConfig), C.POINTER(MoELayer), vp, i64, vp, i64], C.c_int),
@@ -237,6 +239,15 @@ class Context:
         tok, logit = C.c_int64(), C.c_float()
         _check(lib().spt_mul_q80_argmax(self.handle, C.byref(w), _ptr(x), _numel(x), C.byref(tok),
                                         C.byref(logit)))
+        return tok.value, logit.value
+
+    def mul_q80_into_host(self, w: Tensor, x, y):
+        _check(lib().spt_mul_q80_into_host(self.handle, C.byref(w), _ptr(x), _numel(x), _ptr(y), _numel(y)))
+
+    def mul_q80_argmax_host(self, w: Tensor, x):
+        tok, logit = C.c_int64(), C.c_float()
+        _check(lib().spt_mul_q80_argmax_host(self.handle, C.byref(w), _ptr(x), _numel(x), C.byref(tok),
+                                             C.byref(logit)))
         return tok.value, logit.value
 
     def mul_mxfp4_expert(self, w: Tensor, bias, expert: int, x, y, batch: int):

@@ -62,6 +62,22 @@ def test_q80_rows_bit_exact(gpu_ctx, O, input_dim, output_dim):
     _same_argmax((tok, logit), O.mul_q80_argmax(w, x, input_dim, output_dim))
 
 
+def test_q80_host_forms(gpu_ctx, O):
+    """The host-slice entry points give the device forms' results."""
+    from spt import synth
+
+    input_dim, rows = 2880, 3001
+    w = synth.q80_bytes(synth.stream_key(46, 0), rows, input_dim)
+    x = synth.normal(synth.stream_key(47, 0), input_dim)
+    wd = _dev(w)
+    t = _tensor(wd, input_dim, rows)
+    y = np.zeros(rows, np.float32)
+    gpu_ctx.mul_q80_into_host(t, x, y)
+    _same_bits(y, O.mul_q80_f32(w, x, input_dim, rows))
+    tok, logit = gpu_ctx.mul_q80_argmax_host(t, x)
+    _same_argmax((tok, np.float32(logit)), O.mul_q80_argmax(w, x, input_dim, rows))
+
+
 @pytest.mark.parametrize("input_dim", [32, 2880])
 def test_q80_reference_fixture(gpu_ctx, O, input_dim):
     """quantOptimizationFixture rows (scales 1, -0.5, subnormal, the largest
