@@ -134,7 +134,7 @@ def main():
     ctx = spt.Context(0, stream.cuda_stream)
     shp = W.MoEShape()
     if args.lm_head_only:
-        print(json.dumps({"lm_head": lm_head(ctx, stream)}), flush=True)
+        print(json.dumps({"lm_head": lm_head(ctx, stream), "rmsnorm_q8": rmsnorm_rows(ctx, stream)}), flush=True)
         ctx.close()
         return
     if args.prefill_only:
@@ -230,6 +230,7 @@ def main():
     }
     pre = None if args.no_prefill else prefill(args, ctx, layers[0], shp, W, stream)
     lmh = None if args.no_lm_head else lm_head(ctx, stream)
+    rms = None if args.no_lm_head else rmsnorm_rows(ctx, stream)
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(args, shp, W)
@@ -261,6 +262,7 @@ def main():
         "cpu_baseline": cpu,
         "prefill": pre,
         "lm_head": lmh,
+        "rmsnorm_q8": rms,
     }
     print(json.dumps(line), flush=True)
     ctx.close()
@@ -408,6 +410,38 @@ def lm_head(ctx, stream, reps=20, rows=201088, input_dim=2880):
         res[name] = {"us": round(us, 1), "gbps": round(gbps, 1), "frac_hbm": round(gbps / HBM_PEAK_GBPS, 4)}
     log(f"lm_head: {json.dumps(res)}")
     del wb
+    return res
+
+
+def rmsnorm_rows(ctx, stream, reps=50, dim=2880):
+    """The fused RMSNorm + Q8_0 of B rows of 2880 (normBatch order; F32
+    weights), B = 1, 64, 512: microseconds per call (HIP events on the
+    library's stream) and the bytes moved (x, y, Q8_0 and the weights) per
+    microsecond."""
+    import torch
+
+    import spt
+    from spt import synth
+
+    w = torch.from_numpy(synth.normal(synth.stream_key(90, 0), dim)).cuda()
+    t = spt.Tensor.make("norm.weight", spt.TYPE_F32, [dim], w.data_ptr(), dim * 4)
+    res = {}
+    for B in (1, 64, 512):
+        x = torch.from_numpy(synth.normal(synth.stream_key(91, B), B * dim)).cuda()
+        y = torch.empty_like(x)
+        q = torch.empty(B * dim // 32 * 34, dtype=torch.uint8, device="cuda")
+        for _ in range(3):
+            ctx.rmsnorm_batch_into(t, x, y, B, 1e-5, q)
+        ctx.enable_timing(True)
+        ctx.read_timing()
+        for _ in range(reps):
+            ctx.rmsnorm_batch_into(t, x, y, B, 1e-5, q)
+        kt = ctx.read_timing()
+        ctx.enable_timing(False)
+        us = kt["rmsnorm"][0] / kt["rmsnorm"][1] * 1e3
+        nbytes = B * dim * 8 + B * dim // 32 * 34 + dim * 4
+        res[str(B)] = {"us": round(us, 2), "gbps": round(nbytes / (us * 1e-6) / 1e9, 1)}
+    log(f"rmsnorm_q8: {json.dumps(res)}")
     return res
 
 

@@ -149,7 +149,8 @@ enum {
     SPT_KERNEL_GATE_UP_GEMM = 7, /* grouped gate/up GEMM (large groups)       */
     SPT_KERNEL_DOWN_GEMM = 8,    /* grouped down GEMM (large groups)          */
     SPT_KERNEL_Q80 = 9,      /* Q8_0 LM head (GEMV or argmax)                 */
-    SPT_KERNEL_KINDS = 10
+    SPT_KERNEL_RMSNORM = 10, /* RMSNorm (+ Q8_0 of its output)                */
+    SPT_KERNEL_KINDS = 11
 };
 int spt_ctx_enable_timing(struct spt_ctx *ctx, int enable);
 /* Synchronise, then write the summed milliseconds and launch counts of each
@@ -210,6 +211,24 @@ int spt_mul_q80_into_host(struct spt_ctx *ctx, const spt_tensor *w, const float 
                           float *y_host, int64_t y_len);
 int spt_mul_q80_argmax_host(struct spt_ctx *ctx, const spt_tensor *w, const float *x_host,
                             int64_t x_len, int64_t *best_token, float *best_logit);
+
+/* forward.RMSNormInto (forward/rmsnorm.go:19-167): y = x * w * factor,
+ * factor = 1 / sqrt(mean(x^2) + epsilon), with the reference's sum order (an
+ * 8-float simd width), so y matches its bits.  weight: F32 (0), F16 (1) or
+ * BF16 (28) [len(x)].  y may be x itself but may not partially overlap it.
+ * q8_dev: NULL, or len(x)/32 GGML Q8_0 blocks (34 bytes) that receive the
+ * Q8_0 of y -- the input format of the MoE and Q4_0 operators (the rule of
+ * spt_quantize_q8_0); no reference counterpart (the fused quantization). */
+int spt_rmsnorm_into(struct spt_ctx *ctx, const spt_tensor *weight, const float *x_dev, int64_t x_len,
+                     float *y_dev, int64_t y_len, float epsilon, void *q8_dev);
+
+/* normBatch (forward/layer_batch.go:139-195): batch rows of len(x)/batch
+ * in normBatch's order (one 8-lane accumulator per row, so the bits can
+ * differ from spt_rmsnorm_into's by rounding, as in the reference), with
+ * the same optional Q8_0 output. */
+int spt_rmsnorm_batch_into(struct spt_ctx *ctx, const spt_tensor *weight, const float *x_dev,
+                           int64_t x_len, float *y_dev, int64_t y_len, int64_t batch, float epsilon,
+                           void *q8_dev);
 
 /* forward.mulMoEBatchExpert (forward/mxfp4_batch.go:29-53) for one expert of
  * an MXFP4 [in, out, experts] tensor with consecutive (not gathered) rows:

@@ -76,6 +76,10 @@ def lib():
         L.so_mul_q80_argmax.argtypes = [u8p, f32p, C.c_int, C.c_int, C.c_int, C.c_int,
                                         C.POINTER(C.c_int64), C.POINTER(C.c_float)]
         L.so_mul_q80_argmax.restype = None
+        L.so_rmsnorm_f32.argtypes = [f32p, f32p, C.c_int, C.c_float, f32p]
+        L.so_rmsnorm_f32.restype = None
+        L.so_rmsnorm_batch_f32.argtypes = [f32p, f32p, C.c_int, C.c_int, C.c_float, f32p]
+        L.so_rmsnorm_batch_f32.restype = None
         L.so_route.argtypes = [f32p, C.c_void_p, f32p, C.c_int, C.c_int, C.c_int, f32p]
         L.so_route.restype = None
         L.so_select.argtypes = [f32p, C.c_int, C.c_int, i32p, f32p]
@@ -179,6 +183,33 @@ def mul_q80_argmax(w, x, input_dim, output_dim, workers=1, window_rows=0):
     tok, logit = C.c_int64(), C.c_float()
     lib().so_mul_q80_argmax(w, x, input_dim, output_dim, workers, window_rows, C.byref(tok), C.byref(logit))
     return tok.value, np.float32(logit.value)
+
+
+def rmsnorm_f32(x, w, eps):
+    """RMSNormInto numerics (one vector)."""
+    x, w = _c(x, np.float32), _c(w, np.float32)
+    y = np.empty_like(x)
+    lib().so_rmsnorm_f32(x, w, x.size, eps, y)
+    return y
+
+
+def rmsnorm_batch_f32(x, w, batch, eps):
+    """normBatch numerics (batch consecutive vectors of len(w))."""
+    x, w = _c(x, np.float32), _c(w, np.float32)
+    y = np.empty_like(x)
+    lib().so_rmsnorm_batch_f32(x, w, w.size, batch, eps, y)
+    return y
+
+
+def decode_norm_weight(raw, typ):
+    """F32 (0), F16 (1) or BF16 (28 / 30) vector bytes -> float32."""
+    raw = np.ascontiguousarray(raw, np.uint8)
+    if typ == 0:
+        return raw.view(np.float32).copy()
+    h = raw.view(np.uint16)
+    if typ == 1:
+        return h.view(np.float16).astype(np.float32)
+    return (h.astype(np.uint32) << 16).view(np.float32)
 
 
 def route(router, bias, x, batch, hidden, experts):

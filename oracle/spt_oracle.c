@@ -403,6 +403,54 @@ void so_mul_q80_argmax(const uint8_t *w, const float *x, int input, int output, 
     *logit = best_l;
 }
 
+/* forward/rmsnorm.go:59-97,152-164 (RMSNormInto) with the simd width of the
+ * AVX2 build (8 float lanes): four accumulators over 32-element chunks
+ * (MulAdd = FMA), combined ((a0+a1)+a2)+a3, then 8-element chunks into the
+ * combined vector (a partial last chunk zero-filled), the eight lanes summed
+ * in order into a float from 0, factor = 1 / float32(sqrt(float64(sum / n +
+ * eps))), y = (x * w) * factor.  w is the decoded weight vector. */
+void so_rmsnorm_f32(const float *x, const float *w, int n, float eps, float *y) {
+    float sq[4][8] = {{0}};
+    int off = 0;
+    for (; off + 32 <= n; off += 32)
+        for (int a = 0; a < 4; a++)
+            for (int s = 0; s < 8; s++) {
+                float v = x[off + 8 * a + s];
+                sq[a][s] = fmaf(v, v, sq[a][s]);
+            }
+    float lanes[8];
+    for (int s = 0; s < 8; s++) lanes[s] = ((sq[0][s] + sq[1][s]) + sq[2][s]) + sq[3][s];
+    for (; off < n; off += 8)
+        for (int s = 0; s < 8; s++) {
+            float v = off + s < n ? x[off + s] : 0.0f;
+            lanes[s] = fmaf(v, v, lanes[s]);
+        }
+    float sum = 0.0f;
+    for (int s = 0; s < 8; s++) sum += lanes[s];
+    float factor = 1.0f / (float)sqrt((double)(sum / (float)n + eps));
+    for (int i = 0; i < n; i++) y[i] = (x[i] * w[i]) * factor;
+}
+
+/* forward/layer_batch.go:139-195 (normBatch): per item one accumulator over
+ * 8-element chunks (a partial last chunk zero-filled), then the same sum,
+ * factor and products as so_rmsnorm_f32. */
+void so_rmsnorm_batch_f32(const float *x, const float *w, int dim, int batch, float eps, float *y) {
+    for (int t = 0; t < batch; t++) {
+        const float *in = x + (size_t)t * dim;
+        float *out = y + (size_t)t * dim;
+        float lanes[8] = {0};
+        for (int off = 0; off < dim; off += 8)
+            for (int s = 0; s < 8; s++) {
+                float v = off + s < dim ? in[off + s] : 0.0f;
+                lanes[s] = fmaf(v, v, lanes[s]);
+            }
+        float sum = 0.0f;
+        for (int s = 0; s < 8; s++) sum += lanes[s];
+        float factor = 1.0f / (float)sqrt((double)(sum / (float)dim + eps));
+        for (int i = 0; i < dim; i++) out[i] = (in[i] * w[i]) * factor;
+    }
+}
+
 /* ------------------------------------------------------------------------- */
 /* Router, selection, SwiGLU, grouping                                        */
 /* ------------------------------------------------------------------------- */

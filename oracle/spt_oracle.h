@@ -67,6 +67,10 @@ void so_mul_q80_f32(const uint8_t *w, const float *x, float *y, int input, int o
 void so_mul_q80_argmax(const uint8_t *w, const float *x, int input, int output, int workers,
                        int window_rows, int64_t *token, float *logit);
 
+/* RMSNormInto / normBatch (AVX2 lane order); w = decoded weights. */
+void so_rmsnorm_f32(const float *x, const float *w, int n, float eps, float *y);
+void so_rmsnorm_batch_f32(const float *x, const float *w, int dim, int batch, float eps, float *y);
+
 void  so_route(const float *router, const float *bias, const float *x,
                int batch, int hidden, int experts, float *logits);
 void  so_select(const float *logits, int experts, int k,

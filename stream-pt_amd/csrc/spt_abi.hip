@@ -206,6 +206,48 @@ int q80_shape(const spt_tensor *t, int64_t *in, int64_t *out) {
     return SPT_OK;
 }
 
+// The normalization weight of RMSNormInto (forward/rmsnorm.go:42-58) and
+// normBatch (forward/layer_batch.go:145-155): F32 (0), F16 (1) or BF16 (28),
+// one element per input; *wtype is the kernel's encoding (0, 1, 2).
+int norm_weight_check(const spt_tensor *w, int64_t dim, bool batch_form, int *wtype) {
+    uint64_t width;
+    switch (w->type) {
+        case SPT_TYPE_F32: width = 4; *wtype = 0; break;
+        case SPT_TYPE_F16: width = 2; *wtype = 1; break;
+        case 28: width = 2; *wtype = 2; break;
+        default:
+            return fail(SPT_ERR_INVALID, "\"%s\": unsupported normalization weight type %u", tname(w), w->type);
+    }
+    if (batch_form) {
+        if (w->n_dims != 1 || w->shape[0] != (uint64_t)dim || w->nbytes != width * (uint64_t)dim)
+            return fail(SPT_ERR_INVALID, "\"%s\": invalid float vector shape or range", tname(w));
+    } else {
+        if ((uint64_t)dim > (uint64_t)INT64_MAX / width)
+            return fail(SPT_ERR_INVALID, "\"%s\": normalization weight exceeds platform limits", tname(w));
+        if (w->nbytes == 0 || w->nbytes != (uint64_t)dim * width)
+            return fail(SPT_ERR_INVALID, "\"%s\": invalid weight data length", tname(w));
+    }
+    if (!w->data) return fail(SPT_ERR_INVALID, "\"%s\": tensor is not resident (nil data)", tname(w));
+    if ((uintptr_t)w->data & (width - 1))
+        return fail(SPT_ERR_INVALID, "\"%s\": weight data must be %llu-byte aligned", tname(w),
+                    (unsigned long long)width);
+    return SPT_OK;
+}
+
+bool bad_epsilon(float e) { return e < 0.0f || e != e || e == __builtin_inff(); }
+
+// The Q8_0 output of the fused normalization: whole blocks, apart from x and y.
+int norm_q8_check(const void *q8, int64_t total, const float *x, const float *y) {
+    if (!q8) return SPT_OK;
+    if (total % 32 != 0)
+        return fail(SPT_ERR_INVALID, "Q8_0 output needs a dimension that is a multiple of 32, got %lld",
+                    (long long)total);
+    const uint64_t qb = (uint64_t)total / 32 * 34;
+    if (ranges_overlap(q8, qb, x, (uint64_t)total * 4) || (y && ranges_overlap(q8, qb, y, (uint64_t)total * 4)))
+        return fail(SPT_ERR_INVALID, "Q8_0 output overlaps the input or output");
+    return SPT_OK;
+}
+
 // validateMoEBatchExpert (forward/mxfp4_batch.go:17-27).
 int validate_expert(const spt_tensor *t, int64_t input, int64_t output, int64_t experts) {
     if (t->type != SPT_TYPE_MXFP4 || t->n_dims != 3 || t->shape[0] != (uint64_t)input ||
@@ -873,6 +915,55 @@ int spt_mul_q80_argmax_host(spt_ctx *ctx, const spt_tensor *w, const float *x_ho
     (void)hipStreamSynchronize(ctx->stream);
     (void)hipFree(xd);
     return rc;
+}
+
+int spt_rmsnorm_into(spt_ctx *ctx, const spt_tensor *weight, const float *x_dev, int64_t x_len, float *y_dev,
+                     int64_t y_len, float epsilon, void *q8_dev) {
+    int rc;
+    if ((rc = check_ctx(ctx))) return rc;
+    if (!weight) return fail(SPT_ERR_INVALID, "nil GGUF reader");
+    if ((rc = check_cancel(ctx))) return rc;
+    if (x_len <= 0 || y_len != x_len || weight->n_dims != 1 || weight->shape[0] != (uint64_t)x_len)
+        return fail(SPT_ERR_INVALID, "\"%s\": normalization weight, input, and output dimensions differ",
+                    tname(weight));
+    if (!x_dev || !y_dev) return fail(SPT_ERR_INVALID, "nil input or output");
+    if (x_dev != y_dev && ranges_overlap(x_dev, (uint64_t)x_len * 4, y_dev, (uint64_t)y_len * 4))
+        return fail(SPT_ERR_INVALID, "input and output partially overlap");
+    if (bad_epsilon(epsilon)) return fail(SPT_ERR_INVALID, "invalid epsilon: %g", (double)epsilon);
+    int wtype;
+    if ((rc = norm_weight_check(weight, x_len, false, &wtype))) return rc;
+    if ((rc = norm_q8_check(q8_dev, x_len, x_dev, y_dev))) return rc;
+    if (x_len > INT_MAX) return fail(SPT_ERR_INVALID, "input of %lld elements is too long", (long long)x_len);
+    if ((rc = check_device(ctx))) return rc;
+    spt::RmsArgs a{x_dev, weight->data, wtype, (int)x_len, 1, epsilon, y_dev, (uint8_t *)q8_dev};
+    SPT_HIP(timed(ctx, SPT_KERNEL_RMSNORM, [&] { return spt::launch_rmsnorm(ctx->stream, a, false); }));
+    return SPT_OK;
+}
+
+int spt_rmsnorm_batch_into(spt_ctx *ctx, const spt_tensor *weight, const float *x_dev, int64_t x_len, float *y_dev,
+                           int64_t y_len, int64_t batch, float epsilon, void *q8_dev) {
+    int rc;
+    if ((rc = check_ctx(ctx))) return rc;
+    if (!weight) return fail(SPT_ERR_INVALID, "nil GGUF reader");
+    if ((rc = check_cancel(ctx))) return rc;
+    if (bad_epsilon(epsilon)) return fail(SPT_ERR_INVALID, "invalid epsilon: %g", (double)epsilon);
+    if (batch < 1 || x_len <= 0 || x_len % batch != 0 || y_len != x_len)
+        return fail(SPT_ERR_INVALID, "invalid batch %lld for %lld input and %lld output elements", (long long)batch,
+                    (long long)x_len, (long long)y_len);
+    const int64_t dim = x_len / batch;
+    int wtype;
+    if ((rc = norm_weight_check(weight, dim, true, &wtype))) return rc;
+    if (!x_dev || !y_dev) return fail(SPT_ERR_INVALID, "nil input or output");
+    if (x_dev != y_dev && ranges_overlap(x_dev, (uint64_t)x_len * 4, y_dev, (uint64_t)y_len * 4))
+        return fail(SPT_ERR_INVALID, "input and output partially overlap");
+    if ((rc = norm_q8_check(q8_dev, x_len, x_dev, y_dev))) return rc;
+    if (dim > INT_MAX || batch > INT_MAX)
+        return fail(SPT_ERR_INVALID, "invalid batch %lld for %lld input and %lld output elements", (long long)batch,
+                    (long long)x_len, (long long)y_len);
+    if ((rc = check_device(ctx))) return rc;
+    spt::RmsArgs a{x_dev, weight->data, wtype, (int)dim, (int)batch, epsilon, y_dev, (uint8_t *)q8_dev};
+    SPT_HIP(timed(ctx, SPT_KERNEL_RMSNORM, [&] { return spt::launch_rmsnorm(ctx->stream, a, true); }));
+    return SPT_OK;
 }
 
 int spt_mul_mxfp4_expert(spt_ctx *ctx, const spt_tensor *w, const spt_tensor *bias, int32_t expert,

@@ -169,6 +169,20 @@ constexpr int kQ40GemmMinRows = 1024;
 hipError_t launch_q40_gemv(hipStream_t s, const Q40Args &a);
 hipError_t launch_q40_gemm(hipStream_t s, const Q40Args &a);
 int q80_grid_waves(int rows, int nb, int n_cu);
+// RMSNorm of `batch` rows of n (spt_rmsnorm.hip): y = x * w * factor in the
+// lane order of RMSNormInto, or of normBatch with batch_order; with q8 set,
+// also the GGML Q8_0 blocks of y (n % 32 == 0).  y may equal x.
+struct RmsArgs {
+    const float *x;
+    const void *w;
+    int wtype;  // 0 F32, 1 F16, 2 BF16
+    int n;
+    int batch;
+    float eps;
+    float *y;
+    uint8_t *q8;
+};
+hipError_t launch_rmsnorm(hipStream_t s, const RmsArgs &a, bool batch_order);
 hipError_t launch_q80_rows(hipStream_t s, const Q80Args &a, int n_cu);
 hipError_t launch_combine(hipStream_t s, const float *results, const float *weights, int batch,
                           int topk, int hidden, float *out);

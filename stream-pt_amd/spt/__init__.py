@@ -31,9 +31,10 @@ EXPORTED = (
     "spt_forward_moe_batch_host", "spt_block_sums", "spt_synth_mxfp4",
     "spt_ctx_enable_timing", "spt_ctx_read_timing", "spt_ctx_set_gemm_min_group",
     "spt_mul_q80_into", "spt_mul_q80_argmax", "spt_mul_q80_into_host", "spt_mul_q80_argmax_host",
+    "spt_rmsnorm_into", "spt_rmsnorm_batch_into",
 )
 KERNEL_KINDS = ("quantize", "route", "gate_up", "down", "combine", "q40", "select", "gate_up_gemm", "down_gemm",
-                "q80")
+                "q80", "rmsnorm")
 
 
 class SptError(RuntimeError):
@@ -114,6 +115,8 @@ def lib():
         "spt_mul_q80_into": ([vp, T, vp, i64, vp, i64], C.c_int),
         "spt_mul_q80_argmax": ([vp, T, vp, i64, C.POINTER(C.c_int64), C.POINTER(C.c_float)], C.c_int),
         "spt_mul_q80_into_host": ([vp, T, vp, i64, vp, i64], C.c_int),
+        "spt_rmsnorm_into": ([vp, T, vp, i64, vp, i64, C.c_float, vp], C.c_int),
+        "spt_rmsnorm_batch_into": ([vp, T, vp, i64, vp, i64, i64, C.c_float, vp], C.c_int),
         "spt_mul_q80_argmax_host": ([vp, T, vp, i64, C.POINTER(C.c_int64), C.POINTER(C.c_float)], C.c_int),
         "spt_mul_mxfp4_expert": ([vp, T, T, i32, vp, i64, vp, i64, i64], C.c_int),
         "spt_route_moe_batch": ([vp, T, T, vp, i64, vp], C.c_int),
@@ -249,6 +252,14 @@ class Context:
         _check(lib().spt_mul_q80_argmax_host(self.handle, C.byref(w), _ptr(x), _numel(x), C.byref(tok),
                                              C.byref(logit)))
         return tok.value, logit.value
+
+    def rmsnorm_into(self, w: Tensor, x, y, eps: float, q8=None):
+        _check(lib().spt_rmsnorm_into(self.handle, C.byref(w), _ptr(x), _numel(x), _ptr(y), _numel(y), eps,
+                                      _ptr(q8)))
+
+    def rmsnorm_batch_into(self, w: Tensor, x, y, batch: int, eps: float, q8=None):
+        _check(lib().spt_rmsnorm_batch_into(self.handle, C.byref(w), _ptr(x), _numel(x), _ptr(y), _numel(y),
+                                            batch, eps, _ptr(q8)))
 
     def mul_mxfp4_expert(self, w: Tensor, bias, expert: int, x, y, batch: int):
         b = bias if bias is not None else Tensor.absent()

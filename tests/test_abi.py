@@ -207,6 +207,46 @@ def test_q80_validation(vctx):
     assert b"overlap" in L.spt_last_error()
 
 
+def test_rmsnorm_validation(vctx):
+    """RMSNormInto's checks (forward/rmsnorm.go:21-58, rmsnorm_into_test.go:
+    47-60) and normBatch's (layer_batch.go:141-155)."""
+    L = spt.lib()
+
+    def norm(typ=0, shape=(5,), nbytes=None):
+        width = 4 if typ == 0 else 2
+        return spt.Tensor.make("norm", typ, list(shape), 0x40000000, width * 5 if nbytes is None else nbytes)
+
+    def into(w, xl, yl, eps=1e-5, x=X, y=OUT, q8=None):
+        return L.spt_rmsnorm_into(vctx.handle, C.byref(w), x, xl, y, yl, eps, q8)
+
+    def batch(w, xl, yl, b, eps=1e-5, x=X, y=OUT):
+        return L.spt_rmsnorm_batch_into(vctx.handle, C.byref(w), x, xl, y, yl, b, eps, None)
+
+    for typ in (0, 1, 28):
+        assert into(norm(typ), 5, 5) == spt.ERR_DEVICE
+        assert into(norm(typ), 5, 5, y=X) == spt.ERR_DEVICE  # in place
+        assert batch(norm(typ), 10, 10, 2) == spt.ERR_DEVICE
+    cases = [
+        (lambda: into(norm(), 5, 5, eps=-1.0), b"invalid epsilon"),
+        (lambda: into(norm(), 5, 5, eps=float("nan")), b"invalid epsilon"),
+        (lambda: into(norm(), 5, 5, eps=float("inf")), b"invalid epsilon"),
+        (lambda: into(norm(), 5, 5, y=X + 4), b"partially overlap"),
+        (lambda: into(norm(), 5, 4), b"dimensions differ"),
+        (lambda: into(norm(shape=(6,)), 5, 5), b"dimensions differ"),
+        (lambda: into(norm(typ=30), 5, 5), b"unsupported normalization weight type 30"),
+        (lambda: into(norm(nbytes=19), 5, 5), b"invalid weight data length"),
+        (lambda: into(norm(), 5, 5, q8=OUT + 4096), b"multiple of 32"),
+        (lambda: batch(norm(), 10, 10, 2, eps=-1.0), b"invalid epsilon"),
+        (lambda: batch(norm(typ=30), 10, 10, 2), b"unsupported normalization weight type 30"),
+        (lambda: batch(norm(nbytes=19), 10, 10, 2), b"invalid float vector shape or range"),
+        (lambda: batch(norm(), 10, 10, 3), b"invalid batch"),
+        (lambda: batch(norm(), 10, 12, 2), b"invalid batch"),
+    ]
+    for call, msg in cases:
+        assert call() == spt.ERR_INVALID
+        assert msg in L.spt_last_error(), (msg, L.spt_last_error())
+
+
 def test_quantize_validation(vctx):
     L = spt.lib()
     assert L.spt_quantize_q8_0(vctx.handle, X, 33, OUT) == spt.ERR_INVALID
