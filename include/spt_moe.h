@@ -185,6 +185,17 @@ int spt_mul_q40_into(struct spt_ctx *ctx, const spt_tensor *w, const float *x_de
 int spt_mul_q40_batch_into(struct spt_ctx *ctx, const spt_tensor *w, const float *x_dev,
                            int64_t x_len, float *y_dev, int64_t y_len, int64_t batch);
 
+/* The projection step of forward.ForwardLayer / forwardLayerBatch
+ * (forward/layer.go:117-165, layer_batch.go:62-100) on the device:
+ * MulQ40BatchInto, then addBias / biasBatch of the optional [out] bias
+ * (F32, F16 or BF16; absent = NULL or unnamed and empty; layer.go:225-277,
+ * layer_batch.go:124-137) -- y = W x + bias with one f32 add -- and, with
+ * resid_dev set, the residual addVector (layer.go:305-330): resid += y,
+ * resid being the [batch][out] hidden state.  resid must not overlap x or y. */
+int spt_mul_q40_batch_bias_into(struct spt_ctx *ctx, const spt_tensor *w, const spt_tensor *bias,
+                                const float *x_dev, int64_t x_len, float *y_dev, int64_t y_len,
+                                int64_t batch, float *resid_dev);
+
 /* Host-slice form of MulQ40BatchInto for a cgo caller holding Go slices. */
 int spt_mul_q40_batch_into_host(struct spt_ctx *ctx, const spt_tensor *w, const float *x_host,
                                 int64_t x_len, float *y_host, int64_t y_len, int64_t batch);

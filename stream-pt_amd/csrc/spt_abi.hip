@@ -777,9 +777,60 @@ int spt_mul_q40_batch_into(spt_ctx *ctx, const spt_tensor *w, const float *x_dev
     return SPT_OK;
 }
 
+// The projection bias: addBias (forward/layer.go:225-242) for one vector,
+// biasBatch / readFloatVector (layer_batch.go:124-128, layer.go:279-289)
+// for a batch.  *present = false for an absent bias.
+int projection_bias_check(const spt_tensor *b, int64_t out, int64_t batch, bool *present, int *btype) {
+    *present = false;
+    if (!b) return SPT_OK;
+    const bool empty = b->nbytes == 0;
+    if (empty && !named(*b)) return SPT_OK;
+    if (empty && batch == 1) return fail(SPT_ERR_INVALID, "\"%s\": invalid bias range", tname(b));
+    uint64_t width = 4;
+    if (b->type == SPT_TYPE_F16 || b->type == SPT_TYPE_BF16)
+        width = 2;
+    else if (b->type != SPT_TYPE_F32)
+        return fail(SPT_ERR_INVALID, "\"%s\": unsupported float tensor type %u", tname(b), b->type);
+    if (b->n_dims != 1 || b->shape[0] != (uint64_t)out || b->nbytes != width * (uint64_t)out)
+        return fail(SPT_ERR_INVALID, "\"%s\": invalid float vector shape or range", tname(b));
+    if (!b->data) return fail(SPT_ERR_INVALID, "\"%s\": tensor is not resident (nil data)", tname(b));
+    if ((uintptr_t)b->data & (width - 1))
+        return fail(SPT_ERR_INVALID, "\"%s\": bias data must be %llu-byte aligned", tname(b),
+                    (unsigned long long)width);
+    *present = true;
+    *btype = (int)b->type;
+    return SPT_OK;
+}
+
 int spt_mul_q40_into(spt_ctx *ctx, const spt_tensor *w, const float *x_dev, int64_t x_len, float *y_dev,
                      int64_t y_len) {
     return spt_mul_q40_batch_into(ctx, w, x_dev, x_len, y_dev, y_len, 1);
+}
+
+int spt_mul_q40_batch_bias_into(spt_ctx *ctx, const spt_tensor *w, const spt_tensor *bias, const float *x_dev,
+                                int64_t x_len, float *y_dev, int64_t y_len, int64_t batch, float *resid_dev) {
+    int64_t in, out;
+    int rc;
+    if ((rc = validate_q40_call(ctx, w, x_dev, x_len, y_dev, y_len, batch, &in, &out))) return rc;
+    bool has_bias;
+    int btype = 0;
+    if ((rc = projection_bias_check(bias, out, batch, &has_bias, &btype))) return rc;
+    if (resid_dev && (ranges_overlap(resid_dev, (uint64_t)y_len * 4, x_dev, (uint64_t)x_len * 4) ||
+                      ranges_overlap(resid_dev, (uint64_t)y_len * 4, y_dev, (uint64_t)y_len * 4)))
+        return fail(SPT_ERR_INVALID, "residual overlaps the input or output");
+    if ((rc = check_device(ctx))) return rc;
+    const int64_t nb = in / 32;
+    Carve c;
+    char *S;
+    int8_t *codes;
+    float *scales;
+    int32_t *sumq;
+    if ((rc = quantize_into_scratch(ctx, x_dev, batch, nb, c, &S, &codes, &scales, &sumq, nullptr))) return rc;
+    if ((rc = check_cancel(ctx))) return rc;
+    spt::Q40Args a{(const uint8_t *)w->data, w->nbytes, (int)out, (int)nb, codes, scales, sumq, (int)batch, y_dev,
+                   has_bias ? bias->data : nullptr, btype, resid_dev};
+    SPT_HIP(timed(ctx, SPT_KERNEL_Q40, [&] { return spt::launch_q40_gemv(ctx->stream, a); }));
+    return SPT_OK;
 }
 
 int spt_mul_q40_batch_into_host(spt_ctx *ctx, const spt_tensor *w, const float *x_host, int64_t x_len,

@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "spt_device.h"
+
 namespace spt {
 
 constexpr int kMaxTopK = 16;
@@ -127,7 +129,21 @@ struct Q40Args {
     const int32_t *sumq;
     int ntok;
     float *y;
+    // optional epilogue: y = dot + bias[row] (F32 0, F16 1, BF16 30), then
+    // resid += y
+    const void *bias;
+    int bias_type;
+    float *resid;
 };
+
+// The projection epilogue of forward/layer.go:120-165 and
+// layer_batch.go:68-100: addBias (one f32 add of the decoded bias element),
+// the store of y[o], and the residual addVector (x += y, one f32 add).
+__device__ inline void q40_store(const Q40Args &a, size_t o, int row, float v) {
+    if (a.bias) v = v + bias_at(a.bias, a.bias_type, (uint64_t)row);
+    a.y[o] = v;
+    if (a.resid) a.resid[o] = a.resid[o] + v;
+}
 
 // Q8_0 [in, out] x fp32 x (the LM head, spt_q80_head.hip): y = W x, or with
 // part_v set the argmax of W x -- per-wave (logit, row) into part_v / part_i

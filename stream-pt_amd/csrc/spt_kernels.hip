@@ -467,7 +467,7 @@ __global__ __launch_bounds__(kWG) void k_q40_gemv(Q40Args a) {
         if (j == 0 && row_ok) {
 #pragma unroll
             for (int t = 0; t < NT; t++)
-                if (t < nt) a.y[(size_t)(c0 + t) * a.rows + r] = acc[t];
+                if (t < nt) q40_store(a, (size_t)(c0 + t) * a.rows + r, r, acc[t]);
         }
         __syncthreads();
     }

@@ -260,13 +260,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
     for (int tf = 0; tf < 4; tf++) {
         const int t = 16 * tf + i16;
         if (t >= nt) continue;
-        float *yp = a.y + (size_t)(t0 + t) * a.rows + row;
-        if (row + 3 < a.rows && ((reinterpret_cast<uintptr_t>(yp) & 15u) == 0)) {
+        const size_t o = (size_t)(t0 + t) * a.rows + row;
+        float *yp = a.y + o;
+        if (!a.bias && !a.resid && row + 3 < a.rows && ((reinterpret_cast<uintptr_t>(yp) & 15u) == 0)) {
             *reinterpret_cast<v4f *>(yp) = v4f{acc[tf][0], acc[tf][1], acc[tf][2], acc[tf][3]};
         } else {
 #pragma unroll
             for (int r = 0; r < 4; r++)
-                if (row + r < a.rows) yp[r] = acc[tf][r];
+                if (row + r < a.rows) q40_store(a, o + r, row + r, acc[tf][r]);
         }
     }
 }

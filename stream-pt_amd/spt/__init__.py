@@ -31,7 +31,7 @@ EXPORTED = (
     "spt_forward_moe_batch_host", "spt_block_sums", "spt_synth_mxfp4",
     "spt_ctx_enable_timing", "spt_ctx_read_timing", "spt_ctx_set_gemm_min_group",
     "spt_mul_q80_into", "spt_mul_q80_argmax", "spt_mul_q80_into_host", "spt_mul_q80_argmax_host",
-    "spt_rmsnorm_into", "spt_rmsnorm_batch_into",
+    "spt_rmsnorm_into", "spt_rmsnorm_batch_into", "spt_mul_q40_batch_bias_into",
 )
 KERNEL_KINDS = ("quantize", "route", "gate_up", "down", "combine", "q40", "select", "gate_up_gemm", "down_gemm",
                 "q80", "rmsnorm")
@@ -112,6 +112,7 @@ def lib():
         "spt_mul_q40_into": ([vp, T, vp, i64, vp, i64], C.c_int),
         "spt_mul_q40_batch_into": ([vp, T, vp, i64, vp, i64, i64], C.c_int),
         "spt_mul_q40_batch_into_host": ([vp, T, vp, i64, vp, i64, i64], C.c_int),
+        "spt_mul_q40_batch_bias_into": ([vp, T, T, vp, i64, vp, i64, i64, vp], C.c_int),
         "spt_mul_q80_into": ([vp, T, vp, i64, vp, i64], C.c_int),
         "spt_mul_q80_argmax": ([vp, T, vp, i64, C.POINTER(C.c_int64), C.POINTER(C.c_float)], C.c_int),
         "spt_mul_q80_into_host": ([vp, T, vp, i64, vp, i64], C.c_int),
@@ -229,6 +230,11 @@ class Context:
     def mul_q40_batch_into(self, w: Tensor, x, y, batch: int):
         _check(lib().spt_mul_q40_batch_into(self.handle, C.byref(w), _ptr(x), _numel(x), _ptr(y),
                                             _numel(y), batch))
+
+    def mul_q40_batch_bias_into(self, w: Tensor, bias, x, y, batch: int, resid=None):
+        b = bias if bias is not None else Tensor.absent()
+        _check(lib().spt_mul_q40_batch_bias_into(self.handle, C.byref(w), C.byref(b), _ptr(x), _numel(x), _ptr(y),
+                                                 _numel(y), batch, _ptr(resid)))
 
     def mul_q40_batch_into_host(self, w: Tensor, x, y, batch: int):
         _check(lib().spt_mul_q40_batch_into_host(self.handle, C.byref(w), _ptr(x), _numel(x), _ptr(y),

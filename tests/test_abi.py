@@ -247,6 +247,40 @@ def test_rmsnorm_validation(vctx):
         assert msg in L.spt_last_error(), (msg, L.spt_last_error())
 
 
+def test_q40_bias_validation(vctx):
+    """addBias (forward/layer.go:225-242) for one vector, biasBatch /
+    readFloatVector (layer_batch.go:124-128, layer.go:279-289) for a batch."""
+    L = spt.lib()
+
+    def call(bias, batch=1, resid=None):
+        b = bias if bias is not None else spt.Tensor.absent()
+        return L.spt_mul_q40_batch_bias_into(vctx.handle, C.byref(_q40()), C.byref(b), X, 64 * batch, OUT,
+                                             3 * batch, batch, resid)
+
+    def bias(typ=0, shape=(3,), nbytes=None, name="attn_q.bias"):
+        width = 4 if typ == 0 else 2
+        return spt.Tensor.make(name, typ, list(shape), 0x50000000, width * 3 if nbytes is None else nbytes)
+
+    assert call(None) == spt.ERR_DEVICE
+    assert call(spt.Tensor.make("", 0, [3], 0, 0)) == spt.ERR_DEVICE  # unnamed and empty: absent
+    for typ in (0, 1, 30):
+        assert call(bias(typ)) == spt.ERR_DEVICE
+        assert call(bias(typ), batch=2) == spt.ERR_DEVICE
+    assert call(bias(), resid=0x60000000) == spt.ERR_DEVICE
+    cases = [
+        (lambda: call(bias(nbytes=0)), b"invalid bias range"),
+        (lambda: call(bias(nbytes=0), batch=2), b"invalid float vector shape or range"),
+        (lambda: call(bias(typ=8)), b"unsupported float tensor type 8"),
+        (lambda: call(bias(shape=(4,))), b"invalid float vector shape or range"),
+        (lambda: call(bias(nbytes=11)), b"invalid float vector shape or range"),
+        (lambda: call(bias(), resid=X), b"residual overlaps"),
+        (lambda: call(bias(), resid=OUT + 4), b"residual overlaps"),
+    ]
+    for fn, msg in cases:
+        assert fn() == spt.ERR_INVALID
+        assert msg in L.spt_last_error(), (msg, L.spt_last_error())
+
+
 def test_quantize_validation(vctx):
     L = spt.lib()
     assert L.spt_quantize_q8_0(vctx.handle, X, 33, OUT) == spt.ERR_INVALID

@@ -211,6 +211,47 @@ def test_q40_gemv(gpu_ctx, O, input_dim, output_dim, batch):
             assert got[r, b] == O.isum_q40_q8(blk, xq[b * 34 + 2:b * 34 + 34].view(np.int8))
 
 
+@pytest.mark.parametrize("input_dim,output_dim,batch", [(2880, 4096, 1), (2880, 512, 32), (2880, 4096, 512),
+                                                       (4096, 2880, 70), (32, 17, 3)])
+@pytest.mark.parametrize("btype", [0, 1, 30])
+def test_q40_bias_residual(gpu_ctx, O, input_dim, output_dim, batch, btype):
+    """The projection epilogue (addBias / biasBatch, then the residual
+    addVector): y = (W x) + bias with one f32 add of the decoded bias, and
+    resid + y with one more, on the GEMV and on the GEMM (B = 512, 70)."""
+    import torch
+
+    import spt
+    from spt import synth
+
+    w = synth.q40_bytes(synth.stream_key(8, output_dim), output_dim, input_dim)
+    x = synth.normal(synth.stream_key(9, batch), batch * input_dim)
+    bf = synth.normal(synth.stream_key(10, output_dim), output_dim)
+    if btype == 0:
+        braw = bf.view(np.uint8)
+        bdec = bf
+    elif btype == 1:
+        h = bf.astype(np.float16)
+        braw, bdec = h.view(np.uint8), h.astype(np.float32)
+    else:
+        hb = (bf.view(np.uint32) >> 16).astype(np.uint16)
+        braw, bdec = hb.view(np.uint8), (hb.astype(np.uint32) << 16).view(np.float32)
+    r0 = synth.normal(synth.stream_key(11, batch), batch * output_dim)
+    wd, xd, bd, rd = _dev(w), _dev(x), _dev(braw), _dev(r0)
+    t = spt.Tensor.make("attn", spt.TYPE_Q4_0, [input_dim, output_dim], wd.data_ptr(), w.size)
+    bt = spt.Tensor.make("attn.bias", btype, [output_dim], bd.data_ptr(), braw.size)
+    y0 = torch.zeros(batch * output_dim, dtype=torch.float32, device="cuda")
+    y1 = torch.zeros_like(y0)
+    gpu_ctx.mul_q40_batch_into(t, xd, y0, batch)
+    gpu_ctx.mul_q40_batch_bias_into(t, bt, xd, y1, batch, rd)
+    torch.cuda.synchronize()
+    plain, got, resid = y0.cpu().numpy(), y1.cpu().numpy(), rd.cpu().numpy()
+    want = (plain.reshape(batch, output_dim) + bdec[None, :]).astype(np.float32).reshape(-1)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert np.array_equal(resid.view(np.uint32), (r0 + got).astype(np.float32).view(np.uint32))
+    ref = O.mul_q40_q8(w, x, input_dim, output_dim, batch).reshape(batch, output_dim) + bdec[None, :]
+    assert_close(got, ref.reshape(-1), what="q40+bias")
+
+
 @pytest.mark.parametrize("hidden,batch", [(2880, 1), (2880, 19), (96, 3), (32, 2)])
 def test_router_logits_bit_exact(gpu_ctx, O, hidden, batch):
     import torch
