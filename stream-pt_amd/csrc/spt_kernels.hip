@@ -162,8 +162,10 @@ __device__ void select_token(TokenLogits tl, int E, int k, int32_t *ids, float *
     for (int r = 0; r < k; r++) sum += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, e), r));
     if (lane < k) {
         const float w = sum > 0.0f ? e * (1.0f / sum) : e;
-        s_ids[lane] = my_id;
-        s_w[lane] = w;
+        if (s_ids) {
+            s_ids[lane] = my_id;
+            s_w[lane] = w;
+        }
         ids[lane] = my_id;
         weights[lane] = w;
     }
@@ -363,6 +365,36 @@ __global__ __launch_bounds__(kSelWG) void k_select(const float *__restrict__ log
     pack_lists(n, E, o, s_ids, s_w, s_cnt, s_off, s_run, s_bits);
 }
 
+// Large batches: the selections first, a wavefront per token over the whole
+// grid (kTopkWG / 64 tokens per workgroup) ...
+constexpr int kTopkWG = 256;
+__global__ __launch_bounds__(kTopkWG) void k_topk(const float *__restrict__ logits, int batch, int E, int topk,
+                                                  int32_t *ids, float *weights) {
+    const int t = blockIdx.x * (kTopkWG / 64) + (int)(threadIdx.x >> 6);
+    if (t >= batch) return;  // whole wavefronts
+    select_token(load_token_logits(logits + (size_t)t * E, E), E, topk, ids + t * topk, weights + t * topk,
+                 nullptr, nullptr);
+}
+
+// ... then the packing of all of them by one workgroup, from the ids and
+// weights just written.
+__global__ __launch_bounds__(kSelWG) void k_pack(int batch, int E, int topk, SelectOut o) {
+    extern __shared__ int32_t smem_i[];
+    const int n = batch * topk;
+    int32_t *s_ids = smem_i;
+    float *s_w = reinterpret_cast<float *>(smem_i + n);
+    int32_t *s_cnt = smem_i + 2 * n;
+    int32_t *s_off = s_cnt + E;
+    int32_t *s_run = s_off + E + 1;
+    uint32_t *s_bits = reinterpret_cast<uint32_t *>(s_run + E);
+    for (int i = threadIdx.x; i < n; i += kSelWG) {
+        s_ids[i] = o.ids[i];
+        s_w[i] = o.weights[i];
+    }
+    __syncthreads();
+    pack_lists(n, E, o, s_ids, s_w, s_cnt, s_off, s_run, s_bits);
+}
+
 hipError_t launch_route(hipStream_t s, const float *router, const void *bias, int bias_type,
                         const float *x, int batch, int hidden, int experts, float *logits,
                         const QuantOut &q) {
@@ -374,8 +406,18 @@ hipError_t launch_route(hipStream_t s, const float *router, const void *bias, in
 
 hipError_t launch_select(hipStream_t s, const float *logits, int batch, int experts, int topk,
                          const SelectOut &o) {
-    hipLaunchKernelGGL(k_select, dim3(1), dim3(kSelWG), select_lds(batch * topk, experts), s, logits,
-                       batch, experts, topk, o);
+    // Up to one token per wavefront of the packing workgroup: one kernel;
+    // beyond, the selections spread over the grid first.
+    if (batch <= kSelWG / 64) {
+        hipLaunchKernelGGL(k_select, dim3(1), dim3(kSelWG), select_lds(batch * topk, experts), s, logits,
+                           batch, experts, topk, o);
+        return hipGetLastError();
+    }
+    hipLaunchKernelGGL(k_topk, dim3((batch + kTopkWG / 64 - 1) / (kTopkWG / 64)), dim3(kTopkWG), 0, s, logits, batch,
+                       experts, topk, o.ids, o.weights);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k_pack, dim3(1), dim3(kSelWG), select_lds(batch * topk, experts), s, batch, experts, topk, o);
     return hipGetLastError();
 }
 
