@@ -113,7 +113,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (got --gpus {args.gpus}); the expert-parallel "
-              "sharding across GPUs is described in DESIGN.md and is not built.", file=sys.stderr)
+              "sharding across GPUs is not built.", file=sys.stderr)
         sys.exit(2)
     import numpy as np
     import torch
