@@ -28,13 +28,14 @@ namespace {
 
 constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;
-constexpr int kTileRows = 8;                                          // 8 lanes per row
+constexpr int kRowsPerLane = 2;                                       // rows rg and rg + 8 share x reads
+constexpr int kTileRows = 8 * kRowsPerLane;                           // 8 lanes per row
 constexpr int kSeg = 9;                                               // blocks per K segment (90 = 10 x 9)
 constexpr int kPieces = (15 + kSeg * kQ80Block + 15) / 16;            // 16-byte loads per row window
 constexpr int kSlot = 16 * kPieces;                                   // LDS bytes per row in a stage
 constexpr int kSegInstr = (kTileRows * kPieces + 63) / 64;            // LDS DMA loads per segment
 constexpr int kStageBytes = 1024 * kSegInstr;
-constexpr int kBufs = 4;
+constexpr int kBufs = 3;
 constexpr int kGroup = 3;                                             // blocks per LDS read group
 constexpr uint32_t kOOR = 0xFFFFFFF0u;                                // past every descriptor's range
 static_assert(kSeg % kGroup == 0, "segment of whole groups");
@@ -66,23 +67,29 @@ __device__ __attribute__((always_inline)) inline void q80_block(uint32_t qa, uin
 }
 
 struct Q80Grp {
-    uint32_t qa[kGroup], qb[kGroup], d[kGroup];
+    uint32_t qa[kRowsPerLane][kGroup], qb[kRowsPerLane][kGroup], d[kRowsPerLane][kGroup];
     float4 x[kGroup];
 };
 
-// A full segment: kSeg / kGroup groups, each group's LDS reads issued while
-// the previous group is multiplied (two register sets, no copies).
-__device__ __attribute__((always_inline)) inline void q80_segment(const uint16_t *qp, const uint16_t *dp,
-                                                                  const float4 *xp, float nz, float (&c)[4]) {
+// A full segment for the lane's rows: kSeg / kGroup groups, each group's LDS
+// reads issued while the previous group is multiplied (two register sets,
+// no copies); one read of x serves every row.
+__device__ __attribute__((always_inline)) inline void q80_segment(const uint16_t *const (&qp)[kRowsPerLane],
+                                                                  const uint16_t *const (&dp)[kRowsPerLane],
+                                                                  const float4 *xp, float nz,
+                                                                  float (&c)[kRowsPerLane][4]) {
     constexpr int kNG = kSeg / kGroup;
     Q80Grp g[2];
     auto fetch = [&](int gi, Q80Grp &t) {
 #pragma unroll
         for (int k = 0; k < kGroup; k++) {
             const int b = kGroup * gi + k;
-            t.qa[k] = qp[(kQ80Block / 2) * b];
-            t.qb[k] = qp[(kQ80Block / 2) * b + 1];
-            t.d[k] = dp[(kQ80Block / 2) * b];
+#pragma unroll
+            for (int r = 0; r < kRowsPerLane; r++) {
+                t.qa[r][k] = qp[r][(kQ80Block / 2) * b];
+                t.qb[r][k] = qp[r][(kQ80Block / 2) * b + 1];
+                t.d[r][k] = dp[r][(kQ80Block / 2) * b];
+            }
             t.x[k] = xp[8 * b];
         }
     };
@@ -91,7 +98,10 @@ __device__ __attribute__((always_inline)) inline void q80_segment(const uint16_t
     for (int gi = 0; gi < kNG; gi++) {
         if (gi + 1 < kNG) fetch(gi + 1, g[(gi + 1) & 1]);
 #pragma unroll
-        for (int k = 0; k < kGroup; k++) q80_block(g[gi & 1].qa[k], g[gi & 1].qb[k], g[gi & 1].d[k], g[gi & 1].x[k], nz, c);
+        for (int k = 0; k < kGroup; k++)
+#pragma unroll
+            for (int r = 0; r < kRowsPerLane; r++)
+                q80_block(g[gi & 1].qa[r][k], g[gi & 1].qb[r][k], g[gi & 1].d[r][k], g[gi & 1].x[k], nz, c[r]);
     }
 }
 
@@ -103,7 +113,7 @@ __global__ __launch_bounds__(kThreads) void k_q80_rows(Q80Args a) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wl = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int gw = blockIdx.x * kWaves + wl, nw = gridDim.x * kWaves;
-    const int rg = lane >> 3, j = lane & 7;  // row of the tile, chain quad
+    const int rg = lane >> 3, j = lane & 7;  // rows rg + 8r of the tile, chain quad
     const int nb = a.nb, rows = a.rows;
     const uint32_t rb = (uint32_t)nb * kQ80Block;
     const int nseg = (nb + kSeg - 1) / kSeg;
@@ -160,9 +170,14 @@ __global__ __launch_bounds__(kThreads) void k_q80_rows(Q80Args a) {
     const float nz = -0.0f;
     float best_v = -__builtin_inff();
     int best_i = 0;
-    float c[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // chains 4j .. 4j+3 of row rg
-    // y of MulQ80Into: lane 8k + r collects row r of the wave's tile 8m + k
-    // (m counting groups of eight tiles); one store per eight tiles
+    float c[kRowsPerLane][4];  // chains 4j .. 4j+3 of rows rg + 8r
+#pragma unroll
+    for (int r = 0; r < kRowsPerLane; r++)
+#pragma unroll
+        for (int k = 0; k < 4; k++) c[r][k] = 0.0f;
+    // y of MulQ80Into: lane kTileRows * k + i collects row i of the wave's
+    // tile k of each group of kTilesPerStore; one store per group
+    constexpr int kTilesPerStore = 64 / kTileRows;
     float yv = 0.0f;
     int yrow = -1;
     int t = gw, sg = 0, ti = 0;
@@ -177,44 +192,58 @@ __global__ __launch_bounds__(kThreads) void k_q80_rows(Q80Args a) {
         } else {
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         }
-        const int row = kTileRows * t + rg;
         const int b0 = kSeg * sg, jn = min(kSeg, nb - b0);
-        const uint8_t *rowp = stages + (u % kBufs) * kStageBytes + kSlot * rg +
-                              ((le + (uint32_t)row * rb + (uint32_t)(b0 * kQ80Block)) & 15u);
-        const uint16_t *qp = reinterpret_cast<const uint16_t *>(rowp + 2 + 4 * j);
-        const uint16_t *dp = reinterpret_cast<const uint16_t *>(rowp);
+        const uint16_t *qp[kRowsPerLane];
+        const uint16_t *dp[kRowsPerLane];
+#pragma unroll
+        for (int r = 0; r < kRowsPerLane; r++) {
+            const int rl = rg + 8 * r;  // row within the tile
+            const uint8_t *rowp = stages + (u % kBufs) * kStageBytes + kSlot * rl +
+                                  ((le + (uint32_t)(kTileRows * t + rl) * rb + (uint32_t)(b0 * kQ80Block)) & 15u);
+            qp[r] = reinterpret_cast<const uint16_t *>(rowp + 2 + 4 * j);
+            dp[r] = reinterpret_cast<const uint16_t *>(rowp);
+        }
         const float4 *xp = reinterpret_cast<const float4 *>(xs + 32 * b0) + j;
         if (jn == kSeg) {
             q80_segment(qp, dp, xp, nz, c);
         } else {
             for (int b = 0; b < jn; b++)
-                q80_block(qp[(kQ80Block / 2) * b], qp[(kQ80Block / 2) * b + 1], dp[(kQ80Block / 2) * b], xp[8 * b],
-                          nz, c);
+#pragma unroll
+                for (int r = 0; r < kRowsPerLane; r++)
+                    q80_block(qp[r][(kQ80Block / 2) * b], qp[r][(kQ80Block / 2) * b + 1], dp[r][(kQ80Block / 2) * b],
+                              xp[8 * b], nz, c[r]);
         }
         if (sg == nseg - 1) {
-            // t_{4m+k} at lane m < 2 of the row: chains 4m+k + 8, 16, 24 sit
-            // in lanes m + 2, 4, 6; p_k = t_k + t_{k+4} (lanes 0 and 1)
-            float pk4[4];
 #pragma unroll
-            for (int k = 0; k < 4; k++) {
-                const float tk = ((c[k] + __shfl_down(c[k], 2, 8)) + __shfl_down(c[k], 4, 8)) + __shfl_down(c[k], 6, 8);
-                pk4[k] = tk + __shfl_down(tk, 1, 8);
-                c[k] = 0.0f;
-            }
-            const float y = (pk4[0] + pk4[1]) + (pk4[2] + pk4[3]);
-            if constexpr (ARGMAX) {
-                // lane 8r keeps the best of row r across the wave's tiles
-                if (j == 0 && row < rows) argmax_take(y, row, best_v, best_i);
-            } else {
+            for (int r = 0; r < kRowsPerLane; r++) {
+                // t_{4m+k} at lane m < 2 of the row: chains 4m+k + 8, 16, 24
+                // sit in lanes m + 2, 4, 6; p_k = t_k + t_{k+4} (lanes 0 and 1)
+                float pk4[4];
 #pragma unroll
-                for (int r = 0; r < kTileRows; r++) {
-                    const float yr =
-                        __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, y), 8 * r));
-                    const bool mine_r = lane == 8 * (ti & 7) + r;
-                    yv = mine_r ? yr : yv;
-                    yrow = mine_r ? kTileRows * t + r : yrow;
+                for (int k = 0; k < 4; k++) {
+                    const float tk =
+                        ((c[r][k] + __shfl_down(c[r][k], 2, 8)) + __shfl_down(c[r][k], 4, 8)) + __shfl_down(c[r][k], 6, 8);
+                    pk4[k] = tk + __shfl_down(tk, 1, 8);
+                    c[r][k] = 0.0f;
                 }
-                if ((ti & 7) == 7 || u + 1 == units) {
+                const float y = (pk4[0] + pk4[1]) + (pk4[2] + pk4[3]);
+                const int row = kTileRows * t + rg + 8 * r;
+                if constexpr (ARGMAX) {
+                    // lane 8i keeps the best of its rows across the wave's tiles
+                    if (j == 0 && row < rows) argmax_take(y, row, best_v, best_i);
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 8; i++) {
+                        const float yr =
+                            __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, y), 8 * i));
+                        const bool mine_r = lane == kTileRows * (ti % kTilesPerStore) + i + 8 * r;
+                        yv = mine_r ? yr : yv;
+                        yrow = mine_r ? kTileRows * t + i + 8 * r : yrow;
+                    }
+                }
+            }
+            if constexpr (!ARGMAX) {
+                if (ti % kTilesPerStore == kTilesPerStore - 1 || u + 1 == units) {
                     if (yrow >= 0 && yrow < rows) a.y[yrow] = yv;
                     yrow = -1;
                 }
