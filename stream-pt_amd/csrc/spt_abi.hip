@@ -766,6 +766,9 @@ int spt_mul_q40_batch_into(spt_ctx *ctx, const spt_tensor *w, const float *x_dev
     if ((rc = check_device(ctx))) return rc;
     const int64_t nb = in / 32;
     Carve c;
+    // partial sums of the split-K GEMM for narrow projections of large batches
+    const bool split = batch >= spt::kQ40SplitMinTokens && out < spt::kQ40GemmMinRows;
+    const size_t o_part = c.take(split ? (size_t)spt::kQ40SplitK * batch * out * 4 : 0);
     char *S;
     int8_t *codes;
     float *scales;
@@ -773,6 +776,7 @@ int spt_mul_q40_batch_into(spt_ctx *ctx, const spt_tensor *w, const float *x_dev
     if ((rc = quantize_into_scratch(ctx, x_dev, batch, nb, c, &S, &codes, &scales, &sumq, nullptr))) return rc;
     if ((rc = check_cancel(ctx))) return rc;
     spt::Q40Args a{(const uint8_t *)w->data, w->nbytes, (int)out, (int)nb, codes, scales, sumq, (int)batch, y_dev};
+    a.part = split ? (float *)(S + o_part) : nullptr;
     SPT_HIP(timed(ctx, SPT_KERNEL_Q40, [&] { return spt::launch_q40_gemv(ctx->stream, a); }));
     return SPT_OK;
 }
@@ -821,6 +825,8 @@ int spt_mul_q40_batch_bias_into(spt_ctx *ctx, const spt_tensor *w, const spt_ten
     if ((rc = check_device(ctx))) return rc;
     const int64_t nb = in / 32;
     Carve c;
+    const bool split = batch >= spt::kQ40SplitMinTokens && out < spt::kQ40GemmMinRows;
+    const size_t o_part = c.take(split ? (size_t)spt::kQ40SplitK * batch * out * 4 : 0);
     char *S;
     int8_t *codes;
     float *scales;
@@ -828,7 +834,7 @@ int spt_mul_q40_batch_bias_into(spt_ctx *ctx, const spt_tensor *w, const spt_ten
     if ((rc = quantize_into_scratch(ctx, x_dev, batch, nb, c, &S, &codes, &scales, &sumq, nullptr))) return rc;
     if ((rc = check_cancel(ctx))) return rc;
     spt::Q40Args a{(const uint8_t *)w->data, w->nbytes, (int)out, (int)nb, codes, scales, sumq, (int)batch, y_dev,
-                   has_bias ? bias->data : nullptr, btype, resid_dev};
+                   has_bias ? bias->data : nullptr, btype, resid_dev, split ? (float *)(S + o_part) : nullptr};
     SPT_HIP(timed(ctx, SPT_KERNEL_Q40, [&] { return spt::launch_q40_gemv(ctx->stream, a); }));
     return SPT_OK;
 }

@@ -134,6 +134,9 @@ struct Q40Args {
     const void *bias;
     int bias_type;
     float *resid;
+    // optional scratch of kQ40SplitK * ntok * rows floats: narrow projections
+    // of large batches then run on the GEMM with K split kQ40SplitK ways
+    float *part;
 };
 
 // The projection epilogue of forward/layer.go:120-165 and
@@ -182,6 +185,11 @@ hipError_t launch_mx_gemm(hipStream_t s, GemvMode mode, const MxGemmArgs &a, int
 // GEMV.
 constexpr int kQ40GemmMinTokens = 64;
 constexpr int kQ40GemmMinRows = 1024;
+// Narrower projections of kQ40SplitMinTokens tokens and more: the GEMM with
+// K split kQ40SplitK ways (partial sums in Q40Args::part, then summed in
+// order), when the caller provides the scratch.
+constexpr int kQ40SplitK = 4;
+constexpr int kQ40SplitMinTokens = 256;
 hipError_t launch_q40_gemv(hipStream_t s, const Q40Args &a);
 hipError_t launch_q40_gemm(hipStream_t s, const Q40Args &a);
 int q80_grid_waves(int rows, int nb, int n_cu);

@@ -530,7 +530,12 @@ static hipError_t launch_q40_maxp(hipStream_t s, const Q40Args &a) {
 
 hipError_t launch_q40_gemv(hipStream_t s, const Q40Args &a) {
     if (a.rows <= 0 || a.ntok <= 0) return hipSuccess;
-    if (a.ntok >= kQ40GemmMinTokens && a.rows >= kQ40GemmMinRows) return launch_q40_gemm(s, a);
+    if (a.ntok >= kQ40GemmMinTokens && a.rows >= kQ40GemmMinRows) {
+        Q40Args g = a;
+        g.part = nullptr;
+        return launch_q40_gemm(s, g);
+    }
+    if (a.part && a.ntok >= kQ40SplitMinTokens) return launch_q40_gemm(s, a);
     const int per_lane = (a.nb + 15) / 16;
     if (per_lane <= 1) return launch_q40_maxp<1>(s, a);
     if (per_lane <= 2) return launch_q40_maxp<2>(s, a);

@@ -133,7 +133,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
     const int r0 = blockIdx.x * kTR, t0 = blockIdx.y * kTN;
     const int nt = min(kTN, a.ntok - t0);
     const int ntf = (nt + 15) >> 4;
-    const int nseg = (nb + kSeg - 1) / kSeg;
+    // K range of this workgroup: blocks [kb0, kb1) (split over grid z when
+    // the partial sums go to a.part)
+    const int ks = gridDim.z, kz = blockIdx.z;
+    const int kb0 = kz * nb / ks, kb1 = (kz + 1) * nb / ks;
+    const int nseg = (kb1 - kb0 + kSeg - 1) / kSeg;
 
     // the matrix from the 16-byte boundary at or below its first byte
     const uintptr_t wb = reinterpret_cast<uintptr_t>(a.w);
@@ -158,7 +162,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
     u32x4 ra[kALoads], rb[kBLoads];
     uint32_t rsx[kSLoads];
     auto stage_load = [&](int s) {
-        const int b0 = s * kSeg;
+        const int b0 = kb0 + s * kSeg;
 #pragma unroll
         for (int k = 0; k < kALoads; k++) {
             const uint32_t off = ((a_pos[k] + (uint32_t)b0 * kQ40Block) & ~15u) + 16u * (uint32_t)a_pc[k];
@@ -170,7 +174,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
             const int q = tid + kThreads * k, t = q >> 4, pc = q & 15;
             const int b = b0 + (pc >> 1);
             u32x4 v = {0u, 0u, 0u, 0u};
-            if (t < nt && b < nb)
+            if (t < nt && b < kb1)
                 v = *reinterpret_cast<const u32x4 *>(a.codes + ((size_t)(t0 + t) * nb + b) * 32 + 16 * (pc & 1));
             rb[k] = v;
         }
@@ -179,7 +183,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
             const int q = tid + kThreads * k, which = q / (kTN * kSeg), e = q % (kTN * kSeg);
             const int t = e / kSeg, b = b0 + e % kSeg;
             uint32_t v = 0u;
-            if (t < nt && b < nb) {
+            if (t < nt && b < kb1) {
                 const size_t o = (size_t)(t0 + t) * nb + b;
                 v = which == 0 ? __float_as_uint(a.scales[o]) : (uint32_t)a.sumq[o];
             }
@@ -227,7 +231,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
         for (int s = 0; s < nseg; s++) {
             if (s + 1 < nseg) stage_load(s + 1);
             const uint8_t *st = lds + (size_t)(s & 1) * kStageBytes;
-            const int b0 = s * kSeg, jn = min(kSeg, nb - b0);
+            const int b0 = kb0 + s * kSeg, jn = min(kSeg, kb1 - b0);
             // window offsets of this segment: A row (nibble bytes 2+4g..5+4g
             // of block j at lead + 18j + 2 + 4g), and the D rows' scales
             Q40Lane L;
@@ -256,6 +260,19 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
 
     // y[t][row]: rows 4g .. 4g+3 of the wave's 16 for token 16tf + i16
     const int row = r0 + 16 * wave + 4 * g;
+    if (a.part) {
+        // partial sums of K range kz, summed in order by k_q40_reduce
+#pragma unroll
+        for (int tf = 0; tf < 4; tf++) {
+            const int t = 16 * tf + i16;
+            if (t >= nt) continue;
+            float *pp = a.part + ((size_t)kz * a.ntok + t0 + t) * a.rows + row;
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+                if (row + r < a.rows) pp[r] = acc[tf][r];
+        }
+        return;
+    }
 #pragma unroll
     for (int tf = 0; tf < 4; tf++) {
         const int t = 16 * tf + i16;
@@ -272,10 +289,26 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
     }
 }
 
+// y[t][row] = the K ranges' partial sums added in range order, then the
+// projection epilogue.
+__global__ __launch_bounds__(256) void k_q40_reduce(Q40Args a, int ks) {
+    const size_t n = (size_t)a.ntok * a.rows;
+    const size_t o = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (o >= n) return;
+    float v = a.part[o];
+    for (int z = 1; z < ks; z++) v = v + a.part[(size_t)z * n + o];
+    q40_store(a, o, (int)(o % (size_t)a.rows), v);
+}
+
 hipError_t launch_q40_gemm(hipStream_t s, const Q40Args &a) {
     if (a.rows <= 0 || a.ntok <= 0 || a.nb <= 0) return hipSuccess;
-    dim3 grid((a.rows + kTR - 1) / kTR, (a.ntok + kTN - 1) / kTN);
+    const int ks = a.part ? (a.nb < kQ40SplitK ? a.nb : kQ40SplitK) : 1;
+    dim3 grid((a.rows + kTR - 1) / kTR, (a.ntok + kTN - 1) / kTN, ks);
     hipLaunchKernelGGL(k_q40_gemm, grid, dim3(kThreads), 2 * (size_t)kStageBytes, s, a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || !a.part) return e;
+    const size_t n = (size_t)a.ntok * a.rows;
+    hipLaunchKernelGGL(k_q40_reduce, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a, ks);
     return hipGetLastError();
 }
 

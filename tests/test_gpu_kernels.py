@@ -181,6 +181,9 @@ def test_mxfp4_expert_gemv_odd_half_bias(gpu_ctx, O, bias_type):
     # than one 8-block segment and off its multiple
     (2880, 4096, 100), (2880, 512, 64), (4096, 2880, 70), (32, 17, 64), (96, 70, 129),
     (288, 4, 65), (2880, 512, 512),
+    # narrow projections of 256 tokens and up: the GEMM with K split four
+    # ways (fewer ways when the input has fewer blocks)
+    (96, 70, 300), (32, 17, 256), (4096, 512, 257),
 ])
 def test_q40_gemv(gpu_ctx, O, input_dim, output_dim, batch):
     import torch
@@ -212,7 +215,7 @@ def test_q40_gemv(gpu_ctx, O, input_dim, output_dim, batch):
 
 
 @pytest.mark.parametrize("input_dim,output_dim,batch", [(2880, 4096, 1), (2880, 512, 32), (2880, 4096, 512),
-                                                       (4096, 2880, 70), (32, 17, 3)])
+                                                       (4096, 2880, 70), (32, 17, 3), (2880, 512, 300)])
 @pytest.mark.parametrize("btype", [0, 1, 30])
 def test_q40_bias_residual(gpu_ctx, O, input_dim, output_dim, batch, btype):
     """The projection epilogue (addBias / biasBatch, then the residual
