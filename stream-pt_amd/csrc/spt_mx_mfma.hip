@@ -63,23 +63,20 @@ __device__ float lut_row_dot(const ByteView &v, uint32_t row_pos, int nb, const 
 
 }  // namespace
 
-// Weights reach the MFMA through a wave-private LDS image of the wave's 16
-// rows.  The rows of an expert matrix are contiguous, so a wave's 16 rows are
-// one run of 16 * nb * 17 bytes: the wave streams it with fully coalesced
-// 16-byte loads (64 lanes x 16 B = 1 KB per instruction) starting at the
-// 16-byte boundary at or below the run's first byte, stores the image to LDS
-// unchanged, and the MFMA lanes read their blocks back at any byte alignment
-// (five dwords, realigned by byte permutes).  While a wave multiplies one
-// tile the loads of its next tile are in flight.  The image of one tile (nb
-// up to kMaxNb) plus the token tables must fit the LDS of a CU, which holds
-// one workgroup of four waves.
+// Weights reach the MFMA through an LDS image of each 16-row tile.  The rows
+// of an expert matrix are contiguous, so a tile's 16 rows are one run of
+// 16 * nb * 17 bytes: two waves stream it with fully coalesced 16-byte loads
+// (64 lanes x 16 B = 1 KB per instruction) starting at the 16-byte boundary
+// at or below the run's first byte, store the image to LDS unchanged, and
+// the MFMA lanes read their blocks back at any byte alignment (five dwords,
+// realigned by byte permutes).  While the workgroup multiplies one unit (four
+// tiles) the loads of its next unit are in flight, in registers.
 constexpr int kMaxNb = kMxMaxInput / 32;
-constexpr int kMaxNbp = (kMaxNb + 7) / 8 * 8;
 // 1 KB loads of a tile image: 16 rows plus up to 15 bytes before them.
 __host__ __device__ constexpr int tile_loads(int nb) { return (16 * nb * kMxBlock + 15 + 1023) / 1024; }
-// LDS bytes of a wave's image: whole groups of four loads, and room for the
-// reads of the blocks past nb in the last chunk pair (up to nb + 6, 20 bytes
-// each from a dword boundary).
+// LDS bytes of a tile image: whole groups of four loads, and room for the
+// reads of the blocks past nb in the last chunk (up to nb + 2, 20 bytes each
+// from a dword boundary; the bound below allows nb + 6).
 __host__ __device__ constexpr int tile_region(int nb) {
     return (4 * ((tile_loads(nb) + 3) / 4) > (16 * nb * kMxBlock + 137 + 1023) / 1024
                 ? 4 * ((tile_loads(nb) + 3) / 4)
@@ -87,25 +84,9 @@ __host__ __device__ constexpr int tile_region(int nb) {
            1024;
 }
 constexpr int kTileGroups = (tile_loads(kMaxNb) + 3) / 4;  // groups of four 1 KB loads per tile
-constexpr int kWaveGroups = (kTileGroups + 1) / 2;            // of them, loaded by one wave
-constexpr int kTabLoads = (16 * kMaxNbp + kWG - 1) / kWG;  // 16-byte digit-table pieces per thread
-constexpr int kDxLoads = (kTokPerPass * kMaxNbp + kWG - 1) / kWG;  // d_x entries per thread
-constexpr size_t kMaxMxLds = 146 * 1024;  // dynamic LDS; with the static part (< 14 KB) within 160 KB
-
-template <int MODE> struct MxTraits {
-    // Unit outputs staged in LDS before a flush, and the values staged per
-    // row and token (gate/up: act, gate, up; down: the result).
-    static constexpr int kStageUnits = MODE == kGateUp ? 4 : 6;
-    static constexpr int kStageVals = MODE == kGateUp ? 3 : 1;
-    static constexpr int kUnitRows = MODE == kGateUp ? 32 : 64;
-};
-
-// Orders a wave's accesses to its own LDS tile for the compiler (the hardware
-// executes one wave's LDS instructions in order).
-__device__ inline void wave_lds_fence() {
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_wave_barrier();
-}
+constexpr int kWaveGroups = (kTileGroups + 1) / 2;         // of them, loaded by one wave
+constexpr size_t kMaxMxLds = 120 * 1024;  // dynamic LDS; with the static part (< 36 KB) within 160 KB
+constexpr int kStageUnits = 4;             // units whose partial sums are staged before a flush
 
 // Workgroup barrier ordering LDS only.  All communication between the
 // waves of k_mx_mfma goes through LDS, and __syncthreads() would also wait
@@ -127,7 +108,10 @@ typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
 // with five wait states: its descriptor and offset SGPRs may have just been
 // written by a VALU instruction, which a following VMEM read must not see
 // early, and the compiler cannot pad inside inline assembly.  Offsets past
-// the descriptor's range read zeros.
+// the descriptor's range read zeros.  The loads are nontemporal (`nt`): each
+// weight byte is read once per pass and the stream is far larger than the
+// caches, and a plain streaming read reaches about 7.0 TB/s with the bit
+// against 6.1 TB/s without it on MI355X.
 struct TileRegs {
     u32x4v q[4 * kWaveGroups];
 };
@@ -136,10 +120,10 @@ template <int G>
 __device__ inline void tile_issue(TileRegs &t, uint32_t vo, const u32x4v &rs, uint32_t so) {
     asm volatile(
         "s_nop 4\n\t"
-        "buffer_load_dwordx4 %0, %4, %5, %6 offen\n\t"
-        "buffer_load_dwordx4 %1, %4, %5, %6 offen offset:1024\n\t"
-        "buffer_load_dwordx4 %2, %4, %5, %6 offen offset:2048\n\t"
-        "buffer_load_dwordx4 %3, %4, %5, %6 offen offset:3072"
+        "buffer_load_dwordx4 %0, %4, %5, %6 offen nt\n\t"
+        "buffer_load_dwordx4 %1, %4, %5, %6 offen offset:1024 nt\n\t"
+        "buffer_load_dwordx4 %2, %4, %5, %6 offen offset:2048 nt\n\t"
+        "buffer_load_dwordx4 %3, %4, %5, %6 offen offset:3072 nt"
         : "=&v"(t.q[4 * G]), "=&v"(t.q[4 * G + 1]), "=&v"(t.q[4 * G + 2]), "=&v"(t.q[4 * G + 3])
         : "v"(vo), "s"(rs), "s"(so));
 }
@@ -172,62 +156,36 @@ struct LaneRole {
     bool lo_on, hi_on;
 };
 
-// Per token pass and token pair: where this lane's B operand halves and d_x
-// are read at chunk 0 (add 256 bytes and 4 floats per chunk).  A half that
-// carries no data reads the zero area, which is as long as the tables.
-struct PassRole {
-    const uint8_t *bl[2], *bh[2];
-    const float *dx[2];
+// A wave's B operands and d_x for one token pass: chunk c_j = wave + 8j
+// (j < kChunksPerWave), token pair tp.  They are the same for every row of
+// the expert, so they stay in registers for all the units of the pass.
+constexpr int kChunksPerWave = (kMaxNb + 3) / 4 / kWaves + ((kMaxNb + 3) / 4 % kWaves != 0);
+struct PassB {
+    v8i b[kChunksPerWave][2];
+    float dx[kChunksPerWave][2];
 };
 
-// The LDS words of one chunk: the five dwords holding this lane's A block,
-// and per token pair the two halves of the B operand and d_x.
-template <int NP>
-struct ChunkRaw {
-    uint32_t d[5];
-    u32x4v blo[NP], bhi[NP];
-    float x[NP];
-};
-
-template <int NP>
-__device__ __attribute__((always_inline)) inline void chunk_fetch(ChunkRaw<NP> &r, const uint32_t *pa, const PassRole &P, int c) {
+// Loads a pass's B operands from the digit tables (zero past nb, for the
+// unused token slots and for the lane's empty half) and d_x from the scales.
+__device__ inline void load_pass_b(PassB &pb, const MxMfmaArgs &a, const int (&arow)[kTokPerPass], int nt,
+                                   const LaneRole &L, int wave) {
+    const int nb = a.nb;
 #pragma unroll
-    for (int i = 0; i < 5; i++) r.d[i] = pa[17 * c + i];
+    for (int j = 0; j < kChunksPerWave; j++) {
+        const int b = 4 * (wave + kWaves * j) + L.gc;
 #pragma unroll
-    for (int tp = 0; tp < NP; tp++) {
-        r.blo[tp] = *reinterpret_cast<const u32x4v *>(P.bl[tp] + 256 * c);
-        r.bhi[tp] = *reinterpret_cast<const u32x4v *>(P.bh[tp] + 256 * c);
-        r.x[tp] = P.dx[tp][4 * c];
-    }
-}
-
-// MFMAs of a fetched chunk.  MASK: the chunk may hold blocks past nb, which
-// get scale 2^0 (their tables and d_x are zero, so they add 0) and stay out
-// of the special-scale check.
-template <int NP, bool MASK>
-__device__ __attribute__((always_inline)) inline void chunk_mfma(const ChunkRaw<NP> &r, int c, int nb, uint32_t sel, uint32_t esh, const LaneRole &L,
-                                  float acc[2][4], uint32_t &emin, uint32_t &emax) {
-    const uint32_t ev = __builtin_amdgcn_ubfe(r.d[0], esh, 8u);
-    int sa = (int)ev;
-    if (MASK) {
-        const bool in = 4 * c + L.gb < nb;
-        sa = in ? sa : 127;
-        emin = in ? min(emin, ev) : emin;
-        emax = in ? max(emax, ev) : emax;
-    } else {
-        emin = min(emin, ev);
-        emax = max(emax, ev);
-    }
-    const v8i A = {(int)__builtin_amdgcn_perm(r.d[1], r.d[0], sel), (int)__builtin_amdgcn_perm(r.d[2], r.d[1], sel),
-                   (int)__builtin_amdgcn_perm(r.d[3], r.d[2], sel), (int)__builtin_amdgcn_perm(r.d[4], r.d[3], sel),
-                   0, 0, 0, 0};
-#pragma unroll
-    for (int tp = 0; tp < NP; tp++) {
-        const v8i B = __builtin_bit_cast(v8i, __builtin_shufflevector(r.blo[tp], r.bhi[tp], 0, 1, 2, 3, 4, 5, 6, 7));
-        v4f dd = {0.0f, 0.0f, 0.0f, 0.0f};
-        dd = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A, B, dd, 4, 0, 0, sa, 0, L.sb);
-#pragma unroll
-        for (int k = 0; k < 4; k++) acc[tp][k] = __builtin_fmaf(dd[k], r.x[tp], acc[tp][k]);
+        for (int tp = 0; tp < 2; tp++) {
+            const int t = 2 * tp + L.slot;
+            const bool ok = t < nt && b < nb;
+            const int ar = t == 0 ? arow[0] : t == 1 ? arow[1] : t == 2 ? arow[2] : arow[3];
+            const size_t blk = (size_t)ar * nb + b;
+            u32x4v v = {0u, 0u, 0u, 0u};
+            if (ok && (L.lo_on || L.hi_on)) v = *reinterpret_cast<const u32x4v *>(a.mxtab + blk * 64 + L.boff);
+            const u32x4v z = {0u, 0u, 0u, 0u};
+            pb.b[j][tp] = L.lo_on ? __builtin_bit_cast(v8i, __builtin_shufflevector(v, z, 0, 1, 2, 3, 4, 5, 6, 7))
+                                  : __builtin_bit_cast(v8i, __builtin_shufflevector(z, v, 0, 1, 2, 3, 4, 5, 6, 7));
+            pb.dx[j][tp] = ok ? a.scales[blk] : 0.0f;
+        }
     }
 }
 
@@ -254,36 +212,37 @@ __device__ __attribute__((always_inline)) inline TileView tile_view(const uint8_
     return v;
 }
 
-// A special E8M0 (outside [4, 240]) in the tile's valid blocks: the tile's
-// rows are then recomputed with the integer decode, so the MFMA results of
-// such a tile are unused.
+// A special E8M0 (outside [4, 240]) in the blocks this wave multiplied of a
+// tile's valid rows: the tile's rows are then recomputed with the integer
+// decode, so the MFMA results of such a tile are unused.
 __device__ inline bool tile_special(const TileView &v, bool row_ok) {
     return row_ok && (v.emin < (uint32_t)kEMin || v.emax > (uint32_t)kEMax);
 }
 
-// NC consecutive chunks from c0: all their LDS reads, then their A operands,
-// then all their MFMAs back to back, then the FMAs that apply d_x (in chunk
-// order per accumulator), so no FMA waits on the MFMA issued just before it.
-template <int NP, bool MASK, int NC>
-__device__ __attribute__((always_inline)) inline void chunk_run(TileView &v, int c0, int nb, const LaneRole &L,
-                                                                const PassRole &P, float acc[2][4]) {
-    ChunkRaw<NP> r[NC];
+// Chunk c (the wave's j-th) of two row tiles r0, r0 + 1: their LDS reads,
+// then the A operands, then the MFMAs back to back, then the FMAs that apply
+// d_x (in chunk order per accumulator, so no FMA waits on the MFMA issued
+// just before it).  MASK: the chunk holds blocks past nb, which get scale
+// 2^0 (their B operands and d_x are zero, so they add 0) and stay out of the
+// special-scale check.
+template <int NP, bool MASK>
+__device__ __attribute__((always_inline)) inline void chunk_tiles(TileView (&tv)[4], int r0, int c, int j, int nb,
+                                                                  const LaneRole &L, const PassB &pb,
+                                                                  float (&acc)[2][2][4]) {
+    uint32_t d[2][5];
 #pragma unroll
-    for (int h = 0; h < NC; h++) chunk_fetch<NP>(r[h], v.pa, P, c0 + h);
-    // d_x is first needed after the MFMAs; naming it here keeps its reads
-    // with the others, behind one wait, rather than late behind a second.
+    for (int h = 0; h < 2; h++)
 #pragma unroll
-    for (int h = 0; h < NC; h++)
+        for (int i = 0; i < 5; i++) d[h][i] = tv[r0 + h].pa[17 * c + i];
+    v8i A[2];
+    int sa[2];
 #pragma unroll
-        for (int tp = 0; tp < NP; tp++) asm volatile("" : "+v"(r[h].x[tp]));
-    v8i A[NC];
-    int sa[NC];
-#pragma unroll
-    for (int h = 0; h < NC; h++) {
-        const uint32_t ev = __builtin_amdgcn_ubfe(r[h].d[0], v.esh, 8u);
+    for (int h = 0; h < 2; h++) {
+        TileView &v = tv[r0 + h];
+        const uint32_t ev = __builtin_amdgcn_ubfe(d[h][0], v.esh, 8u);
         sa[h] = (int)ev;
         if (MASK) {
-            const bool in = 4 * (c0 + h) + L.gb < nb;
+            const bool in = 4 * c + L.gb < nb;
             sa[h] = in ? sa[h] : 127;
             v.emin = in ? min(v.emin, ev) : v.emin;
             v.emax = in ? max(v.emax, ev) : v.emax;
@@ -291,65 +250,39 @@ __device__ __attribute__((always_inline)) inline void chunk_run(TileView &v, int
             v.emin = min(v.emin, ev);
             v.emax = max(v.emax, ev);
         }
-        A[h] = v8i{(int)__builtin_amdgcn_perm(r[h].d[1], r[h].d[0], v.sel), (int)__builtin_amdgcn_perm(r[h].d[2], r[h].d[1], v.sel),
-                   (int)__builtin_amdgcn_perm(r[h].d[3], r[h].d[2], v.sel), (int)__builtin_amdgcn_perm(r[h].d[4], r[h].d[3], v.sel),
+        A[h] = v8i{(int)__builtin_amdgcn_perm(d[h][1], d[h][0], v.sel), (int)__builtin_amdgcn_perm(d[h][2], d[h][1], v.sel),
+                   (int)__builtin_amdgcn_perm(d[h][3], d[h][2], v.sel), (int)__builtin_amdgcn_perm(d[h][4], d[h][3], v.sel),
                    0, 0, 0, 0};
     }
-    v4f dd[NC][NP];
+    v4f dd[2][NP];
 #pragma unroll
-    for (int h = 0; h < NC; h++)
+    for (int h = 0; h < 2; h++)
 #pragma unroll
         for (int tp = 0; tp < NP; tp++) {
-            const v8i B = __builtin_bit_cast(v8i, __builtin_shufflevector(r[h].blo[tp], r[h].bhi[tp], 0, 1, 2, 3, 4, 5, 6, 7));
             const v4f z = {0.0f, 0.0f, 0.0f, 0.0f};
-            dd[h][tp] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A[h], B, z, 4, 0, 0, sa[h], 0, L.sb);
+            dd[h][tp] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A[h], pb.b[j][tp], z, 4, 0, 0, sa[h], 0, L.sb);
         }
 #pragma unroll
-    for (int h = 0; h < NC; h++)
+    for (int h = 0; h < 2; h++)
 #pragma unroll
         for (int tp = 0; tp < NP; tp++)
 #pragma unroll
-            for (int k = 0; k < 4; k++) acc[tp][k] = __builtin_fmaf(dd[h][tp][k], r[h].x[tp], acc[tp][k]);
+            for (int k = 0; k < 4; k++)
+                acc[h][tp][k] = __builtin_fmaf(dd[h][tp][k], pb.dx[j][tp], acc[h][tp][k]);
 }
 
-template <int NP, bool MASK>
-__device__ __attribute__((always_inline)) inline void chunk_quad(TileView &v, int c0, int nb, const LaneRole &L, const PassRole &P, float acc[2][4]) {
-    chunk_run<NP, MASK, 4>(v, c0, nb, L, P, acc);
-}
-
-template <int NP, bool MASK>
-__device__ __attribute__((always_inline)) inline void chunk_pair(TileView &v, int c0, int nb, const LaneRole &L, const PassRole &P, float acc[2][4]) {
-    chunk_run<NP, MASK, 2>(v, c0, nb, L, P, acc);
-}
-
-// Part `part` (0..2) of the chunks of wave half h (the waves of a row tile
-// split its chunks in halves, each in three parts; before each part a wave
-// issues one group of the next tile's loads).  24 chunks (nb in [89, 96]:
-// the GPT-OSS dimension 2880 has nb = 90): half h takes chunks 12h..12h+11
-// as three straight-line quads, chunks 22-23 (possibly past nb) masked; any
-// other even chunk count: half h takes half of the chunk pairs, split over
-// the three parts, the pairs holding blocks past nb masked.
+// The wave's chunk c (its j-th) of row tiles r0, r0 + 1.  A tile past the
+// matrix's rows is multiplied too (whatever its LDS region holds; E2M1 codes
+// are finite): its results are never stored and its rows are not checked
+// for special scales.
 template <int NP>
-__device__ __attribute__((always_inline)) inline void tile_part(int part, int h, TileView &v, int nb, int nch,
-                                                                const LaneRole &L, const PassRole &P, float acc[2][4]) {
-    if (nch == 24) {
-        const int c0 = 12 * h + 4 * part;
-        if (c0 < 20) {
-            chunk_quad<NP, false>(v, c0, nb, L, P, acc);
-        } else {
-            chunk_pair<NP, false>(v, 20, nb, L, P, acc);
-            chunk_pair<NP, true>(v, 22, nb, L, P, acc);
-        }
-        return;
-    }
-    const int npairs = nch / 2, nfull = nb / 8;  // pairs, and pairs whose 8 blocks are all < nb
-    const int p0 = h ? npairs / 2 : 0, np = h ? npairs - npairs / 2 : npairs / 2;
-    for (int p = p0 + part * np / 3; p < p0 + (part + 1) * np / 3; p++) {
-        if (p < nfull)
-            chunk_pair<NP, false>(v, 2 * p, nb, L, P, acc);
-        else
-            chunk_pair<NP, true>(v, 2 * p, nb, L, P, acc);
-    }
+__device__ __attribute__((always_inline)) inline void chunk_pair(TileView (&tv)[4], int r0, int c, int j, int nb,
+                                                                 const LaneRole &L, const PassB &pb,
+                                                                 float (&acc)[2][2][4]) {
+    if (4 * c + 3 < nb)
+        chunk_tiles<NP, false>(tv, r0, c, j, nb, L, pb, acc);
+    else
+        chunk_tiles<NP, true>(tv, r0, c, j, nb, L, pb, acc);
 }
 
 // Sum over each group of eight lanes (every lane of the group gets it),
@@ -428,22 +361,26 @@ __device__ inline int pick4(const int (&v)[kTokPerPass], int t) {
 }
 
 // Persistent workgroups, one per CU, of eight waves: workgroup b takes work
-// items [b*W/G, (b+1)*W/G) of the W = total passes x row tiles, in order, so
-// consecutive items share an expert's token pass and its staged token
-// tables, and every workgroup streams the same number of weight bytes.
-// Gate/up units are 32 output rows (row tiles 0-1 gate, 2-3 up, so SwiGLU
-// and the Q8_0 of the 32-element act block stay in the workgroup); down and
-// single-expert units are 64 rows; a row tile is 16 rows.  Waves r and r + 4
-// (the same SIMD) share row tile r's image: each loads half of its load
-// groups and multiplies half of its chunks, and their partial row sums are
-// added in the epilogue, so every SIMD runs two waves that hide each
-// other's latencies.
+// items [b*W/G, (b+1)*W/G) of the W = total passes x units, in order, so
+// consecutive items share an expert's token pass.  Gate/up units are 32
+// output rows (row tiles 0-1 gate, 2-3 up, so SwiGLU and the Q8_0 of the
+// 32-element act block stay in the workgroup); down and single-expert units
+// are 64 rows; a row tile is 16 rows.
 //
-// Each step: wait for the prefetched tile and write it (and, at a new pass,
-// the token tables) to LDS; flush staged outputs if the stage is full;
-// multiply, issuing the next unit's load groups between parts of the
-// multiply; reduce and stage the unit's outputs.  The only wait for global
-// loads is at the top of a step, for loads issued during the step before.
+// The waves split the unit's K range, not its rows: wave w multiplies chunks
+// w, w + 8, w + 16 of all four row tiles, so its B operands (the pass's
+// tokens, block-diagonal) are loaded into registers once per pass and each
+// tile image in LDS is read once, as A.  Wave w streams half of tile
+// (w & 3)'s image: the image's load groups are split between waves w and
+// w ^ 4.  Each wave's partial row sums go to LDS; every kStage units (and at
+// the end) the workgroup adds the eight partials of each output in wave
+// order and applies the epilogue: bias, and for gate/up the clamped SwiGLU
+// and the Q8_0 of the act block.
+//
+// Each step: wait for this wave's prefetched groups; barrier (every wave is
+// past the previous unit's multiply); write the groups to LDS; flush staged
+// units when the stage is full; barrier; multiply, issuing the next unit's
+// load groups between its chunks; write the partial sums.
 template <int MODE>
 __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(2))) void k_mx_mfma(MxMfmaArgs a, const int32_t *__restrict__ r_active,
                                                                       const int32_t *__restrict__ r_offsets,
@@ -451,56 +388,44 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(2))) void k
                                                                       const int32_t *__restrict__ r_list,
                                                                       const int32_t *__restrict__ r_n_active) {
     extern __shared__ __align__(16) uint8_t smem_b[];
+    constexpr int kStage = kStageUnits;
+    constexpr int kUnitRows = MODE == kGateUp ? 32 : 64;
+    constexpr int kNBias = MODE == kGateUp ? 2 : 1;
     // Output pointers of the epilogue, kept in LDS rather than in scalar
     // registers across the loop.
+    typedef __attribute__((address_space(1))) float gf32;
+    typedef __attribute__((address_space(1))) int8_t gi8;
+    typedef __attribute__((address_space(1))) uint8_t gu8;
     struct EpiPtrs {
-        float *out, *tap0, *tap1, *act_scales;
-        int8_t *act_codes;
-        uint8_t *act_mxtab, *act_blocks34;
+        gf32 *out, *tap0, *tap1, *act_scales;
+        gi8 *act_codes;
+        gu8 *act_mxtab, *act_blocks34;
     };
     __shared__ EpiPtrs s_epi;
-    // Partial row sums of a unit per wave half and row tile, and the waves'
-    // special-scale flags (double-buffered by step parity, so a step's
-    // staging and the next step's sums need no barrier apart).
-    __shared__ float s_res[2][2][4][16][kTokPerPass];
-    __shared__ int s_special[2][kWaves];
-    // Outputs of finished units, written to global memory kStageUnits units
-    // at a time, at the top of a step.  Gate/up also stages each act block's
-    // Q8_0 codes, digit-table bytes and fp16 scale bits.
-    constexpr int kStage = MxTraits<MODE>::kStageUnits;
-    constexpr int kUnitRows = MxTraits<MODE>::kUnitRows;
-    constexpr int kQStage = MODE == kGateUp ? kStage : 1;
-    __shared__ float s_stage[kStage][MxTraits<MODE>::kStageVals][kTokPerPass][kUnitRows];
-    __shared__ int8_t s_sq[kQStage][kTokPerPass][32];
-    __shared__ uint8_t s_smx[kQStage][kTokPerPass][64];
-    __shared__ uint16_t s_sdh[kQStage][kTokPerPass];
+    // Per staged unit: partial row sums [wave][tile][row][token], the
+    // waves' special-scale tile masks, biases, and where the unit's outputs go.
+    __shared__ float s_part[kStage][kWaves][4][16][kTokPerPass];
+    __shared__ int s_special[kStage][kWaves];
+    __shared__ float s_bias[kStage][kNBias][kUnitRows];
     __shared__ int s_stage_ent[kStage][kTokPerPass];
-    __shared__ int s_stage_tile[kStage];
-    __shared__ int s_stage_nt[kStage];
+    __shared__ int s_stage_tile[kStage], s_stage_nt[kStage], s_stage_e[kStage];
 
     const int nb = a.nb;
-    const int nbp = (nb + 7) & ~7;  // token tables padded with zero blocks to whole chunk pairs
-    const int nch = nbp / 4;
     const uint32_t row_bytes = (uint32_t)nb * kMxBlock;
     const int ngroups = (tile_loads(nb) + 3) / 4;
     const int region = tile_region(nb);
     // wave-uniform: keeps per-wave descriptors and offsets in scalar registers
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int rt4 = wave & 3, half = wave >> 2;  // row tile, and which half of it this wave takes
+    const int rt4 = wave & 3, half = wave >> 2;  // the row tile this wave loads, and which half of its groups
     // load groups of this wave: [g0, g0 + gmine)
     const int g0 = half ? (ngroups + 1) / 2 : 0;
     const int gmine = half ? ngroups / 2 : (ngroups + 1) / 2;
-    // LDS: row tiles' images, then [tok][nbp][64] digit tables, [tok][nbp] d_x, zeros
-    uint8_t *img = smem_b + (size_t)rt4 * region;
-    uint8_t *s_mx = smem_b + (size_t)4 * region;
-    // LDS address of this lane's 16 bytes of the image's first group of this wave
     typedef __attribute__((address_space(3))) uint8_t lds_u8;
-    const uint32_t img_lds =
-        (uint32_t)reinterpret_cast<uintptr_t>((lds_u8 *)img) + 4096u * (uint32_t)g0 + 16u * (uint32_t)lane;
-    float *s_dx = reinterpret_cast<float *>(s_mx + (size_t)kTokPerPass * nbp * 64);
-    uint8_t *s_zero = reinterpret_cast<uint8_t *>(s_dx + kTokPerPass * nbp);  // nbp * 64 bytes of zeros
+    // LDS address of this lane's 16 bytes of the first group this wave loads
+    const uint32_t img_lds = (uint32_t)reinterpret_cast<uintptr_t>((lds_u8 *)(smem_b + (size_t)rt4 * region)) +
+                             4096u * (uint32_t)g0 + 16u * (uint32_t)lane;
 
-    const int tile_rows = MODE == kGateUp ? 32 : 64;
+    const int tile_rows = kUnitRows;
     const int tiles = (a.rows + tile_rows - 1) / tile_rows;
     const Route rt{r_active, r_offsets, r_pass_off, r_list};
     const int n_slots = MODE == kRows ? 1 : *r_n_active;
@@ -521,8 +446,10 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(2))) void k
         slot0 = ones - 1;
     }
 
-    const int m = MODE == kGateUp ? (rt4 >> 1) : 0;
-    const int roff = MODE == kGateUp ? (rt4 & 1) * 16 : rt4 * 16;
+    // matrix and first row (within the unit) of each row tile
+    auto tile_m = [](int r) { return MODE == kGateUp ? (r >> 1) : 0; };
+    auto tile_roff = [](int r) { return MODE == kGateUp ? (r & 1) * 16 : r * 16; };
+    const int m_load = tile_m(rt4), roff_load = tile_roff(rt4);
     LaneRole L;
     L.i = lane & 15;
     L.gb = lane >> 4;
@@ -534,15 +461,16 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(2))) void k
     L.hi_on = L.gc == (L.gb >> 1) + 2;
     L.boff = part * 32 + 16 * (L.gb & 1);
     L.sb = (L.gb == L.gc) ? (part == 0 ? 131 : 127) : 127;
-    if (tid == 0) s_epi = EpiPtrs{a.out, a.tap[0], a.tap[1], a.act_scales, a.act_codes, a.act_mxtab, a.act_blocks34};
-    for (int i = tid; i < nbp * 4; i += kWG) reinterpret_cast<u32x4v *>(s_zero)[i] = u32x4v{0u, 0u, 0u, 0u};
+    if (tid == 0)
+        s_epi = EpiPtrs{(gf32 *)a.out,        (gf32 *)a.tap[0],    (gf32 *)a.tap[1],      (gf32 *)a.act_scales,
+                        (gi8 *)a.act_codes, (gu8 *)a.act_mxtab, (gu8 *)a.act_blocks34};
 
-    // Epilogue element of this thread: gate/up: row tid&31 of the unit,
-    // token tid>>5 (waves 0-1); down/rows: row tid&63, token tid>>6 (waves 0-3).
-    const int erow = MODE == kGateUp ? (tid & 31) : (tid & 63);
+    // Bias element of this thread (rows of a unit): threads tid < kUnitRows
+    // stage row tid of each unit's biases.
+    const int brow_l = tid & (kUnitRows - 1);
     const BiasView bv0 = make_bias_view(a.bias[0], a.bias_bytes[0], a.bias_type[0]);
     const BiasView bv1 = make_bias_view(a.bias[1], a.bias_bytes[1], a.bias_type[1]);
-    const uint8_t *wbase = a.w[m];
+    const uint8_t *wload = a.w[m_load];
 
     Cursor cur;
     cur.w = w0;
@@ -552,10 +480,8 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(2))) void k
     slot_info<MODE>(a, rt, cur);
 
     // Registers of the next unit: this wave's groups of its tile image, and
-    // the epilogue element's raw bias words.
+    // the bias words of this thread's row.
     TileRegs tr;
-    // the next unit's tile: descriptor, aligned start of this wave's groups,
-    // and whether this wave loads it
     u32x4v nrs = {0u, 0u, 0u, 0u};
     uint32_t na0 = 0u;
     bool nxt_ok = false;
@@ -569,10 +495,10 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(2))) void k
     };
     uint32_t b0r = 0u, b1r = 0u;
     auto prefetch = [&](const Cursor &c) {
-        const uint32_t brow = (uint32_t)c.e * (uint32_t)a.rows + (uint32_t)(c.tile * tile_rows + erow);
+        const uint32_t brow = (uint32_t)c.e * (uint32_t)a.rows + (uint32_t)(c.tile * tile_rows + brow_l);
         b0r = bias_raw(bv0, brow);
         if (MODE == kGateUp) b1r = bias_raw(bv1, brow);
-        const int row0 = c.tile * tile_rows + roff;
+        const int row0 = c.tile * tile_rows + roff_load;
         nxt_ok = false;
         if (row0 < a.rows) {
             // The expert matrix from the 16-byte boundary at or below its
@@ -580,7 +506,7 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(2))) void k
             // that crosses the range's end reads zeros, and the bytes up to
             // that boundary share the last byte's page); loads past it read
             // zeros.  Bytes past the matrix only reach rows past a.rows.
-            const uintptr_t mb = reinterpret_cast<uintptr_t>(wbase + (uint64_t)c.e * a.expert_bytes);
+            const uintptr_t mb = reinterpret_cast<uintptr_t>(wload + (uint64_t)c.e * a.expert_bytes);
             const uint32_t le = (uint32_t)(mb & 15u);
             const uint64_t base = mb - le;
             // descriptor words: base, base_hi (stride 0), num_records, format
@@ -592,49 +518,86 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(2))) void k
         }
     };
 
-    int staged_slot = -1, staged_p = -1, npair = 0;
-    PassRole PR;
-    float acc[2][4];
-#pragma unroll
-    for (int p = 0; p < 2; p++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) acc[p][i] = 0.0f;
-
-    // Write out the staged units (all waves, after a barrier).  Gate/up:
-    // thread-per-element act (for the tap), the gate/up taps and the act
-    // blocks' Q8_0 in every layout (the unit is one Q8_0 block of each
-    // token's act row); down: thread-per-element results.
-    int n_staged = 0;
+    // Adds each output's eight partials in wave order and writes the staged
+    // units out.  Row tiles with special scales are first recomputed with
+    // the integer decode (their sums replace wave 0's partials, the others
+    // zeroed).  Called by every thread after a barrier; the caller's next
+    // barrier separates it from the stage's reuse.
     auto flush = [&](int count) {
+        int spec = 0;
+        for (int k = 0; k < count; k++)
+#pragma unroll
+            for (int v = 0; v < kWaves; v++) spec |= s_special[k][v];
+        if (spec) {
+            for (int ci = wave; ci < 4 * count; ci += kWaves) {
+                const int k = ci >> 2, r = ci & 3;
+                int mask = 0;
+#pragma unroll
+                for (int v = 0; v < kWaves; v++) mask |= s_special[k][v];
+                if (!((mask >> r) & 1)) continue;
+                const int e = s_stage_e[k], nt = s_stage_nt[k];
+                const int row0 = s_stage_tile[k] * tile_rows + tile_roff(r);
+                const ByteView cview = make_view(a.w[tile_m(r)] + (uint64_t)e * a.expert_bytes, a.expert_bytes);
+                const int row_l = lane >> 2, sub = lane & 3;
+                const int row = row0 + row_l;
+                const uint32_t pos = (uint32_t)(row < a.rows ? row : 0) * row_bytes;
+                for (int t = 0; t < nt; t++) {
+                    const int ent = s_stage_ent[k][t];
+                    const int ar = MODE == kGateUp ? ent / a.topk : ent;
+                    const uint32_t *codes = reinterpret_cast<const uint32_t *>(a.codes + (size_t)ar * nb * 32);
+                    const float v = lut_row_dot(cview, pos, nb, codes, a.scales + (size_t)ar * nb, sub);
+                    if (sub == 0) {
+                        s_part[k][0][r][row_l][t] = v;
+#pragma unroll
+                        for (int q = 1; q < kWaves; q++) s_part[k][q][r][row_l][t] = 0.0f;
+                    }
+                }
+            }
+            lds_barrier();
+        }
         const EpiPtrs ep = s_epi;
         if constexpr (MODE == kGateUp) {
-            for (int i = tid; i < count * kTokPerPass * 32; i += kWG) {
-                const int k = i >> 7, t = (i >> 5) & 3, e = i & 31;
-                if (t >= s_stage_nt[k]) continue;
-                const int tile = s_stage_tile[k], ent = s_stage_ent[k][t];
-                const int r = tile * 32 + e;
-                if (r < a.rows) {
-                    const size_t o = (size_t)ent * a.rows + r;
-                    if (ep.out) ep.out[o] = s_stage[k][0][t][e];
-                    if (ep.tap0) ep.tap0[o] = s_stage[k][1][t][e];
-                    if (ep.tap1) ep.tap1[o] = s_stage[k][2][t][e];
+            // thread: unit k, token t, act row e (a half-wave per token)
+            const int k = tid >> 7, t = (tid >> 5) & 3, e = tid & 31;
+            if (k < count) {
+                const int rg = e >> 4, ri = e & 15;
+                float gv = s_part[k][0][rg][ri][t], uv = s_part[k][0][2 + rg][ri][t];
+#pragma unroll
+                for (int v = 1; v < kWaves; v++) {
+                    gv += s_part[k][v][rg][ri][t];
+                    uv += s_part[k][v][2 + rg][ri][t];
                 }
-                if (ep.act_codes && tile * 32 + 32 <= a.rows) {
-                    const size_t blk = (size_t)ent * (a.rows / 32) + tile;
-                    const int8_t qv = s_sq[k][t][e];
-                    const uint16_t dh = s_sdh[k][t];
-                    ep.act_codes[blk * 32 + e] = qv;
-                    if (ep.act_mxtab) {
-                        ep.act_mxtab[blk * 64 + e] = s_smx[k][t][e];
-                        ep.act_mxtab[blk * 64 + 32 + e] = s_smx[k][t][32 + e];
+                gv += s_bias[k][0][e];
+                uv += s_bias[k][kNBias - 1][e];
+                const float act = swiglu(gv, uv);
+                uint16_t dh;
+                const int qv = q8_quantize_half(act, lane, &dh);
+                const int tile = s_stage_tile[k];
+                if (t < s_stage_nt[k]) {
+                    const int ent = s_stage_ent[k][t];
+                    const int r = tile * 32 + e;
+                    if (r < a.rows) {
+                        const size_t o = (size_t)ent * a.rows + r;
+                        if (ep.out) ep.out[o] = act;
+                        if (ep.tap0) ep.tap0[o] = gv;
+                        if (ep.tap1) ep.tap1[o] = uv;
                     }
-                    if (ep.act_scales && e == 0) ep.act_scales[blk] = f16_bits_to_f32(dh);
-                    if (ep.act_blocks34) {
-                        if (e == 0) {
-                            ep.act_blocks34[blk * kQ80Block] = (uint8_t)(dh & 0xff);
-                            ep.act_blocks34[blk * kQ80Block + 1] = (uint8_t)(dh >> 8);
+                    if (ep.act_codes && tile * 32 + 32 <= a.rows) {
+                        const size_t blk = (size_t)ent * (a.rows / 32) + tile;
+                        ep.act_codes[blk * 32 + e] = (int8_t)qv;
+                        if (ep.act_mxtab) {
+                            const int pn = 2 * (e & 15) + (e >> 4);  // nibble position of element e
+                            ep.act_mxtab[blk * 64 + pn] = (uint8_t)e4m3_small(qv >> 4);
+                            ep.act_mxtab[blk * 64 + 32 + pn] = (uint8_t)e4m3_small(qv & 15);
                         }
-                        ep.act_blocks34[blk * kQ80Block + 2 + e] = (uint8_t)qv;
+                        if (ep.act_scales && e == 0) ep.act_scales[blk] = f16_bits_to_f32(dh);
+                        if (ep.act_blocks34) {
+                            if (e == 0) {
+                                ep.act_blocks34[blk * kQ80Block] = (uint8_t)(dh & 0xff);
+                                ep.act_blocks34[blk * kQ80Block + 1] = (uint8_t)(dh >> 8);
+                            }
+                            ep.act_blocks34[blk * kQ80Block + 2 + e] = (uint8_t)qv;
+                        }
                     }
                 }
             }
@@ -642,12 +605,21 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(2))) void k
             for (int i = tid; i < count * kTokPerPass * kUnitRows; i += kWG) {
                 const int k = i / (kTokPerPass * kUnitRows), t = (i / kUnitRows) % kTokPerPass, r = i % kUnitRows;
                 const int row = s_stage_tile[k] * kUnitRows + r;
-                if (t < s_stage_nt[k] && row < a.rows)
-                    ep.out[(size_t)s_stage_ent[k][t] * a.rows + row] = s_stage[k][0][t][r];
+                if (t < s_stage_nt[k] && row < a.rows) {
+                    const int rg = r >> 4, ri = r & 15;
+                    float v = s_part[k][0][rg][ri][t];
+#pragma unroll
+                    for (int q = 1; q < kWaves; q++) v += s_part[k][q][rg][ri][t];
+                    ep.out[(size_t)s_stage_ent[k][t] * a.rows + row] = v + s_bias[k][0][r];
+                }
             }
         }
     };
 
+    int staged_slot = -1, staged_p = -1, npair = 0;
+    PassB pb;
+
+    int n_staged = 0;
     PassTokens npt = pass_tokens<MODE>(a, rt, cur);  // tokens of the unit in the registers
     prefetch(cur);
     static_assert(kWaveGroups == 3, "issue list below");
@@ -658,205 +630,132 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(2))) void k
     for (int w = w0; w < w1; w++) {
         const Cursor u = cur;
         const PassTokens pt = npt;
-        const bool new_tab = u.slot != staged_slot || u.p != staged_p;
-        if (new_tab) {
-            // Every wave is past the previous unit's first epilogue barrier,
-            // after its last table read, so the tables are free.  Digit
-            // tables [tok][nbp][64] and d_x [tok][nbp] of the pass's tokens,
-            // zero past nb and for the unused token slots.  A pass change is
-            // rare (each workgroup walks a contiguous range of work items),
-            // so these loads are not prefetched.
-            u32x4v tq[kTabLoads];
-            float tdx[kDxLoads];
-#pragma unroll
-            for (int k = 0; k < kTabLoads; k++) {
-                const int j = tid + kWG * k;  // 16-byte piece of [tok][nbp][64]
-                const int t = j / (4 * nbp), rem = j - t * 4 * nbp, b = rem >> 2;
-                u32x4v v = {0u, 0u, 0u, 0u};
-                if (t < pt.nt && b < nb)
-                    v = *reinterpret_cast<const u32x4v *>(a.mxtab + ((size_t)pick4(pt.arow, t) * nb + b) * 64 +
-                                                          (rem & 3) * 16);
-                tq[k] = v;
-            }
-#pragma unroll
-            for (int k = 0; k < kDxLoads; k++) {
-                const int i = tid + kWG * k;
-                const int t = i / nbp, b = i - t * nbp;
-                float v = 0.0f;
-                if (t < pt.nt && b < nb) v = a.scales[(size_t)pick4(pt.arow, t) * nb + b];
-                tdx[k] = v;
-            }
-#pragma unroll
-            for (int k = 0; k < kTabLoads; k++) {
-                const int j = tid + kWG * k;
-                if (j < 16 * nbp) *reinterpret_cast<u32x4v *>(s_mx + (size_t)j * 16) = tq[k];
-            }
-#pragma unroll
-            for (int k = 0; k < kDxLoads; k++) {
-                const int i = tid + kWG * k;
-                if (i < kTokPerPass * nbp) s_dx[i] = tdx[k];
-            }
-#pragma unroll
-            for (int tp = 0; tp < 2; tp++) {
-                const int t = 2 * tp + L.slot;
-                const uint8_t *tb = s_mx + (t * nbp + L.gc) * 64 + L.boff;
-                PR.bl[tp] = (L.lo_on && t < pt.nt) ? tb : s_zero;
-                PR.bh[tp] = (L.hi_on && t < pt.nt) ? tb : s_zero;
-                PR.dx[tp] = s_dx + t * nbp + L.gc;
-            }
+        if (u.slot != staged_slot || u.p != staged_p) {
+            // A new token pass: its B operands and d_x, loaded before the
+            // wait below so that it covers them (pass changes are rare:
+            // each workgroup walks a contiguous range of work items).
+            load_pass_b(pb, a, pt.arow, pt.nt, L, wave);
             npair = (pt.nt + 1) >> 1;
             staged_slot = u.slot;
             staged_p = u.p;
         }
-        const int row0 = u.tile * tile_rows + roff;
-        const bool wave_ok = row0 < a.rows;
         tile_wait(tr);
-        // Both waves of a row tile have passed the previous unit's first
-        // epilogue barrier, after their last read of the image.
-        if (wave_ok) {
+        // Everything loaded before the wait has arrived; take it now so no
+        // later use waits on the next unit's loads.
+#pragma unroll
+        for (int j = 0; j < kChunksPerWave; j++)
+#pragma unroll
+            for (int tp = 0; tp < 2; tp++) asm volatile("" : "+v"(pb.b[j][tp]), "+v"(pb.dx[j][tp]));
+        uint32_t bw0 = b0r, bw1 = b1r;
+        asm volatile("" : "+v"(bw0), "+v"(bw1));
+        // every wave is past the previous unit's multiply (its image reads)
+        // and has written that unit's partial sums
+        lds_barrier();
+        const int row0_load = u.tile * tile_rows + roff_load;
+        if (row0_load < a.rows) {
             static_assert(kWaveGroups == 3, "stores below");
             if (gmine > 0) tile_store<0>(img_lds, tr);
             if (gmine > 1) tile_store<1>(img_lds + 4096u, tr);
             if (gmine > 2) tile_store<2>(img_lds + 8192u, tr);
         }
-        // The bias words arrived with the tile; take them now so no later
-        // use waits on the next unit's loads.
-        uint32_t bw0 = b0r, bw1 = b1r;
-        asm volatile("" : "+v"(bw0), "+v"(bw1));
-        nxt_ok = false;
-        if (w + 1 < w1) {
-            cursor_advance<MODE>(a, rt, cur, tiles);
-            const bool ntab = cur.slot != u.slot || cur.p != u.p;
-            if (ntab) npt = pass_tokens<MODE>(a, rt, cur);
-            prefetch(cur);
-        }
-        // the other wave's half of the image, and new tables, are in place
-        lds_barrier();
         if (n_staged == kStage) {
             flush(n_staged);
             n_staged = 0;
         }
-
-        const uint8_t *view_base = wbase + (uint64_t)u.e * a.expert_bytes;
-        bool special = false;
-        {
-            const uint32_t lead = (uint32_t)((reinterpret_cast<uintptr_t>(view_base) & 15u) + (uint32_t)row0 * row_bytes) & 15u;
-            TileView tv = tile_view(img, lead + (uint32_t)L.i * row_bytes, L);
-            auto segment = [&](auto gc) {
-                constexpr int G = decltype(gc)::value;
-                issue(gc);
-                if (wave_ok) {
-                    if (npair == 2)
-                        tile_part<2>(G, half, tv, nb, nch, L, PR, acc);
-                    else
-                        tile_part<1>(G, half, tv, nb, nch, L, PR, acc);
-                }
-            };
-            static_assert(kWaveGroups == 3, "segments below");
-            segment(std::integral_constant<int, 0>{});
-            segment(std::integral_constant<int, 1>{});
-            segment(std::integral_constant<int, 2>{});
-            special = wave_ok && tile_special(tv, row0 + L.i < a.rows);
+        nxt_ok = false;
+        if (w + 1 < w1) {
+            cursor_advance<MODE>(a, rt, cur, tiles);
+            if (cur.slot != u.slot || cur.p != u.p) npt = pass_tokens<MODE>(a, rt, cur);
+            prefetch(cur);
         }
-
-        // Sum the eight columns of each token slot (parts h/l x blocks).
-#pragma unroll
-        for (int tp = 0; tp < 2; tp++)
-#pragma unroll
-            for (int i = 0; i < 4; i++) acc[tp][i] = sum8(acc[tp][i]);
-        const int par = w & 1;
-        if ((c16 & 7) == 0) {
-#pragma unroll
-            for (int tp = 0; tp < 2; tp++) {
-                const int t = 2 * tp + L.slot;
-                if (t < pt.nt) {
-#pragma unroll
-                    for (int i = 0; i < 4; i++) s_res[par][half][rt4][4 * L.gb + i][t] = acc[tp][i];
-                }
-            }
-        }
-        const bool wsp = __any(special);
-        if (lane == 0) s_special[par][wave] = wsp ? 1 : 0;
+        // the images are in place, and the flush has read the stage
         lds_barrier();
-        // Row tiles with special scales: the half-0 wave recomputes all 16
-        // rows with the integer decode (workgroup-uniform test, so the
-        // barrier after it is reached by every wave).
-        bool any_special = false;
-#pragma unroll
-        for (int i = 0; i < kWaves; i++) any_special |= s_special[par][i] != 0;
-        if (any_special) {
-            if (half == 0 && (s_special[par][rt4] | s_special[par][rt4 + 4])) {
-                const ByteView cview = make_view(view_base, a.expert_bytes);
-                const int row_l = lane >> 2, sub = lane & 3;
-                const int row = row0 + row_l;
-                const uint32_t pos = (uint32_t)(row < a.rows ? row : 0) * row_bytes;
-                for (int t = 0; t < pt.nt; t++) {
-                    const uint32_t *codes = reinterpret_cast<const uint32_t *>(a.codes + (size_t)pick4(pt.arow, t) * nb * 32);
-                    const float v = lut_row_dot(cview, pos, nb, codes, s_dx + t * nbp, sub);
-                    if (sub == 0) {
-                        s_res[par][0][rt4][row_l][t] = v;
-                        s_res[par][1][rt4][row_l][t] = 0.0f;
-                    }
-                }
-            }
-            lds_barrier();
-        }
-        float(*res0)[16][kTokPerPass] = s_res[par][0];
-        float(*res1)[16][kTokPerPass] = s_res[par][1];
-        const uint32_t brow = (uint32_t)u.e * (uint32_t)a.rows + (uint32_t)(u.tile * tile_rows + erow);
         const int k = n_staged;
+        if (tid < kUnitRows) {
+            const uint32_t brow = (uint32_t)u.e * (uint32_t)a.rows + (uint32_t)(u.tile * tile_rows + tid);
+            s_bias[k][0][tid] = bias_value(bv0, bw0, brow);
+            if (MODE == kGateUp) s_bias[k][kNBias - 1][tid] = bias_value(bv1, bw1, brow);
+        }
         if (tid == 0) {
             s_stage_tile[k] = u.tile;
             s_stage_nt[k] = pt.nt;
+            s_stage_e[k] = u.e;
         }
         if (tid < kTokPerPass) s_stage_ent[k][tid] = pick4(pt.ent, tid);
-        if constexpr (MODE == kGateUp) {
-            // 32 rows x nt tokens (waves 0-1, a half-wave per token): bias,
-            // clamped SwiGLU, and the Q8_0 block of the act row.
-            if (wave < 2) {
-                const int t = tid >> 5;
-                const float b0 = bias_value(bv0, bw0, brow), b1 = bias_value(bv1, bw1, brow);
-                const int rg = erow >> 4, ri = erow & 15;
-                const float gv = (res0[rg][ri][t] + res1[rg][ri][t]) + b0;
-                const float uv = (res0[2 + rg][ri][t] + res1[2 + rg][ri][t]) + b1;
-                const float v = swiglu(gv, uv);
-                uint16_t dh;
-                const int qv = q8_quantize_half(v, lane, &dh);
-                if (t < pt.nt) {
-                    s_stage[k][0][t][erow] = v;
-                    s_stage[k][1][t][erow] = gv;
-                    s_stage[k][2][t][erow] = uv;
-                    s_sq[k][t][erow] = (int8_t)qv;
-                    const int pn = 2 * (erow & 15) + (erow >> 4);  // nibble position of element erow
-                    s_smx[k][t][pn] = (uint8_t)e4m3_small(qv >> 4);
-                    s_smx[k][t][32 + pn] = (uint8_t)e4m3_small(qv & 15);
-                    if (erow == 0) s_sdh[k][t] = dh;
+
+        TileView tv[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const uint8_t *vb = a.w[tile_m(r)] + (uint64_t)u.e * a.expert_bytes;
+            const int row0 = u.tile * tile_rows + tile_roff(r);
+            const uint32_t lead = (uint32_t)((reinterpret_cast<uintptr_t>(vb) & 15u) + (uint32_t)row0 * row_bytes) & 15u;
+            tv[r] = tile_view(smem_b + (size_t)r * region, lead + (uint32_t)L.i * row_bytes, L);
+        }
+        // Two row tiles at a time: the wave's chunks of both, then their
+        // partial sums (add the eight columns of each token slot, parts h/l
+        // x blocks; lane j of each group of eight then holds token pair
+        // j >> 2, row 4 * gb + (j & 3) of the slot: one store per tile).
+        const int nchunks = (nb + 3) >> 2;
+        const int j8 = c16 & 7;
+        int smask = 0;
+#pragma unroll
+        for (int r0 = 0; r0 < 4; r0 += 2) {
+            float acc[2][2][4];
+#pragma unroll
+            for (int h = 0; h < 2; h++)
+#pragma unroll
+                for (int p = 0; p < 2; p++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) acc[h][p][i] = 0.0f;
+            // the next unit's load groups go out one every other chunk
+            // call, spread over the multiply (a wave stalls at a load's
+            // issue while its CU's memory queue is full)
+            auto chunk = [&](auto jc) {
+                constexpr int J = decltype(jc)::value;
+                if constexpr (J % 2 == 0) {
+                    if (r0 == 0) issue(std::integral_constant<int, J / 2>{});
+                } else if constexpr (J == 1) {
+                    if (r0 == 2) issue(std::integral_constant<int, 2>{});
                 }
-            }
-        } else {
-            if (wave < 4) {
-                const int t = tid >> 6;
-                const float b0 = bias_value(bv0, bw0, brow);
-                const int rg = erow >> 4, ri = erow & 15;
-                if (t < pt.nt) s_stage[k][0][t][erow] = (res0[rg][ri][t] + res1[rg][ri][t]) + b0;
+                const int c = wave + kWaves * J;
+                if (c < nchunks) {
+                    if (npair == 2)
+                        chunk_pair<2>(tv, r0, c, J, nb, L, pb, acc);
+                    else
+                        chunk_pair<1>(tv, r0, c, J, nb, L, pb, acc);
+                }
+            };
+            static_assert(kChunksPerWave == 3, "chunks below");
+            chunk(std::integral_constant<int, 0>{});
+            chunk(std::integral_constant<int, 1>{});
+            chunk(std::integral_constant<int, 2>{});
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const int r = r0 + h;
+                float sm[2][4];
+#pragma unroll
+                for (int tp = 0; tp < 2; tp++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) sm[tp][i] = sum8(acc[h][tp][i]);
+                float v = sm[0][0];
+#pragma unroll
+                for (int q = 1; q < 8; q++) v = j8 == q ? sm[q >> 2][q & 3] : v;
+                s_part[k][wave][r][4 * L.gb + (j8 & 3)][2 * (j8 >> 2) + L.slot] = v;
+                const int row0 = u.tile * tile_rows + tile_roff(r);
+                if (__any(tile_special(tv[r], row0 + L.i < a.rows))) smask |= 1 << r;
             }
         }
+        if (lane == 0) s_special[k][wave] = smask;
         ++n_staged;
-#pragma unroll
-        for (int p = 0; p < 2; p++)
-#pragma unroll
-            for (int i = 0; i < 4; i++) acc[p][i] = 0.0f;
-        // the stage is complete before the next step's flush
-        if (n_staged == kStage || w + 1 == w1) lds_barrier();
     }
-    if (n_staged > 0) flush(n_staged);
+    lds_barrier();
+    flush(n_staged);
 }
 
 hipError_t launch_mx_mfma(hipStream_t s, GemvMode mode, const MxMfmaArgs &a, int slots) {
     if (slots <= 0 || a.rows <= 0) return hipSuccess;
     if (a.nb <= 0 || a.nb > kMaxNb) return hipErrorInvalidConfiguration;
-    const size_t nbp = (size_t)(a.nb + 7) / 8 * 8;
-    const size_t lds = 4 * (size_t)tile_region(a.nb) + (size_t)kTokPerPass * nbp * (64 + 4) + nbp * 64;
+    const size_t lds = 4 * (size_t)tile_region(a.nb);
     if (lds > kMaxMxLds) return hipErrorInvalidConfiguration;
     // one-time opt-in to more than 64 KB of dynamic LDS
     static const hipError_t attr = [] {
