@@ -1,7 +1,8 @@
 """Build-time check of k_mx_mfma's inline-assembly weight loads.
 
 The grouped GEMV issues each row tile's loads with inline assembly and waits
-for them with one `s_waitcnt vmcnt(0)` at the top of the next step; the
+for them with one `s_waitcnt vmcnt(0)` at the top of the next step (marked
+with the comment `spt tile wait` in the assembly); the
 compiler does not know that the load registers are written asynchronously.
 This scans the gfx950 assembly of spt_mx_mfma.hip (hipcc -S) and fails if any
 instruction other than the loads, that wait and the LDS stores that consume
@@ -45,8 +46,7 @@ def check_kernel(lines):
         return 'no inline-assembly tile loads found'
     tile = set().union(*[r for _, _, r in issues])
     consumers = {k for k, l in ins if l.startswith('ds_write_b128') and vregs(l.split(',', 1)[1]) & tile}
-    waits = [k for idx, (k, l) in enumerate(ins) if l.startswith('s_waitcnt vmcnt(0)')
-             and any(x[0] in consumers for x in ins[idx + 1: idx + 40])]
+    waits = [k for k, l in enumerate(lines) if 'spt tile wait' in l and l.strip().startswith('s_waitcnt vmcnt(0)')]
     if not waits:
         return 'tile wait not found'
     wait = waits[0]

@@ -130,7 +130,7 @@ __device__ inline void tile_issue(TileRegs &t, uint32_t vo, const u32x4v &rs, ui
 
 __device__ inline void tile_wait(TileRegs &t) {
     static_assert(kWaveGroups == 3, "operand list below");
-    asm volatile("s_waitcnt vmcnt(0)"
+    asm volatile("s_waitcnt vmcnt(0) ; spt tile wait"
                  : "+v"(t.q[0]), "+v"(t.q[1]), "+v"(t.q[2]), "+v"(t.q[3]), "+v"(t.q[4]), "+v"(t.q[5]),
                    "+v"(t.q[6]), "+v"(t.q[7]), "+v"(t.q[8]), "+v"(t.q[9]), "+v"(t.q[10]), "+v"(t.q[11]));
 }
@@ -219,70 +219,94 @@ __device__ inline bool tile_special(const TileView &v, bool row_ok) {
     return row_ok && (v.emin < (uint32_t)kEMin || v.emax > (uint32_t)kEMax);
 }
 
-// Chunk c (the wave's j-th) of two row tiles r0, r0 + 1: their LDS reads,
-// then the A operands, then the MFMAs back to back, then the FMAs that apply
-// d_x (in chunk order per accumulator, so no FMA waits on the MFMA issued
-// just before it).  MASK: the chunk holds blocks past nb, which get scale
-// 2^0 (their B operands and d_x are zero, so they add 0) and stay out of the
-// special-scale check.
-template <int NP, bool MASK>
-__device__ __attribute__((always_inline)) inline void chunk_tiles(TileView (&tv)[4], int r0, int c, int j, int nb,
-                                                                  const LaneRole &L, const PassB &pb,
-                                                                  float (&acc)[2][2][4]) {
-    uint32_t d[2][5];
+// The wave's chunks j < NC (chunk c_j = wave + 8j) of two row tiles r0,
+// r0 + 1: all their LDS reads, then the A operands, then the MFMAs back to
+// back, then the FMAs that apply d_x (in chunk order per accumulator), so
+// the LDS and MFMA latencies are met once per call.  MASKLAST: the last
+// chunk holds blocks past nb, which get scale 2^0 (their B operands and d_x
+// are zero, so they add 0) and stay out of the special-scale check.  A tile
+// past the matrix's rows is multiplied too (whatever its LDS region holds;
+// E2M1 codes are finite): its results are never stored and its rows are not
+// checked for special scales.
+template <int NP, int NC, bool MASKLAST>
+__device__ __attribute__((always_inline)) inline void tile_pair_run(TileView (&tv)[4], int r0, int wave, int nb,
+                                                                    const LaneRole &L, const PassB &pb,
+                                                                    float (&acc)[2][2][4]) {
+    uint32_t d[NC][2][5];
 #pragma unroll
-    for (int h = 0; h < 2; h++)
+    for (int j = 0; j < NC; j++)
 #pragma unroll
-        for (int i = 0; i < 5; i++) d[h][i] = tv[r0 + h].pa[17 * c + i];
-    v8i A[2];
-    int sa[2];
+        for (int h = 0; h < 2; h++)
 #pragma unroll
-    for (int h = 0; h < 2; h++) {
-        TileView &v = tv[r0 + h];
-        const uint32_t ev = __builtin_amdgcn_ubfe(d[h][0], v.esh, 8u);
-        sa[h] = (int)ev;
-        if (MASK) {
-            const bool in = 4 * c + L.gb < nb;
-            sa[h] = in ? sa[h] : 127;
-            v.emin = in ? min(v.emin, ev) : v.emin;
-            v.emax = in ? max(v.emax, ev) : v.emax;
-        } else {
-            v.emin = min(v.emin, ev);
-            v.emax = max(v.emax, ev);
+            for (int i = 0; i < 5; i++) d[j][h][i] = tv[r0 + h].pa[17 * (wave + kWaves * j) + i];
+    v8i A[NC][2];
+    int sa[NC][2];
+#pragma unroll
+    for (int j = 0; j < NC; j++)
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            TileView &v = tv[r0 + h];
+            const uint32_t ev = __builtin_amdgcn_ubfe(d[j][h][0], v.esh, 8u);
+            sa[j][h] = (int)ev;
+            if (MASKLAST && j == NC - 1) {
+                const bool in = 4 * (wave + kWaves * j) + L.gb < nb;
+                sa[j][h] = in ? sa[j][h] : 127;
+                v.emin = in ? min(v.emin, ev) : v.emin;
+                v.emax = in ? max(v.emax, ev) : v.emax;
+            } else {
+                v.emin = min(v.emin, ev);
+                v.emax = max(v.emax, ev);
+            }
+            A[j][h] = v8i{(int)__builtin_amdgcn_perm(d[j][h][1], d[j][h][0], v.sel),
+                          (int)__builtin_amdgcn_perm(d[j][h][2], d[j][h][1], v.sel),
+                          (int)__builtin_amdgcn_perm(d[j][h][3], d[j][h][2], v.sel),
+                          (int)__builtin_amdgcn_perm(d[j][h][4], d[j][h][3], v.sel), 0, 0, 0, 0};
         }
-        A[h] = v8i{(int)__builtin_amdgcn_perm(d[h][1], d[h][0], v.sel), (int)__builtin_amdgcn_perm(d[h][2], d[h][1], v.sel),
-                   (int)__builtin_amdgcn_perm(d[h][3], d[h][2], v.sel), (int)__builtin_amdgcn_perm(d[h][4], d[h][3], v.sel),
-                   0, 0, 0, 0};
-    }
-    v4f dd[2][NP];
+    v4f dd[NC][2][NP];
 #pragma unroll
-    for (int h = 0; h < 2; h++)
+    for (int j = 0; j < NC; j++)
 #pragma unroll
-        for (int tp = 0; tp < NP; tp++) {
-            const v4f z = {0.0f, 0.0f, 0.0f, 0.0f};
-            dd[h][tp] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A[h], pb.b[j][tp], z, 4, 0, 0, sa[h], 0, L.sb);
-        }
+        for (int h = 0; h < 2; h++)
 #pragma unroll
-    for (int h = 0; h < 2; h++)
+            for (int tp = 0; tp < NP; tp++) {
+                const v4f z = {0.0f, 0.0f, 0.0f, 0.0f};
+                dd[j][h][tp] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A[j][h], pb.b[j][tp], z, 4, 0, 0,
+                                                                                sa[j][h], 0, L.sb);
+            }
 #pragma unroll
-        for (int tp = 0; tp < NP; tp++)
+    for (int j = 0; j < NC; j++)
 #pragma unroll
-            for (int k = 0; k < 4; k++)
-                acc[h][tp][k] = __builtin_fmaf(dd[h][tp][k], pb.dx[j][tp], acc[h][tp][k]);
+        for (int h = 0; h < 2; h++)
+#pragma unroll
+            for (int tp = 0; tp < NP; tp++)
+#pragma unroll
+                for (int k = 0; k < 4; k++)
+                    acc[h][tp][k] = __builtin_fmaf(dd[j][h][tp][k], pb.dx[j][tp], acc[h][tp][k]);
 }
 
-// The wave's chunk c (its j-th) of row tiles r0, r0 + 1.  A tile past the
-// matrix's rows is multiplied too (whatever its LDS region holds; E2M1 codes
-// are finite): its results are never stored and its rows are not checked
-// for special scales.
+// The wave's chunks of row tiles r0, r0 + 1: nc (0..kChunksPerWave) of
+// them, the last masked when it holds blocks past nb.
 template <int NP>
-__device__ __attribute__((always_inline)) inline void chunk_pair(TileView (&tv)[4], int r0, int c, int j, int nb,
-                                                                 const LaneRole &L, const PassB &pb,
-                                                                 float (&acc)[2][2][4]) {
-    if (4 * c + 3 < nb)
-        chunk_tiles<NP, false>(tv, r0, c, j, nb, L, pb, acc);
-    else
-        chunk_tiles<NP, true>(tv, r0, c, j, nb, L, pb, acc);
+__device__ __attribute__((always_inline)) inline void tile_pair(TileView (&tv)[4], int r0, int wave, int nc, bool mask_last,
+                                                                int nb, const LaneRole &L, const PassB &pb,
+                                                                float (&acc)[2][2][4]) {
+    static_assert(kChunksPerWave == 3, "cases below");
+    if (nc == 3) {
+        if (mask_last)
+            tile_pair_run<NP, 3, true>(tv, r0, wave, nb, L, pb, acc);
+        else
+            tile_pair_run<NP, 3, false>(tv, r0, wave, nb, L, pb, acc);
+    } else if (nc == 2) {
+        if (mask_last)
+            tile_pair_run<NP, 2, true>(tv, r0, wave, nb, L, pb, acc);
+        else
+            tile_pair_run<NP, 2, false>(tv, r0, wave, nb, L, pb, acc);
+    } else if (nc == 1) {
+        if (mask_last)
+            tile_pair_run<NP, 1, true>(tv, r0, wave, nb, L, pb, acc);
+        else
+            tile_pair_run<NP, 1, false>(tv, r0, wave, nb, L, pb, acc);
+    }
 }
 
 // Sum over each group of eight lanes (every lane of the group gets it),
@@ -379,8 +403,13 @@ __device__ inline int pick4(const int (&v)[kTokPerPass], int t) {
 //
 // Each step: wait for this wave's prefetched groups; barrier (every wave is
 // past the previous unit's multiply); write the groups to LDS; flush staged
-// units when the stage is full; barrier; multiply, issuing the next unit's
-// load groups between its chunks; write the partial sums.
+// units when the stage is full; barrier; multiply (tiles 0-1, then 2-3),
+// issuing the next unit's load groups before each tile pair; write the
+// partial sums.  Measured alternatives, all slower for gate/up at 64 tokens:
+// one wave role loading and another multiplying (208 us against 190 us: one
+// multiplying wave per SIMD leaves the LDS and MFMA latencies exposed), and
+// tile pairs streamed by LDS DMA into a two-deep ring (370 us: in-flight
+// bytes drop to zero at every pair).
 template <int MODE>
 __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(2))) void k_mx_mfma(MxMfmaArgs a, const int32_t *__restrict__ r_active,
                                                                       const int32_t *__restrict__ r_offsets,
@@ -696,6 +725,10 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(2))) void k
         // x blocks; lane j of each group of eight then holds token pair
         // j >> 2, row 4 * gb + (j & 3) of the slot: one store per tile).
         const int nchunks = (nb + 3) >> 2;
+        // this wave's chunks wave + 8j < nchunks; only the last chunk of the
+        // matrix can hold blocks past nb
+        const int nc = nchunks > wave ? min(kChunksPerWave, (nchunks - 1 - wave) / kWaves + 1) : 0;
+        const bool mask_last = nc > 0 && 4 * (wave + kWaves * (nc - 1)) + 3 >= nb;
         const int j8 = c16 & 7;
         int smask = 0;
 #pragma unroll
@@ -707,28 +740,21 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(2))) void k
                 for (int p = 0; p < 2; p++)
 #pragma unroll
                     for (int i = 0; i < 4; i++) acc[h][p][i] = 0.0f;
-            // the next unit's load groups go out one every other chunk
-            // call, spread over the multiply (a wave stalls at a load's
-            // issue while its CU's memory queue is full)
-            auto chunk = [&](auto jc) {
-                constexpr int J = decltype(jc)::value;
-                if constexpr (J % 2 == 0) {
-                    if (r0 == 0) issue(std::integral_constant<int, J / 2>{});
-                } else if constexpr (J == 1) {
-                    if (r0 == 2) issue(std::integral_constant<int, 2>{});
-                }
-                const int c = wave + kWaves * J;
-                if (c < nchunks) {
-                    if (npair == 2)
-                        chunk_pair<2>(tv, r0, c, J, nb, L, pb, acc);
-                    else
-                        chunk_pair<1>(tv, r0, c, J, nb, L, pb, acc);
-                }
-            };
-            static_assert(kChunksPerWave == 3, "chunks below");
-            chunk(std::integral_constant<int, 0>{});
-            chunk(std::integral_constant<int, 1>{});
-            chunk(std::integral_constant<int, 2>{});
+            // the next unit's load groups: two before the first tile pair's
+            // multiplies, one before the second's (a wave stalls at a load's
+            // issue while its CU's memory queue is full: all three at once
+            // measured 218 us for gate/up at 64 tokens against 190 us, one
+            // per pair and one after 195 us)
+            if (r0 == 0) {
+                issue(std::integral_constant<int, 0>{});
+                issue(std::integral_constant<int, 1>{});
+            } else {
+                issue(std::integral_constant<int, 2>{});
+            }
+            if (npair == 2)
+                tile_pair<2>(tv, r0, wave, nc, mask_last, nb, L, pb, acc);
+            else
+                tile_pair<1>(tv, r0, wave, nc, mask_last, nb, L, pb, acc);
 #pragma unroll
             for (int h = 0; h < 2; h++) {
                 const int r = r0 + h;

@@ -25,7 +25,7 @@ def kernel(inside_loop="", before_wait=""):
     return f"""{NAME}:
 \tv_mov_b32_e32 v1, 0
 {issue}.LBB0_1:                                ; =>This Loop Header: Depth=1
-{before_wait}\ts_waitcnt vmcnt(0)
+{before_wait}\ts_waitcnt vmcnt(0) ; spt tile wait
 \tds_write_b128 v2, v[40:43]
 \tds_write_b128 v2, v[44:47] offset:1024
 \tds_write_b128 v2, v[48:51] offset:2048
