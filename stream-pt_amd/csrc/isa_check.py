@@ -49,25 +49,34 @@ def check_kernel(lines):
     waits = [k for k, l in enumerate(lines) if 'spt tile wait' in l and l.strip().startswith('s_waitcnt vmcnt(0)')]
     if not waits:
         return 'tile wait not found'
-    wait = waits[0]
-    hdrs = [k for k, l in enumerate(lines) if 'Loop Header: Depth=1' in l and k < wait]
-    if not hdrs:
+    # the main loop: the outermost loop holding the last tile wait
+    loop = None
+    for k, l in enumerate(lines):
+        if 'Loop Header: Depth=1' not in l or k > waits[-1]:
+            continue
+        label = l.split(':')[0].strip()
+        ends = [j for j, x in ins if re.search(r's_c?branch\w* ' + re.escape(label) + r'$', x)]
+        if ends and max(ends) > waits[-1]:
+            loop = (k, max(ends))
+    if loop is None:
         return 'main loop not found'
-    hdr = max(hdrs)
-    label = lines[hdr].split(':')[0].strip()
-    ends = [k for k, l in ins if re.search(r's_c?branch\w* ' + re.escape(label) + r'$', l)]
-    if not ends:
-        return 'main loop back edge not found'
-    lend = max(ends)
-    allowed = consumers.union(*[ks for _, ks, _ in issues])
+    hdr, lend = loop
+    last_wait = max(w for w in waits if hdr <= w <= lend) if any(hdr <= w <= lend for w in waits) else None
+    if last_wait is None:
+        return 'no tile wait in the main loop'
+    allowed = consumers.union(*[ks for _, ks, _ in issues]) | set(waits)
     bad = []
     for k0, ks, regs in issues:
-        windows = [(k0, wait)] if k0 < hdr else [(k0, lend), (hdr, wait)]
+        # Conservative windows: from the issue to the loop's end (or, before
+        # the loop, to its header), and from the header to the loop's last
+        # tile wait, so every path from an issue to the wait that covers it
+        # lies inside them.
+        windows = [(k0, lend if k0 >= hdr else hdr), (hdr, last_wait)]
         for a, b in windows:
             for k, l in ins:
                 if a <= k <= b and k not in allowed and vregs(l) & regs:
                     bad.append('%d: %s' % (k, l))
-    return '; '.join(bad[:5]) if bad else None
+    return '; '.join(sorted(set(bad))[:5]) if bad else None
 
 
 def main(path):
