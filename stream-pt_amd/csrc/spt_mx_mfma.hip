@@ -504,9 +504,11 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(2))) void k
     Cursor cur;
     cur.w = w0;
     cur.slot = slot0;
-    cur.p = MODE == kRows ? q0 : q0 - rt.pass_off[slot0];
     cur.tile = w0 - q0 * tiles;
-    slot_info<MODE>(a, rt, cur);
+    // The first unit's expert is all its tile loads need: they are issued
+    // before its pass and token list are read (two dependent round trips
+    // fewer before the first weights are in flight).
+    cur.e = MODE == kRows ? a.expert : rt.active[slot0];
 
     // Registers of the next unit: this wave's groups of its tile image, and
     // the bias words of this thread's row.
@@ -649,12 +651,14 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(2))) void k
     PassB pb;
 
     int n_staged = 0;
-    PassTokens npt = pass_tokens<MODE>(a, rt, cur);  // tokens of the unit in the registers
     prefetch(cur);
     static_assert(kWaveGroups == 3, "issue list below");
     issue(std::integral_constant<int, 0>{});
     issue(std::integral_constant<int, 1>{});
     issue(std::integral_constant<int, 2>{});
+    cur.p = MODE == kRows ? q0 : q0 - rt.pass_off[slot0];
+    slot_info<MODE>(a, rt, cur);
+    PassTokens npt = pass_tokens<MODE>(a, rt, cur);  // tokens of the unit in the registers
 
     for (int w = w0; w < w1; w++) {
         const Cursor u = cur;
