@@ -86,7 +86,7 @@ __host__ __device__ constexpr int tile_region(int nb) {
 constexpr int kTileGroups = (tile_loads(kMaxNb) + 3) / 4;  // groups of four 1 KB loads per tile
 constexpr int kWaveGroups = (kTileGroups + 1) / 2;         // of them, loaded by one wave
 constexpr size_t kMaxMxLds = 120 * 1024;  // dynamic LDS; with the static part (< 36 KB) within 160 KB
-constexpr int kStageUnits = 4;             // units whose partial sums are staged before a flush
+constexpr int kStageUnits = 2;             // units per stage set (two sets: one fills while the other is flushed)
 
 // Workgroup barrier ordering LDS only.  All communication between the
 // waves of k_mx_mfma goes through LDS, and __syncthreads() would also wait
@@ -433,11 +433,11 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(2))) void k
     __shared__ EpiPtrs s_epi;
     // Per staged unit: partial row sums [wave][tile][row][token], the
     // waves' special-scale tile masks, biases, and where the unit's outputs go.
-    __shared__ float s_part[kStage][kWaves][4][16][kTokPerPass];
-    __shared__ int s_special[kStage][kWaves];
-    __shared__ float s_bias[kStage][kNBias][kUnitRows];
-    __shared__ int s_stage_ent[kStage][kTokPerPass];
-    __shared__ int s_stage_tile[kStage], s_stage_nt[kStage], s_stage_e[kStage];
+    __shared__ float s_part[2 * kStage][kWaves][4][16][kTokPerPass];
+    __shared__ int s_special[2 * kStage][kWaves];
+    __shared__ float s_bias[2 * kStage][kNBias][kUnitRows];
+    __shared__ int s_stage_ent[2 * kStage][kTokPerPass];
+    __shared__ int s_stage_tile[2 * kStage], s_stage_nt[2 * kStage], s_stage_e[2 * kStage];
 
     const int nb = a.nb;
     const uint32_t row_bytes = (uint32_t)nb * kMxBlock;
@@ -554,33 +554,33 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(2))) void k
     // the integer decode (their sums replace wave 0's partials, the others
     // zeroed).  Called by every thread after a barrier; the caller's next
     // barrier separates it from the stage's reuse.
-    auto flush = [&](int count) {
+    auto flush = [&](int base, int count) {
         int spec = 0;
         for (int k = 0; k < count; k++)
 #pragma unroll
-            for (int v = 0; v < kWaves; v++) spec |= s_special[k][v];
+            for (int v = 0; v < kWaves; v++) spec |= s_special[base + k][v];
         if (spec) {
             for (int ci = wave; ci < 4 * count; ci += kWaves) {
                 const int k = ci >> 2, r = ci & 3;
                 int mask = 0;
 #pragma unroll
-                for (int v = 0; v < kWaves; v++) mask |= s_special[k][v];
+                for (int v = 0; v < kWaves; v++) mask |= s_special[base + k][v];
                 if (!((mask >> r) & 1)) continue;
-                const int e = s_stage_e[k], nt = s_stage_nt[k];
-                const int row0 = s_stage_tile[k] * tile_rows + tile_roff(r);
+                const int e = s_stage_e[base + k], nt = s_stage_nt[base + k];
+                const int row0 = s_stage_tile[base + k] * tile_rows + tile_roff(r);
                 const ByteView cview = make_view(a.w[tile_m(r)] + (uint64_t)e * a.expert_bytes, a.expert_bytes);
                 const int row_l = lane >> 2, sub = lane & 3;
                 const int row = row0 + row_l;
                 const uint32_t pos = (uint32_t)(row < a.rows ? row : 0) * row_bytes;
                 for (int t = 0; t < nt; t++) {
-                    const int ent = s_stage_ent[k][t];
+                    const int ent = s_stage_ent[base + k][t];
                     const int ar = MODE == kGateUp ? ent / a.topk : ent;
                     const uint32_t *codes = reinterpret_cast<const uint32_t *>(a.codes + (size_t)ar * nb * 32);
                     const float v = lut_row_dot(cview, pos, nb, codes, a.scales + (size_t)ar * nb, sub);
                     if (sub == 0) {
-                        s_part[k][0][r][row_l][t] = v;
+                        s_part[base + k][0][r][row_l][t] = v;
 #pragma unroll
-                        for (int q = 1; q < kWaves; q++) s_part[k][q][r][row_l][t] = 0.0f;
+                        for (int q = 1; q < kWaves; q++) s_part[base + k][q][r][row_l][t] = 0.0f;
                     }
                 }
             }
@@ -592,20 +592,20 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(2))) void k
             const int k = tid >> 7, t = (tid >> 5) & 3, e = tid & 31;
             if (k < count) {
                 const int rg = e >> 4, ri = e & 15;
-                float gv = s_part[k][0][rg][ri][t], uv = s_part[k][0][2 + rg][ri][t];
+                float gv = s_part[base + k][0][rg][ri][t], uv = s_part[base + k][0][2 + rg][ri][t];
 #pragma unroll
                 for (int v = 1; v < kWaves; v++) {
-                    gv += s_part[k][v][rg][ri][t];
-                    uv += s_part[k][v][2 + rg][ri][t];
+                    gv += s_part[base + k][v][rg][ri][t];
+                    uv += s_part[base + k][v][2 + rg][ri][t];
                 }
-                gv += s_bias[k][0][e];
-                uv += s_bias[k][kNBias - 1][e];
+                gv += s_bias[base + k][0][e];
+                uv += s_bias[base + k][kNBias - 1][e];
                 const float act = swiglu(gv, uv);
                 uint16_t dh;
                 const int qv = q8_quantize_half(act, lane, &dh);
-                const int tile = s_stage_tile[k];
-                if (t < s_stage_nt[k]) {
-                    const int ent = s_stage_ent[k][t];
+                const int tile = s_stage_tile[base + k];
+                if (t < s_stage_nt[base + k]) {
+                    const int ent = s_stage_ent[base + k][t];
                     const int r = tile * 32 + e;
                     if (r < a.rows) {
                         const size_t o = (size_t)ent * a.rows + r;
@@ -635,13 +635,13 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(2))) void k
         } else {
             for (int i = tid; i < count * kTokPerPass * kUnitRows; i += kWG) {
                 const int k = i / (kTokPerPass * kUnitRows), t = (i / kUnitRows) % kTokPerPass, r = i % kUnitRows;
-                const int row = s_stage_tile[k] * kUnitRows + r;
-                if (t < s_stage_nt[k] && row < a.rows) {
+                const int row = s_stage_tile[base + k] * kUnitRows + r;
+                if (t < s_stage_nt[base + k] && row < a.rows) {
                     const int rg = r >> 4, ri = r & 15;
-                    float v = s_part[k][0][rg][ri][t];
+                    float v = s_part[base + k][0][rg][ri][t];
 #pragma unroll
-                    for (int q = 1; q < kWaves; q++) v += s_part[k][q][rg][ri][t];
-                    ep.out[(size_t)s_stage_ent[k][t] * a.rows + row] = v + s_bias[k][0][r];
+                    for (int q = 1; q < kWaves; q++) v += s_part[base + k][q][rg][ri][t];
+                    ep.out[(size_t)s_stage_ent[base + k][t] * a.rows + row] = v + s_bias[base + k][0][r];
                 }
             }
         }
@@ -650,7 +650,9 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(2))) void k
     int staged_slot = -1, staged_p = -1, npair = 0;
     PassB pb;
 
-    int n_staged = 0;
+    // stage slots kStage * set + i; a full set is flushed during the next
+    // unit's multiply, after its first loads are issued
+    int n_staged = 0, cur_set = 0, pending = -1;
     prefetch(cur);
     static_assert(kWaveGroups == 3, "issue list below");
     issue(std::integral_constant<int, 0>{});
@@ -691,10 +693,6 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(2))) void k
             if (gmine > 1) tile_store<1>(img_lds + 4096u, tr);
             if (gmine > 2) tile_store<2>(img_lds + 8192u, tr);
         }
-        if (n_staged == kStage) {
-            flush(n_staged);
-            n_staged = 0;
-        }
         nxt_ok = false;
         if (w + 1 < w1) {
             cursor_advance<MODE>(a, rt, cur, tiles);
@@ -703,7 +701,7 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(2))) void k
         }
         // the images are in place, and the flush has read the stage
         lds_barrier();
-        const int k = n_staged;
+        const int k = kStage * cur_set + n_staged;
         if (tid < kUnitRows) {
             const uint32_t brow = (uint32_t)u.e * (uint32_t)a.rows + (uint32_t)(u.tile * tile_rows + tid);
             s_bias[k][0][tid] = bias_value(bv0, bw0, brow);
@@ -752,6 +750,10 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(2))) void k
             if (r0 == 0) {
                 issue(std::integral_constant<int, 0>{});
                 issue(std::integral_constant<int, 1>{});
+                if (pending >= 0) {
+                    flush(kStage * pending, kStage);
+                    pending = -1;
+                }
             } else {
                 issue(std::integral_constant<int, 2>{});
             }
@@ -776,10 +778,15 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(2))) void k
             }
         }
         if (lane == 0) s_special[k][wave] = smask;
-        ++n_staged;
+        if (++n_staged == kStage) {
+            pending = cur_set;
+            cur_set ^= 1;
+            n_staged = 0;
+        }
     }
     lds_barrier();
-    flush(n_staged);
+    if (pending >= 0) flush(kStage * pending, kStage);
+    if (n_staged > 0) flush(kStage * cur_set, n_staged);
 }
 
 hipError_t launch_mx_mfma(hipStream_t s, GemvMode mode, const MxMfmaArgs &a, int slots) {
