@@ -135,6 +135,14 @@ __device__ inline void tile_wait(TileRegs &t) {
                    "+v"(t.q[6]), "+v"(t.q[7]), "+v"(t.q[8]), "+v"(t.q[9]), "+v"(t.q[10]), "+v"(t.q[11]));
 }
 
+// After the stores of a step: the LDS writes are complete, so their data
+// registers have been read before the next loads overwrite them.
+__device__ inline void tile_stored(TileRegs &t) {
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(t.q[0]), "+v"(t.q[1]), "+v"(t.q[2]), "+v"(t.q[3]), "+v"(t.q[4]), "+v"(t.q[5]),
+                   "+v"(t.q[6]), "+v"(t.q[7]), "+v"(t.q[8]), "+v"(t.q[9]), "+v"(t.q[10]), "+v"(t.q[11])::"memory");
+}
+
 template <int G>
 __device__ inline void tile_store(uint32_t lds, const TileRegs &t) {
     asm volatile(
@@ -683,6 +691,13 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(2))) void k
             for (int tp = 0; tp < 2; tp++) asm volatile("" : "+v"(pb.b[j][tp]), "+v"(pb.dx[j][tp]));
         uint32_t bw0 = b0r, bw1 = b1r;
         asm volatile("" : "+v"(bw0), "+v"(bw1));
+        // the next unit's cursor and load addresses, before the barrier
+        nxt_ok = false;
+        if (w + 1 < w1) {
+            cursor_advance<MODE>(a, rt, cur, tiles);
+            if (cur.slot != u.slot || cur.p != u.p) npt = pass_tokens<MODE>(a, rt, cur);
+            prefetch(cur);
+        }
         // every wave is past the previous unit's multiply (its image reads)
         // and has written that unit's partial sums
         lds_barrier();
@@ -693,13 +708,11 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(2))) void k
             if (gmine > 1) tile_store<1>(img_lds + 4096u, tr);
             if (gmine > 2) tile_store<2>(img_lds + 8192u, tr);
         }
-        nxt_ok = false;
-        if (w + 1 < w1) {
-            cursor_advance<MODE>(a, rt, cur, tiles);
-            if (cur.slot != u.slot || cur.p != u.p) npt = pass_tokens<MODE>(a, rt, cur);
-            prefetch(cur);
-        }
-        // the images are in place, and the flush has read the stage
+        // The next unit's first load group goes out before the barrier
+        // (a second one there measured 189 us for gate/up at 64 tokens,
+        // against 176 us; none, 188 us); after it the images are in place.
+        tile_stored(tr);
+        issue(std::integral_constant<int, 0>{});
         lds_barrier();
         const int k = kStage * cur_set + n_staged;
         if (tid < kUnitRows) {
@@ -748,7 +761,6 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(2))) void k
             // measured 218 us for gate/up at 64 tokens against 190 us, one
             // per pair and one after 195 us)
             if (r0 == 0) {
-                issue(std::integral_constant<int, 0>{});
                 issue(std::integral_constant<int, 1>{});
                 if (pending >= 0) {
                     flush(kStage * pending, kStage);
