@@ -705,14 +705,18 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(2))) void k
         if (row0_load < a.rows) {
             static_assert(kWaveGroups == 3, "stores below");
             if (gmine > 0) tile_store<0>(img_lds, tr);
+        }
+        // the first group's registers are free once its stores are done
+        tile_stored(tr);
+        issue(std::integral_constant<int, 0>{});
+        if (row0_load < a.rows) {
             if (gmine > 1) tile_store<1>(img_lds + 4096u, tr);
             if (gmine > 2) tile_store<2>(img_lds + 8192u, tr);
         }
-        // The next unit's first load group goes out before the barrier
-        // (a second one there measured 189 us for gate/up at 64 tokens,
-        // against 176 us; none, 188 us); after it the images are in place.
-        tile_stored(tr);
-        issue(std::integral_constant<int, 0>{});
+        // The next unit's first load group went out between the stores
+        // (measured for gate/up at 64 tokens: 172 us; after all the stores
+        // 176 us; a second group there too 189 us; none before the barrier
+        // 188 us); after the barrier the images are in place.
         lds_barrier();
         const int k = kStage * cur_set + n_staged;
         if (tid < kUnitRows) {
