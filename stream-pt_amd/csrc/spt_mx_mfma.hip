@@ -759,11 +759,11 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(2))) void k
                 for (int p = 0; p < 2; p++)
 #pragma unroll
                     for (int i = 0; i < 4; i++) acc[h][p][i] = 0.0f;
-            // the next unit's load groups: two before the first tile pair's
-            // multiplies, one before the second's (a wave stalls at a load's
-            // issue while its CU's memory queue is full: all three at once
-            // measured 218 us for gate/up at 64 tokens against 190 us, one
-            // per pair and one after 195 us)
+            // the next unit's second load group before the first tile
+            // pair's multiplies, the third before the second's (a wave
+            // stalls at a load's issue while its CU's memory queue is full;
+            // measured for gate/up at 64 tokens: both here 184 us, against
+            // 172 us)
             if (r0 == 0) {
                 issue(std::integral_constant<int, 1>{});
                 if (pending >= 0) {
