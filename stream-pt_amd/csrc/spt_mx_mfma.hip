@@ -404,20 +404,23 @@ __device__ inline int pick4(const int (&v)[kTokPerPass], int t) {
 // tokens, block-diagonal) are loaded into registers once per pass and each
 // tile image in LDS is read once, as A.  Wave w streams half of tile
 // (w & 3)'s image: the image's load groups are split between waves w and
-// w ^ 4.  Each wave's partial row sums go to LDS; every kStage units (and at
-// the end) the workgroup adds the eight partials of each output in wave
-// order and applies the epilogue: bias, and for gate/up the clamped SwiGLU
-// and the Q8_0 of the act block.
+// w ^ 4.  Each wave's partial row sums go to LDS, in two stage sets of
+// kStage units; when a set is full, the workgroup adds the eight partials
+// of each of its outputs in wave order during the next unit's multiply (and
+// the rest at the end) and applies the epilogue: bias, and for gate/up the
+// clamped SwiGLU and the Q8_0 of the act block.
 //
-// Each step: wait for this wave's prefetched groups; barrier (every wave is
-// past the previous unit's multiply); write the groups to LDS; flush staged
-// units when the stage is full; barrier; multiply (tiles 0-1, then 2-3),
-// issuing the next unit's load groups before each tile pair; write the
-// partial sums.  Measured alternatives, all slower for gate/up at 64 tokens:
-// one wave role loading and another multiplying (208 us against 190 us: one
-// multiplying wave per SIMD leaves the LDS and MFMA latencies exposed), and
-// tile pairs streamed by LDS DMA into a two-deep ring (370 us: in-flight
-// bytes drop to zero at every pair).
+// Each step: wait for this wave's prefetched groups; advance the cursor to
+// the next unit; barrier (every wave is past the previous unit's multiply);
+// write the groups to LDS, issuing the next unit's first load group after
+// the first; barrier; multiply (tiles 0-1, then 2-3), issuing the second
+// and third groups before each tile pair and flushing a full stage set
+// after the second; write the partial sums.  Measured alternatives, all
+// slower for gate/up at 64 tokens: one wave role loading and another
+// multiplying (208 us against 190 us at the time: one multiplying wave per
+// SIMD leaves the LDS and MFMA latencies exposed), and tile pairs streamed
+// by LDS DMA into a two-deep ring (370 us: in-flight bytes drop to zero at
+// every pair).
 template <int MODE>
 __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(2))) void k_mx_mfma(MxMfmaArgs a, const int32_t *__restrict__ r_active,
                                                                       const int32_t *__restrict__ r_offsets,
