@@ -36,6 +36,8 @@ MFMA_PROFILE = os.path.join(ROOT, "profiles", "k_mx_gemm_prefill_b512_hot.md")
 # grouped-GEMM policy of the library's default (spt_abi.hip: kGemmMinGroup,
 # kGemmMinSelections; select: items must fill the device)
 GEMM_MIN_GROUP, GEMM_MIN_SELECTIONS = 9, 1024
+# host threads for the CPU baseline: the box's CPU share per GPU
+CPU_SHARE = 16
 
 
 def measured_traffic(batch, layers, seed):
@@ -81,7 +83,7 @@ def parse():
     ap.add_argument("--extra-batches", default="1,8", help="other batch sizes reported beside it")
     ap.add_argument("--layers", type=int, default=36)
     ap.add_argument("--seed", type=int, default=3)
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--cpu-seconds", type=float, default=8.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill workloads")
     ap.add_argument("--prefill-only", action="store_true",
@@ -447,14 +449,18 @@ def rmsnorm_rows(ctx, stream, reps=50, dim=2880):
 
 def cpu_baseline(args, shp, W):
     """Reference-algorithm layer on the host: fp32 activations in the
-    reference's AVX2/FMA order, rows split over all cores (the Go worker
-    pool's partition), weights pre-faulted in RAM."""
+    reference's AVX2/FMA order, rows split over threads like the Go worker
+    pool (forward/workers_quant.go:42-52), weights pre-faulted in RAM (1.4 GB
+    for layer 0's ~108 experts, far beyond the last-level cache).  Timed with
+    the box's CPU share of threads (16 per GPU, capped by the affinity mask)
+    and with one thread."""
     import numpy as np
 
     from oracle import oracle as O
 
     B = args.batch
-    threads = max(1, min(len(os.sched_getaffinity(0)), int(os.environ.get("OMP_NUM_THREADS", "16") or 16)))
+    host_cpus = len(os.sched_getaffinity(0))
+    threads = max(1, min(host_cpus, CPU_SHARE))
     x = W.x_tokens(args.seed, 0, B, shp.hidden)
     small = W.host_small_tensors(args.seed, 0, shp)
     logits = O.route(small["router"], small.get("router_bias"), x, B, shp.hidden, shp.experts)
@@ -462,22 +468,31 @@ def cpu_baseline(args, shp, W):
     t0 = time.time()
     lay = W.host_layer(args.seed, 0, shp, experts=np.unique(ids))
     log(f"cpu baseline: layer 0 weights for {len(np.unique(ids))} experts generated in {time.time() - t0:.1f}s")
-    O.forward_moe_batch(lay, x, B, q8=False, threads=threads)  # warm (page in)
-    reps, t0 = 0, time.perf_counter()
-    while True:
-        O.forward_moe_batch(lay, x, B, q8=False, threads=threads)
-        reps += 1
-        el = time.perf_counter() - t0
-        if el >= args.cpu_seconds or reps >= 200:
-            break
-    per_layer = el / reps
+
+    def timed(n_threads, seconds):
+        O.forward_moe_batch(lay, x, B, q8=False, threads=n_threads)  # warm (page in)
+        reps, t1 = 0, time.perf_counter()
+        while True:
+            O.forward_moe_batch(lay, x, B, q8=False, threads=n_threads)
+            reps += 1
+            el = time.perf_counter() - t1
+            if el >= seconds or reps >= 400:
+                return reps, el
+
+    reps, el = timed(threads, args.cpu_seconds)
+    reps1, el1 = timed(1, args.cpu_seconds)
+    per_layer, per_layer1 = el / reps, el1 / reps1
+    log(f"cpu baseline: {threads} threads {per_layer * 1e3:.1f} ms/layer, 1 thread {per_layer1 * 1e3:.1f} ms/layer")
     return {
         "value": round(B / per_layer, 2),
         "unit": "tokens/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"layer 0 of the same workload, B={B} tokens, {len(np.unique(ids))} distinct experts, "
-                  f"{reps} repetitions in {el:.1f}s ({per_layer * 1e3:.1f} ms/layer); MoE-layer tokens/s",
+        "sample": f"layer 0 of the same workload, B={B} tokens, {len(np.unique(ids))} distinct experts: "
+                  f"{reps} repetitions in {el:.1f}s on {threads} threads ({per_layer * 1e3:.1f} ms/layer), "
+                  f"{reps1} in {el1:.1f}s on 1 thread ({per_layer1 * 1e3:.1f} ms/layer); MoE-layer tokens/s",
+        "value_1core": round(B / per_layer1, 2),
+        "host_cpus": host_cpus,
         "cpu": _cpu_model(),
     }
 

@@ -176,7 +176,9 @@ int spt_tensor_upload(struct spt_ctx *ctx, spt_tensor *t, const void *src_host);
 int spt_quantize_q8_0(struct spt_ctx *ctx, const float *x_dev, int64_t n, void *out_dev);
 
 /* forward.MulQ40Into (forward/q40.go:33-38): y = W x for a Q4_0 [in, out]
- * matrix.  x_len/y_len are element counts (len(x), len(y)). */
+ * matrix.  x_len/y_len are element counts (len(x), len(y)).  in <= 131072
+ * (the device GEMV stages a token's Q8_0 input in LDS); the matrix is below
+ * 4 GiB.  These limits hold for every Q4_0 entry point. */
 int spt_mul_q40_into(struct spt_ctx *ctx, const spt_tensor *w, const float *x_dev,
                      int64_t x_len, float *y_dev, int64_t y_len);
 
@@ -196,7 +198,36 @@ int spt_mul_q40_batch_bias_into(struct spt_ctx *ctx, const spt_tensor *w, const 
                                 const float *x_dev, int64_t x_len, float *y_dev, int64_t y_len,
                                 int64_t batch, float *resid_dev);
 
-/* Host-slice form of MulQ40BatchInto for a cgo caller holding Go slices. */
+/* MulQ40BatchInto + biasBatch (+ residual addVector) of
+ * spt_mul_q40_batch_bias_into with the input given as its GGML Q8_0 blocks:
+ * xq_dev holds batch x in/32 blocks of 34 bytes (fp16 d, 32 int8 codes;
+ * 2-byte aligned), as spt_rmsnorm[_batch]_into and spt_quantize_q8_0 write
+ * them, so an input already quantized on the device (the normed hidden
+ * state, the attention context) is not quantized again.  y is the same as
+ * spt_mul_q40_batch_bias_into's on the fp32 input those blocks come from.
+ * No reference counterpart (the reference multiplies fp32 activations;
+ * forward/q40.go:46, layer.go:152-165). */
+int spt_mul_q40_batch_q8_into(struct spt_ctx *ctx, const spt_tensor *w, const spt_tensor *bias,
+                              const void *xq_dev, int64_t batch, float *y_dev, int64_t y_len,
+                              float *resid_dev);
+
+/* The Q, K, V projection step of forwardLayerBatch / ForwardLayer
+ * (forward/layer_batch.go:62-74, layer.go:117-136): three MulQ40BatchInto
+ * + biasBatch over the same normed input, w[i] with optional bias[i] into
+ * y_dev[i] (y_len[i] elements), in one pass: the input is quantized once
+ * (x_dev, fp32) or given as GGML Q8_0 blocks (xq_dev; exactly one of the
+ * two), and the three matrices' rows share one GEMV launch below the GEMM
+ * batch sizes.  x_len = batch * in.  Each y equals what
+ * spt_mul_q40_batch_bias_into gives for that projection.  bias may be NULL
+ * (no biases); outputs must not overlap each other or the input. */
+int spt_mul_q40_qkv_batch_into(struct spt_ctx *ctx, const spt_tensor *w, const spt_tensor *bias,
+                               const float *x_dev, const void *xq_dev, int64_t x_len, int64_t batch,
+                               float *const *y_dev, const int64_t *y_len);
+
+/* Host-slice form of MulQ40BatchInto for a cgo caller holding Go slices.
+ * The slices are staged through the context's pinned host buffer and its
+ * device arena, which grow on demand and are reused: once they have grown,
+ * a call allocates nothing. */
 int spt_mul_q40_batch_into_host(struct spt_ctx *ctx, const spt_tensor *w, const float *x_host,
                                 int64_t x_len, float *y_host, int64_t y_len, int64_t batch);
 
@@ -217,7 +248,8 @@ int spt_mul_q80_argmax(struct spt_ctx *ctx, const spt_tensor *w, const float *x_
                        int64_t *best_token, float *best_logit);
 
 /* Host-slice forms of MulQ80Into / MulQ80Argmax for a cgo caller holding Go
- * slices (forward/engine.go:223,228 pass the final hidden state). */
+ * slices (forward/engine.go:223,228 pass the final hidden state), staged
+ * like spt_mul_q40_batch_into_host (no allocation once grown). */
 int spt_mul_q80_into_host(struct spt_ctx *ctx, const spt_tensor *w, const float *x_host, int64_t x_len,
                           float *y_host, int64_t y_len);
 int spt_mul_q80_argmax_host(struct spt_ctx *ctx, const spt_tensor *w, const float *x_host,
@@ -273,7 +305,20 @@ int spt_forward_moe_batch_ex(struct spt_ctx *ctx, const spt_moe_config *cfg,
                              float *out_dev, int64_t out_len, int64_t batch,
                              const spt_moe_taps *taps);
 
-/* Host-slice form of forwardMoEBatch for a cgo caller holding Go slices. */
+/* forwardMoEBatch with the Q8_0 of x supplied: xq_dev holds the GGML Q8_0
+ * blocks of x (batch x hidden/32 blocks of 34 bytes, 2-byte aligned), as the
+ * fused RMSNorm (spt_rmsnorm[_batch]_into's q8_dev) writes them beside the
+ * normed x.  The router still reads the fp32 x (forward/moe_batch.go:137-139
+ * routes fp32 activations); the expert projections use the given codes and
+ * scales instead of quantizing x again.  With xq_dev = Q8_0(x) the results
+ * are those of spt_forward_moe_batch bit for bit.  No reference counterpart
+ * (the fused quantization of this path). */
+int spt_forward_moe_batch_q8(struct spt_ctx *ctx, const spt_moe_config *cfg, const spt_moe_layer *lw,
+                             const float *x_dev, const void *xq_dev, int64_t x_len, float *out_dev,
+                             int64_t out_len, int64_t batch);
+
+/* Host-slice form of forwardMoEBatch for a cgo caller holding Go slices,
+ * staged like spt_mul_q40_batch_into_host (no allocation once grown). */
 int spt_forward_moe_batch_host(struct spt_ctx *ctx, const spt_moe_config *cfg,
                                const spt_moe_layer *lw, const float *x_host, int64_t x_len,
                                float *out_host, int64_t out_len, int64_t batch);

@@ -24,6 +24,8 @@ struct spt_ctx {
     const volatile int32_t *cancel = nullptr;
     void *scratch = nullptr;
     size_t scratch_bytes = 0;
+    void *pinned = nullptr;  // host staging of the *_host entry points
+    size_t pinned_bytes = 0;
     bool timing = false;
     std::vector<std::pair<int, std::pair<hipEvent_t, hipEvent_t>>> pending;
     std::vector<hipEvent_t> free_events;
@@ -356,56 +358,82 @@ int copy_tap(spt_ctx *ctx, void *dst, const void *src, size_t bytes) {
 constexpr int kGemmMinGroup = 9;
 constexpr int kGemmMinSelections = 1024;
 
-int run_moe(spt_ctx *ctx, const spt_moe_layer *lw, const float *x, float *out, const MoEDims &m,
-            const spt_moe_taps *taps) {
+// Scratch layout of one forwardMoEBatch call (offsets into the arena).
+struct MoELayout {
+    bool use_gemm;
+    int gemm_min;
+    bool forced;
+    size_t o_xc, o_xs, o_xm, o_xb, o_logits, o_ids, o_w, o_cnt, o_off, o_list, o_act_list, o_na;
+    size_t o_gv, o_gvn, o_gvp, o_gm, o_gmn, o_gmt, o_act, o_ac, o_as, o_am, o_ab, o_res;
+    size_t total;
+};
+
+// An expert's group holds at most n selections: with fewer than the
+// threshold no expert can reach the GEMM, which is then not launched.  An
+// explicit threshold (spt_ctx_set_gemm_min_group) applies as given; the
+// default also needs kGemmMinSelections and a full device of items.  The
+// fp32 act buffer exists only for the act tap.
+MoELayout moe_layout(const spt_ctx *ctx, const MoEDims &m, bool act_tap, size_t base) {
+    const int64_t h = m.h, d = m.d, E = m.E, B = m.batch, n = m.batch * m.k;
+    const int64_t nbh = h / 32, nbd = d / 32;
+    MoELayout L{};
+    L.forced = ctx->gemm_min_group > 0;
+    L.gemm_min = L.forced ? ctx->gemm_min_group : kGemmMinGroup;
+    L.use_gemm = n >= L.gemm_min && (L.forced || n >= kGemmMinSelections);
+    Carve c;
+    c.off = base;
+    L.o_xc = c.take(B * h), L.o_xs = c.take(B * nbh * 4), L.o_xm = c.take(B * nbh * 64);
+    L.o_xb = c.take(L.use_gemm ? B * nbh * 64 : 0);
+    L.o_logits = c.take(B * E * 4);
+    L.o_ids = c.take(n * 4), L.o_w = c.take(n * 4), L.o_cnt = c.take(E * 4), L.o_off = c.take((E + 1) * 4);
+    L.o_list = c.take(n * 4), L.o_act_list = c.take(E * 4), L.o_na = c.take(4);
+    L.o_gv = c.take(E * 4), L.o_gvn = c.take(4), L.o_gvp = c.take((E + 1) * 4);
+    L.o_gm = c.take(E * 4), L.o_gmn = c.take(4), L.o_gmt = c.take((E + 1) * 4);
+    L.o_act = c.take(act_tap ? n * d * 4 : 0), L.o_ac = c.take(n * d), L.o_as = c.take(n * nbd * 4);
+    L.o_am = c.take(n * nbd * 64);
+    L.o_ab = c.take(L.use_gemm ? n * nbd * 64 : 0);
+    L.o_res = c.take(n * h * 4);
+    L.total = c.off;
+    return L;
+}
+
+// The launch sequence of forwardMoEBatch over a scratch arena S laid out by L
+// (S holds at least L.total bytes).
+int run_moe_at(spt_ctx *ctx, const spt_moe_layer *lw, const float *x, float *out, const MoEDims &m,
+               const spt_moe_taps *taps, char *S, const MoELayout &L, const uint8_t *xq34 = nullptr) {
     const int64_t h = m.h, d = m.d, E = m.E, k = m.k, B = m.batch, n = B * k;
     const int64_t nbh = h / 32, nbd = d / 32;
-    // An expert's group holds at most n selections: with fewer than the
-    // threshold no expert can reach the GEMM, which is then not launched.
-    // An explicit threshold (spt_ctx_set_gemm_min_group) applies as given;
-    // the default also needs kGemmMinSelections and a full device of items.
-    const bool forced = ctx->gemm_min_group > 0;
-    const int gemm_min = forced ? ctx->gemm_min_group : kGemmMinGroup;
-    const bool use_gemm = n >= gemm_min && (forced || n >= kGemmMinSelections);
-    Carve c;
-    size_t o_xc = c.take(B * h), o_xs = c.take(B * nbh * 4), o_xm = c.take(B * nbh * 64);
-    size_t o_xb = c.take(use_gemm ? B * nbh * 64 : 0);
-    size_t o_logits = c.take(B * E * 4);
-    size_t o_ids = c.take(n * 4), o_w = c.take(n * 4), o_cnt = c.take(E * 4), o_off = c.take((E + 1) * 4);
-    size_t o_list = c.take(n * 4), o_act_list = c.take(E * 4), o_na = c.take(4);
-    size_t o_gv = c.take(E * 4), o_gvn = c.take(4), o_gvp = c.take((E + 1) * 4);
-    size_t o_gm = c.take(E * 4), o_gmn = c.take(4), o_gmt = c.take((E + 1) * 4);
-    size_t o_act = c.take(n * d * 4), o_ac = c.take(n * d), o_as = c.take(n * nbd * 4), o_am = c.take(n * nbd * 64);
-    size_t o_ab = c.take(use_gemm ? n * nbd * 64 : 0);
-    size_t o_res = c.take(n * h * 4);
-    char *S;
+    const bool use_gemm = L.use_gemm, forced = L.forced;
+    const int gemm_min = L.gemm_min;
     int rc;
-    if ((rc = scratch(ctx, c.off, &S))) return rc;
-    int8_t *xc = (int8_t *)(S + o_xc), *ac = (int8_t *)(S + o_ac);
-    float *xs = (float *)(S + o_xs), *logits = (float *)(S + o_logits), *act = (float *)(S + o_act);
-    uint8_t *xm = (uint8_t *)(S + o_xm), *am = (uint8_t *)(S + o_am);
-    uint32_t *xb = use_gemm ? (uint32_t *)(S + o_xb) : nullptr, *ab = use_gemm ? (uint32_t *)(S + o_ab) : nullptr;
-    float *as = (float *)(S + o_as), *res = (float *)(S + o_res);
+    int8_t *xc = (int8_t *)(S + L.o_xc), *ac = (int8_t *)(S + L.o_ac);
+    float *xs = (float *)(S + L.o_xs), *logits = (float *)(S + L.o_logits);
+    float *act = taps && taps->act ? (float *)(S + L.o_act) : nullptr;
+    uint8_t *xm = (uint8_t *)(S + L.o_xm), *am = (uint8_t *)(S + L.o_am);
+    uint32_t *xb = use_gemm ? (uint32_t *)(S + L.o_xb) : nullptr, *ab = use_gemm ? (uint32_t *)(S + L.o_ab) : nullptr;
+    float *as = (float *)(S + L.o_as), *res = (float *)(S + L.o_res);
     spt::SelectOut so{};
-    so.ids = (int32_t *)(S + o_ids);
-    so.weights = (float *)(S + o_w);
-    so.counts = (int32_t *)(S + o_cnt);
-    so.offsets = (int32_t *)(S + o_off);
-    so.list = (int32_t *)(S + o_list);
-    so.active = (int32_t *)(S + o_act_list);
-    so.n_active = (int32_t *)(S + o_na);
+    so.ids = (int32_t *)(S + L.o_ids);
+    so.weights = (float *)(S + L.o_w);
+    so.counts = (int32_t *)(S + L.o_cnt);
+    so.offsets = (int32_t *)(S + L.o_off);
+    so.list = (int32_t *)(S + L.o_list);
+    so.active = (int32_t *)(S + L.o_act_list);
+    so.n_active = (int32_t *)(S + L.o_na);
     so.gemm_min = use_gemm ? gemm_min : INT_MAX;
     so.gemm_units = (int32_t)((d + 127) / 128);
     so.gemm_min_items = forced ? 0 : ctx->n_cu;
-    so.gv_active = (int32_t *)(S + o_gv);
-    so.gv_n = (int32_t *)(S + o_gvn);
-    so.gv_pass_off = (int32_t *)(S + o_gvp);
-    so.gm_active = (int32_t *)(S + o_gm);
-    so.gm_n = (int32_t *)(S + o_gmn);
-    so.gm_tile_off = (int32_t *)(S + o_gmt);
+    so.gv_active = (int32_t *)(S + L.o_gv);
+    so.gv_n = (int32_t *)(S + L.o_gvn);
+    so.gv_pass_off = (int32_t *)(S + L.o_gvp);
+    so.gm_active = (int32_t *)(S + L.o_gm);
+    so.gm_n = (int32_t *)(S + L.o_gmn);
+    so.gm_tile_off = (int32_t *)(S + L.o_gmt);
     hipStream_t s = ctx->stream;
 
-    const spt::QuantOut xq{xc, xs, xm, taps ? (uint8_t *)taps->xq : nullptr, xb};
+    // the Q8_0 of x: quantized by the router's launch, or unpacked there from
+    // the caller's GGML blocks (the fused RMSNorm's output)
+    const spt::QuantOut xq{xc, xs, xm, taps ? (uint8_t *)taps->xq : nullptr, xb, xq34};
     if ((rc = check_cancel(ctx))) return rc;
     if (taps && taps->logits_in) {
         SPT_HIP(timed(ctx, SPT_KERNEL_QUANTIZE, [&] {
@@ -445,7 +473,7 @@ int run_moe(spt_ctx *ctx, const spt_moe_layer *lw, const float *x, float *out, c
     ga.offsets = so.offsets;
     ga.list = so.list;
     ga.topk = (int)k;
-    ga.out = taps && taps->act ? act : nullptr;  // fp32 act only for the tap
+    ga.out = act;  // fp32 act only for the tap
     ga.tap[0] = taps ? taps->gate : nullptr;
     ga.tap[1] = taps ? taps->up : nullptr;
     ga.act_codes = ac;
@@ -554,6 +582,15 @@ int run_moe(spt_ctx *ctx, const spt_moe_layer *lw, const float *x, float *out, c
     return SPT_OK;
 }
 
+int run_moe(spt_ctx *ctx, const spt_moe_layer *lw, const float *x, float *out, const MoEDims &m,
+            const spt_moe_taps *taps) {
+    const MoELayout L = moe_layout(ctx, m, taps && taps->act, 0);
+    char *S;
+    int rc;
+    if ((rc = scratch(ctx, L.total, &S))) return rc;
+    return run_moe_at(ctx, lw, x, out, m, taps, S, L);
+}
+
 // Quantize `rows` activation rows of nb blocks into the scratch arena: Q8_0
 // codes, scales, per-block code sums (Q4_0) and the E4M3 digit table (MXFP4).
 int quantize_into_scratch(spt_ctx *ctx, const float *x, int64_t rows, int64_t nb, Carve &c, char **S,
@@ -581,6 +618,10 @@ int validate_q40_call(spt_ctx *ctx, const spt_tensor *w, const float *x, int64_t
     if ((rc = check_cancel(ctx))) return rc;
     int64_t row_bytes;
     if ((rc = q40_shape(w, in, out, &row_bytes))) return rc;
+    // no reference counterpart: the device GEMV stages a token's Q8_0 input in LDS
+    if (*in > spt::kQ40MaxInput)
+        return fail(SPT_ERR_INVALID, "\"%s\": Q4_0 input dimension %lld exceeds the supported %d", tname(w),
+                    (long long)*in, spt::kQ40MaxInput);
     if (batch < 1 || batch > INT64_MAX / *in || batch > INT64_MAX / *out)
         return fail(SPT_ERR_INVALID, "invalid or oversized batch: %lld", (long long)batch);
     if (x_len != batch * *in || y_len != batch * *out)
@@ -591,6 +632,235 @@ int validate_q40_call(spt_ctx *ctx, const spt_tensor *w, const float *x, int64_t
     if (ranges_overlap(x, (uint64_t)x_len * 4, y, (uint64_t)y_len * 4))
         return fail(SPT_ERR_INVALID, "input and output must not overlap");
     if (batch > INT_MAX || *out > INT_MAX) return fail(SPT_ERR_INVALID, "invalid or oversized batch: %lld", (long long)batch);
+    return SPT_OK;
+}
+
+// The projection bias: addBias (forward/layer.go:225-242) for one vector,
+// biasBatch / readFloatVector (layer_batch.go:124-128, layer.go:279-289)
+// for a batch.  *present = false for an absent bias.
+int projection_bias_check(const spt_tensor *b, int64_t out, int64_t batch, bool *present, int *btype) {
+    *present = false;
+    if (!b) return SPT_OK;
+    const bool empty = b->nbytes == 0;
+    if (empty && !named(*b)) return SPT_OK;
+    if (empty && batch == 1) return fail(SPT_ERR_INVALID, "\"%s\": invalid bias range", tname(b));
+    uint64_t width = 4;
+    if (b->type == SPT_TYPE_F16 || b->type == SPT_TYPE_BF16)
+        width = 2;
+    else if (b->type != SPT_TYPE_F32)
+        return fail(SPT_ERR_INVALID, "\"%s\": unsupported float tensor type %u", tname(b), b->type);
+    if (b->n_dims != 1 || b->shape[0] != (uint64_t)out || b->nbytes != width * (uint64_t)out)
+        return fail(SPT_ERR_INVALID, "\"%s\": invalid float vector shape or range", tname(b));
+    if (!b->data) return fail(SPT_ERR_INVALID, "\"%s\": tensor is not resident (nil data)", tname(b));
+    if ((uintptr_t)b->data & (width - 1))
+        return fail(SPT_ERR_INVALID, "\"%s\": bias data must be %llu-byte aligned", tname(b),
+                    (unsigned long long)width);
+    *present = true;
+    *btype = (int)b->type;
+    return SPT_OK;
+}
+
+int check_resid(const float *resid, int64_t y_len, const void *in, uint64_t in_bytes, const float *y) {
+    if (resid && (ranges_overlap(resid, (uint64_t)y_len * 4, in, in_bytes) ||
+                  ranges_overlap(resid, (uint64_t)y_len * 4, y, (uint64_t)y_len * 4)))
+        return fail(SPT_ERR_INVALID, "residual overlaps the input or output");
+    return SPT_OK;
+}
+
+// MulQ40BatchInto's checks (forward/q40.go:46-71) with the input given as
+// batch x in/32 GGML Q8_0 blocks (34 bytes each, 2-byte aligned).
+int validate_q40_q8_call(spt_ctx *ctx, const spt_tensor *w, const void *xq, int64_t batch, const float *y,
+                         int64_t y_len, int64_t *in, int64_t *out) {
+    int rc;
+    if ((rc = check_ctx(ctx))) return rc;
+    if (!w) return fail(SPT_ERR_INVALID, "nil GGUF reader");
+    if ((rc = check_cancel(ctx))) return rc;
+    int64_t row_bytes;
+    if ((rc = q40_shape(w, in, out, &row_bytes))) return rc;
+    if (*in > spt::kQ40MaxInput)
+        return fail(SPT_ERR_INVALID, "\"%s\": Q4_0 input dimension %lld exceeds the supported %d", tname(w),
+                    (long long)*in, spt::kQ40MaxInput);
+    if (batch < 1 || batch > INT_MAX || batch > INT64_MAX / (*in / 32 * 34) || batch > INT64_MAX / *out)
+        return fail(SPT_ERR_INVALID, "invalid or oversized batch: %lld", (long long)batch);
+    if (y_len != batch * *out)
+        return fail(SPT_ERR_INVALID, "\"%s\": expected %lld output elements, got %lld", tname(w),
+                    (long long)(batch * *out), (long long)y_len);
+    if (!xq || !y) return fail(SPT_ERR_INVALID, "nil input or output");
+    if ((uintptr_t)xq & 1) return fail(SPT_ERR_INVALID, "Q8_0 input must be 2-byte aligned");
+    if (ranges_overlap(xq, (uint64_t)(batch * (*in / 32)) * 34, y, (uint64_t)y_len * 4))
+        return fail(SPT_ERR_INVALID, "input and output must not overlap");
+    if (*out > INT_MAX) return fail(SPT_ERR_INVALID, "invalid or oversized batch: %lld", (long long)batch);
+    return SPT_OK;
+}
+
+size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
+
+// Grow-only pinned host buffer of the context: the host-slice entry points
+// stage their inputs and outputs there (a pageable copy, then DMA).
+int staging(spt_ctx *ctx, size_t bytes, char **out) {
+    if (bytes > ctx->pinned_bytes) {
+        if (ctx->pinned) {
+            hipError_t e = hipStreamSynchronize(ctx->stream);
+            if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+            (void)hipHostFree(ctx->pinned);
+            ctx->pinned = nullptr;
+            ctx->pinned_bytes = 0;
+        }
+        const size_t want = bytes + bytes / 4 + 4096;
+        if (hipHostMalloc(&ctx->pinned, want, hipHostMallocDefault) != hipSuccess) {
+            ctx->pinned = nullptr;
+            return fail(SPT_ERR_NOMEM, "cannot allocate %zu bytes of pinned host staging", want);
+        }
+        ctx->pinned_bytes = want;
+    }
+    *out = static_cast<char *>(ctx->pinned);
+    return SPT_OK;
+}
+
+// One Q4_0 projection of a call (validated).
+struct Q40Proj {
+    const spt_tensor *w;
+    int64_t out;
+    bool has_bias;
+    int btype;
+    const void *bias;
+    float *y;
+    float *resid;
+};
+
+// The int8-MFMA GEMM forms (launch_q40_gemv's choice): 64 tokens and more
+// on 1024 rows and more, or 256 tokens and more on narrower projections (K
+// split kQ40SplitK ways through partial sums in the arena).
+bool q40_gemm_form(int64_t out, int64_t batch) {
+    return (batch >= spt::kQ40GemmMinTokens && out >= spt::kQ40GemmMinRows) ||
+           (batch >= spt::kQ40SplitMinTokens && out < spt::kQ40GemmMinRows);
+}
+
+// Arena layout of a Q4_0 call over np projections sharing one input.  The
+// activation views (codes, widened scales, code sums) exist unless the input
+// is GGML Q8_0 blocks that every projection's GEMV reads directly.
+struct Q40Plan {
+    bool views;
+    int64_t nb, batch;
+    size_t o_c, o_s, o_q, o_part, total;
+};
+
+Q40Plan q40_plan(const Q40Proj *p, int np, int64_t nb, int64_t batch, bool q8_in, size_t base) {
+    Q40Plan L{};
+    bool gemm = false;
+    size_t part = 0;
+    for (int i = 0; i < np; i++) {
+        if (!q40_gemm_form(p[i].out, batch)) continue;
+        gemm = true;
+        if (p[i].out < spt::kQ40GemmMinRows)
+            part = std::max(part, (size_t)spt::kQ40SplitK * batch * p[i].out * 4);
+    }
+    L.views = !q8_in || gemm;
+    L.nb = nb;
+    L.batch = batch;
+    Carve c;
+    c.off = base;
+    L.o_c = c.take(L.views ? batch * nb * 32 : 0);
+    L.o_s = c.take(L.views ? batch * nb * 4 : 0);
+    L.o_q = c.take(L.views ? batch * nb * 4 : 0);
+    L.o_part = c.take(part);
+    L.total = c.off;
+    return L;
+}
+
+// Quantize (x) or unpack (xq34) the input into the plan's views when it has
+// them, then one GEMV launch over every projection not on a GEMM form and
+// one GEMM launch per projection that is.
+int run_q40_at(spt_ctx *ctx, const Q40Proj *p, int np, const Q40Plan &L, char *S, const float *x,
+               const uint8_t *xq34) {
+    const int64_t nb = L.nb, batch = L.batch;
+    int8_t *codes = L.views ? (int8_t *)(S + L.o_c) : nullptr;
+    float *scales = L.views ? (float *)(S + L.o_s) : nullptr;
+    int32_t *sumq = L.views ? (int32_t *)(S + L.o_q) : nullptr;
+    if (L.views) {
+        SPT_HIP(timed(ctx, SPT_KERNEL_QUANTIZE, [&] {
+            return x ? spt::launch_quantize(ctx->stream, x, batch * nb, codes, scales, sumq, nullptr, nullptr, nullptr)
+                     : spt::launch_q8_unpack(ctx->stream, xq34, batch * nb, codes, scales, sumq, nullptr);
+        }));
+    }
+    int rc;
+    spt::Q40Args g{};
+    int ng = 0;
+    for (int i = 0; i < np; i++) {
+        if ((rc = check_cancel(ctx))) return rc;
+        const spt_tensor *w = p[i].w;
+        if (q40_gemm_form(p[i].out, batch)) {
+            spt::Q40Args a{(const uint8_t *)w->data, w->nbytes, (int)p[i].out, (int)nb, codes, scales, sumq,
+                           (int)batch, p[i].y, p[i].bias, p[i].btype, p[i].resid,
+                           p[i].out < spt::kQ40GemmMinRows ? (float *)(S + L.o_part) : nullptr};
+            SPT_HIP(timed(ctx, SPT_KERNEL_Q40, [&] { return spt::launch_q40_gemv(ctx->stream, a); }));
+            continue;
+        }
+        if (ng == 0) {
+            g = spt::Q40Args{(const uint8_t *)w->data, w->nbytes, (int)p[i].out, (int)nb, codes, scales, sumq,
+                             (int)batch, p[i].y, p[i].bias, p[i].btype, p[i].resid, nullptr};
+        } else {
+            g.more[ng - 1] = spt::Q40Mat{(const uint8_t *)w->data, w->nbytes, (int)p[i].out, p[i].y, p[i].bias,
+                                         p[i].btype, p[i].resid};
+        }
+        ng++;
+    }
+    if (ng) {
+        g.nmore = ng - 1;
+        g.xq34 = L.views ? nullptr : xq34;
+        if ((rc = check_cancel(ctx))) return rc;
+        SPT_HIP(timed(ctx, SPT_KERNEL_Q40, [&] { return spt::launch_q40_gemv(ctx->stream, g); }));
+    }
+    return SPT_OK;
+}
+
+// MulQ80Argmax's checks (forward/q80.go:20-45).
+int validate_q80_argmax(spt_ctx *ctx, const spt_tensor *w, const float *x, int64_t x_len, int64_t *best_token,
+                        float *best_logit, int64_t *in, int64_t *out) {
+    int rc;
+    if ((rc = check_ctx(ctx))) return rc;
+    if (!w) return fail(SPT_ERR_INVALID, "nil reader");
+    if ((rc = check_cancel(ctx))) return rc;
+    if ((rc = q80_shape(w, in, out))) return rc;
+    if (x_len != *in)
+        return fail(SPT_ERR_INVALID, "\"%s\": expected %lld input elements, got %lld", tname(w), (long long)*in,
+                    (long long)x_len);
+    if (!x || !best_token || !best_logit) return fail(SPT_ERR_INVALID, "nil input or output");
+    return SPT_OK;
+}
+
+// Arena layout of the argmax: per-wave partial (logit, row) pairs and the
+// merged pair (8 bytes at o_out).
+struct Q80ArgmaxPlan {
+    int waves;
+    size_t o_v, o_i, o_out;
+};
+
+Q80ArgmaxPlan q80_argmax_plan(const spt_ctx *ctx, int64_t in, int64_t out, size_t base, size_t *total) {
+    Q80ArgmaxPlan L{};
+    L.waves = spt::q80_grid_waves((int)out, (int)(in / 32), ctx->n_cu);
+    Carve c;
+    c.off = base;
+    L.o_v = c.take((size_t)L.waves * 4);
+    L.o_i = c.take((size_t)L.waves * 4);
+    L.o_out = c.take(8);
+    *total = c.off;
+    return L;
+}
+
+int q80_argmax_at(spt_ctx *ctx, const spt_tensor *w, int64_t in, int64_t out, const float *x, char *S,
+                  const Q80ArgmaxPlan &L) {
+    spt::Q80Args a{};
+    a.w = (const uint8_t *)w->data;
+    a.nbytes = w->nbytes;
+    a.rows = (int)out;
+    a.nb = (int)(in / 32);
+    a.x = x;
+    a.part_v = (float *)(S + L.o_v);
+    a.part_i = (int32_t *)(S + L.o_i);
+    a.out_v = (float *)(S + L.o_out);
+    a.out_i = (int32_t *)(S + L.o_out + 4);
+    SPT_HIP(timed(ctx, SPT_KERNEL_Q80, [&] { return spt::launch_q80_rows(ctx->stream, a, ctx->n_cu); }));
     return SPT_OK;
 }
 
@@ -626,6 +896,7 @@ int spt_ctx_destroy(spt_ctx *ctx) {
         (void)hipSetDevice(ctx->device);
         (void)hipStreamSynchronize(ctx->stream);
         if (ctx->scratch) (void)hipFree(ctx->scratch);
+        if (ctx->pinned) (void)hipHostFree(ctx->pinned);
         for (auto &p : ctx->pending) {
             (void)hipEventDestroy(p.second.first);
             (void)hipEventDestroy(p.second.second);
@@ -760,104 +1031,123 @@ int spt_quantize_q8_0(spt_ctx *ctx, const float *x_dev, int64_t n, void *out_dev
 
 int spt_mul_q40_batch_into(spt_ctx *ctx, const spt_tensor *w, const float *x_dev, int64_t x_len,
                            float *y_dev, int64_t y_len, int64_t batch) {
-    int64_t in, out;
-    int rc;
-    if ((rc = validate_q40_call(ctx, w, x_dev, x_len, y_dev, y_len, batch, &in, &out))) return rc;
-    if ((rc = check_device(ctx))) return rc;
-    const int64_t nb = in / 32;
-    Carve c;
-    // partial sums of the split-K GEMM for narrow projections of large batches
-    const bool split = batch >= spt::kQ40SplitMinTokens && out < spt::kQ40GemmMinRows;
-    const size_t o_part = c.take(split ? (size_t)spt::kQ40SplitK * batch * out * 4 : 0);
-    char *S;
-    int8_t *codes;
-    float *scales;
-    int32_t *sumq;
-    if ((rc = quantize_into_scratch(ctx, x_dev, batch, nb, c, &S, &codes, &scales, &sumq, nullptr))) return rc;
-    if ((rc = check_cancel(ctx))) return rc;
-    spt::Q40Args a{(const uint8_t *)w->data, w->nbytes, (int)out, (int)nb, codes, scales, sumq, (int)batch, y_dev};
-    a.part = split ? (float *)(S + o_part) : nullptr;
-    SPT_HIP(timed(ctx, SPT_KERNEL_Q40, [&] { return spt::launch_q40_gemv(ctx->stream, a); }));
-    return SPT_OK;
-}
-
-// The projection bias: addBias (forward/layer.go:225-242) for one vector,
-// biasBatch / readFloatVector (layer_batch.go:124-128, layer.go:279-289)
-// for a batch.  *present = false for an absent bias.
-int projection_bias_check(const spt_tensor *b, int64_t out, int64_t batch, bool *present, int *btype) {
-    *present = false;
-    if (!b) return SPT_OK;
-    const bool empty = b->nbytes == 0;
-    if (empty && !named(*b)) return SPT_OK;
-    if (empty && batch == 1) return fail(SPT_ERR_INVALID, "\"%s\": invalid bias range", tname(b));
-    uint64_t width = 4;
-    if (b->type == SPT_TYPE_F16 || b->type == SPT_TYPE_BF16)
-        width = 2;
-    else if (b->type != SPT_TYPE_F32)
-        return fail(SPT_ERR_INVALID, "\"%s\": unsupported float tensor type %u", tname(b), b->type);
-    if (b->n_dims != 1 || b->shape[0] != (uint64_t)out || b->nbytes != width * (uint64_t)out)
-        return fail(SPT_ERR_INVALID, "\"%s\": invalid float vector shape or range", tname(b));
-    if (!b->data) return fail(SPT_ERR_INVALID, "\"%s\": tensor is not resident (nil data)", tname(b));
-    if ((uintptr_t)b->data & (width - 1))
-        return fail(SPT_ERR_INVALID, "\"%s\": bias data must be %llu-byte aligned", tname(b),
-                    (unsigned long long)width);
-    *present = true;
-    *btype = (int)b->type;
-    return SPT_OK;
+    return spt_mul_q40_batch_bias_into(ctx, w, nullptr, x_dev, x_len, y_dev, y_len, batch, nullptr);
 }
 
 int spt_mul_q40_into(spt_ctx *ctx, const spt_tensor *w, const float *x_dev, int64_t x_len, float *y_dev,
                      int64_t y_len) {
-    return spt_mul_q40_batch_into(ctx, w, x_dev, x_len, y_dev, y_len, 1);
+    return spt_mul_q40_batch_bias_into(ctx, w, nullptr, x_dev, x_len, y_dev, y_len, 1, nullptr);
 }
 
 int spt_mul_q40_batch_bias_into(spt_ctx *ctx, const spt_tensor *w, const spt_tensor *bias, const float *x_dev,
                                 int64_t x_len, float *y_dev, int64_t y_len, int64_t batch, float *resid_dev) {
-    int64_t in, out;
+    Q40Proj p;
+    int64_t in;
     int rc;
-    if ((rc = validate_q40_call(ctx, w, x_dev, x_len, y_dev, y_len, batch, &in, &out))) return rc;
-    bool has_bias;
-    int btype = 0;
-    if ((rc = projection_bias_check(bias, out, batch, &has_bias, &btype))) return rc;
-    if (resid_dev && (ranges_overlap(resid_dev, (uint64_t)y_len * 4, x_dev, (uint64_t)x_len * 4) ||
-                      ranges_overlap(resid_dev, (uint64_t)y_len * 4, y_dev, (uint64_t)y_len * 4)))
-        return fail(SPT_ERR_INVALID, "residual overlaps the input or output");
+    if ((rc = validate_q40_call(ctx, w, x_dev, x_len, y_dev, y_len, batch, &in, &p.out))) return rc;
+    if ((rc = projection_bias_check(bias, p.out, batch, &p.has_bias, &p.btype))) return rc;
+    if ((rc = check_resid(resid_dev, y_len, x_dev, (uint64_t)x_len * 4, y_dev))) return rc;
     if ((rc = check_device(ctx))) return rc;
-    const int64_t nb = in / 32;
-    Carve c;
-    const bool split = batch >= spt::kQ40SplitMinTokens && out < spt::kQ40GemmMinRows;
-    const size_t o_part = c.take(split ? (size_t)spt::kQ40SplitK * batch * out * 4 : 0);
+    p.w = w;
+    p.bias = p.has_bias ? bias->data : nullptr;
+    p.y = y_dev;
+    p.resid = resid_dev;
+    const Q40Plan plan = q40_plan(&p, 1, in / 32, batch, false, 0);
     char *S;
-    int8_t *codes;
-    float *scales;
-    int32_t *sumq;
-    if ((rc = quantize_into_scratch(ctx, x_dev, batch, nb, c, &S, &codes, &scales, &sumq, nullptr))) return rc;
-    if ((rc = check_cancel(ctx))) return rc;
-    spt::Q40Args a{(const uint8_t *)w->data, w->nbytes, (int)out, (int)nb, codes, scales, sumq, (int)batch, y_dev,
-                   has_bias ? bias->data : nullptr, btype, resid_dev, split ? (float *)(S + o_part) : nullptr};
-    SPT_HIP(timed(ctx, SPT_KERNEL_Q40, [&] { return spt::launch_q40_gemv(ctx->stream, a); }));
-    return SPT_OK;
+    if ((rc = scratch(ctx, plan.total, &S))) return rc;
+    return run_q40_at(ctx, &p, 1, plan, S, x_dev, nullptr);
+}
+
+int spt_mul_q40_batch_q8_into(spt_ctx *ctx, const spt_tensor *w, const spt_tensor *bias, const void *xq_dev,
+                              int64_t batch, float *y_dev, int64_t y_len, float *resid_dev) {
+    Q40Proj p;
+    int64_t in;
+    int rc;
+    if ((rc = validate_q40_q8_call(ctx, w, xq_dev, batch, y_dev, y_len, &in, &p.out))) return rc;
+    if ((rc = projection_bias_check(bias, p.out, batch, &p.has_bias, &p.btype))) return rc;
+    if ((rc = check_resid(resid_dev, y_len, xq_dev, (uint64_t)(batch * (in / 32)) * 34, y_dev))) return rc;
+    if ((rc = check_device(ctx))) return rc;
+    p.w = w;
+    p.bias = p.has_bias ? bias->data : nullptr;
+    p.y = y_dev;
+    p.resid = resid_dev;
+    const Q40Plan plan = q40_plan(&p, 1, in / 32, batch, true, 0);
+    char *S;
+    if ((rc = scratch(ctx, plan.total, &S))) return rc;
+    return run_q40_at(ctx, &p, 1, plan, S, nullptr, (const uint8_t *)xq_dev);
+}
+
+int spt_mul_q40_qkv_batch_into(spt_ctx *ctx, const spt_tensor *w, const spt_tensor *bias, const float *x_dev,
+                               const void *xq_dev, int64_t x_len, int64_t batch, float *const *y_dev,
+                               const int64_t *y_len) {
+    int rc;
+    if ((rc = check_ctx(ctx))) return rc;
+    if (!w || !y_dev || !y_len) return fail(SPT_ERR_INVALID, "nil GGUF reader");
+    if (!x_dev == !xq_dev) return fail(SPT_ERR_INVALID, "exactly one of the fp32 and the Q8_0 input must be given");
+    Q40Proj p[3];
+    int64_t in = 0;
+    for (int i = 0; i < 3; i++) {
+        int64_t in_i;
+        if (x_dev) {
+            rc = validate_q40_call(ctx, &w[i], x_dev, x_len, y_dev[i], y_len[i], batch, &in_i, &p[i].out);
+        } else {
+            rc = validate_q40_q8_call(ctx, &w[i], xq_dev, batch, y_dev[i], y_len[i], &in_i, &p[i].out);
+            if (!rc && x_len != batch * in_i)
+                rc = fail(SPT_ERR_INVALID, "\"%s\": expected %lld input elements, got %lld", tname(&w[i]),
+                          (long long)(batch * in_i), (long long)x_len);
+        }
+        if (rc) return rc;
+        if (i > 0 && in_i != in)
+            return fail(SPT_ERR_INVALID, "\"%s\": input dimension %lld differs from %lld", tname(&w[i]),
+                        (long long)in_i, (long long)in);
+        in = in_i;
+        if ((rc = projection_bias_check(bias ? &bias[i] : nullptr, p[i].out, batch, &p[i].has_bias, &p[i].btype)))
+            return rc;
+        for (int j = 0; j < i; j++)
+            if (ranges_overlap(y_dev[i], (uint64_t)y_len[i] * 4, y_dev[j], (uint64_t)y_len[j] * 4))
+                return fail(SPT_ERR_INVALID, "projection outputs overlap");
+        p[i].w = &w[i];
+        p[i].bias = p[i].has_bias ? bias[i].data : nullptr;
+        p[i].y = y_dev[i];
+        p[i].resid = nullptr;
+    }
+    if ((rc = check_device(ctx))) return rc;
+    const Q40Plan plan = q40_plan(p, 3, in / 32, batch, xq_dev != nullptr, 0);
+    char *S;
+    if ((rc = scratch(ctx, plan.total, &S))) return rc;
+    return run_q40_at(ctx, p, 3, plan, S, x_dev, (const uint8_t *)xq_dev);
 }
 
 int spt_mul_q40_batch_into_host(spt_ctx *ctx, const spt_tensor *w, const float *x_host, int64_t x_len,
                                 float *y_host, int64_t y_len, int64_t batch) {
-    int64_t in, out;
+    Q40Proj p;
+    int64_t in;
     int rc;
-    if ((rc = validate_q40_call(ctx, w, x_host, x_len, y_host, y_len, batch, &in, &out))) return rc;
+    if ((rc = validate_q40_call(ctx, w, x_host, x_len, y_host, y_len, batch, &in, &p.out))) return rc;
     if ((rc = check_device(ctx))) return rc;
-    void *xd = nullptr, *yd = nullptr;
-    if ((rc = spt_alloc(ctx, (uint64_t)x_len * 4, &xd))) return rc;
-    if ((rc = spt_alloc(ctx, (uint64_t)y_len * 4, &yd))) {
-        (void)hipFree(xd);
-        return rc;
+    // x and y travel through the context's pinned staging buffer and the
+    // head of its device arena; nothing is allocated once both have grown
+    const size_t xb = align256((size_t)x_len * 4), yb = align256((size_t)y_len * 4);
+    p.w = w;
+    p.has_bias = false;
+    p.btype = 0;
+    p.bias = nullptr;
+    p.resid = nullptr;
+    const Q40Plan plan = q40_plan(&p, 1, in / 32, batch, false, xb + yb);
+    char *S, *P;
+    if ((rc = scratch(ctx, plan.total, &S)) || (rc = staging(ctx, xb + yb, &P))) return rc;
+    p.y = (float *)(S + xb);
+    memcpy(P, x_host, (size_t)x_len * 4);
+    SPT_HIP(hipMemcpyAsync(S, P, (size_t)x_len * 4, hipMemcpyHostToDevice, ctx->stream));
+    rc = run_q40_at(ctx, &p, 1, plan, S, (const float *)S, nullptr);
+    if (!rc) {
+        SPT_HIP(hipMemcpyAsync(P + xb, S + xb, (size_t)y_len * 4, hipMemcpyDeviceToHost, ctx->stream));
     }
-    rc = spt_copy_h2d(ctx, xd, x_host, (uint64_t)x_len * 4);
-    if (!rc) rc = spt_mul_q40_batch_into(ctx, w, (const float *)xd, x_len, (float *)yd, y_len, batch);
-    if (!rc) rc = spt_copy_d2h(ctx, y_host, yd, (uint64_t)y_len * 4);
-    (void)hipStreamSynchronize(ctx->stream);
-    (void)hipFree(xd);
-    (void)hipFree(yd);
-    return rc;
+    const hipError_t e = hipStreamSynchronize(ctx->stream);
+    if (rc) return rc;
+    if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+    memcpy(y_host, P + xb, (size_t)y_len * 4);
+    return SPT_OK;
 }
 
 int spt_mul_q80_into(spt_ctx *ctx, const spt_tensor *w, const float *x_dev, int64_t x_len, float *y_dev,
@@ -889,37 +1179,19 @@ int spt_mul_q80_into(spt_ctx *ctx, const spt_tensor *w, const float *x_dev, int6
 int spt_mul_q80_argmax(spt_ctx *ctx, const spt_tensor *w, const float *x_dev, int64_t x_len, int64_t *best_token,
                        float *best_logit) {
     int rc;
-    if ((rc = check_ctx(ctx))) return rc;
-    if (!w) return fail(SPT_ERR_INVALID, "nil reader");
-    if ((rc = check_cancel(ctx))) return rc;
     int64_t in, out;
-    if ((rc = q80_shape(w, &in, &out))) return rc;
-    if (x_len != in)
-        return fail(SPT_ERR_INVALID, "\"%s\": expected %lld input elements, got %lld", tname(w), (long long)in,
-                    (long long)x_len);
-    if (!x_dev || !best_token || !best_logit) return fail(SPT_ERR_INVALID, "nil input or output");
+    if ((rc = validate_q80_argmax(ctx, w, x_dev, x_len, best_token, best_logit, &in, &out))) return rc;
     if ((rc = check_device(ctx))) return rc;
-    const int waves = spt::q80_grid_waves((int)out, (int)(in / 32), ctx->n_cu);
-    Carve c;
-    const size_t o_v = c.take((size_t)waves * 4), o_i = c.take((size_t)waves * 4), o_out = c.take(8);
+    size_t total;
+    const Q80ArgmaxPlan L = q80_argmax_plan(ctx, in, out, 0, &total);
     char *S;
-    if ((rc = scratch(ctx, c.off, &S))) return rc;
-    spt::Q80Args a{};
-    a.w = (const uint8_t *)w->data;
-    a.nbytes = w->nbytes;
-    a.rows = (int)out;
-    a.nb = (int)(in / 32);
-    a.x = x_dev;
-    a.part_v = (float *)(S + o_v);
-    a.part_i = (int32_t *)(S + o_i);
-    a.out_v = (float *)(S + o_out);
-    a.out_i = (int32_t *)(S + o_out + 4);
-    SPT_HIP(timed(ctx, SPT_KERNEL_Q80, [&] { return spt::launch_q80_rows(ctx->stream, a, ctx->n_cu); }));
+    if ((rc = scratch(ctx, total, &S))) return rc;
+    if ((rc = q80_argmax_at(ctx, w, in, out, x_dev, S, L))) return rc;
     struct {
         float v;
         int32_t i;
     } res;
-    SPT_HIP(hipMemcpyAsync(&res, S + o_out, sizeof res, hipMemcpyDeviceToHost, ctx->stream));
+    SPT_HIP(hipMemcpyAsync(&res, S + L.o_out, sizeof res, hipMemcpyDeviceToHost, ctx->stream));
     SPT_HIP(hipStreamSynchronize(ctx->stream));
     *best_token = res.i;
     *best_logit = res.v;
@@ -938,40 +1210,51 @@ int spt_mul_q80_into_host(spt_ctx *ctx, const spt_tensor *w, const float *x_host
                     (long long)in, (long long)out, (long long)x_len, (long long)y_len);
     if (!x_host || !y_host) return fail(SPT_ERR_INVALID, "nil input or output");
     if ((rc = check_device(ctx))) return rc;
-    void *xd = nullptr, *yd = nullptr;
-    if ((rc = spt_alloc(ctx, (uint64_t)x_len * 4, &xd))) return rc;
-    if ((rc = spt_alloc(ctx, (uint64_t)y_len * 4, &yd))) {
-        (void)hipFree(xd);
-        return rc;
+    // x and the logits travel through the context's pinned staging buffer and
+    // the head of its device arena
+    const size_t xb = align256((size_t)x_len * 4), yb = align256((size_t)y_len * 4);
+    char *S, *P;
+    if ((rc = scratch(ctx, xb + yb, &S)) || (rc = staging(ctx, xb + yb, &P))) return rc;
+    memcpy(P, x_host, (size_t)x_len * 4);
+    SPT_HIP(hipMemcpyAsync(S, P, (size_t)x_len * 4, hipMemcpyHostToDevice, ctx->stream));
+    rc = spt_mul_q80_into(ctx, w, (const float *)S, x_len, (float *)(S + xb), y_len);
+    if (!rc) {
+        SPT_HIP(hipMemcpyAsync(P + xb, S + xb, (size_t)y_len * 4, hipMemcpyDeviceToHost, ctx->stream));
     }
-    rc = spt_copy_h2d(ctx, xd, x_host, (uint64_t)x_len * 4);
-    if (!rc) rc = spt_mul_q80_into(ctx, w, (const float *)xd, x_len, (float *)yd, y_len);
-    if (!rc) rc = spt_copy_d2h(ctx, y_host, yd, (uint64_t)y_len * 4);
-    (void)hipStreamSynchronize(ctx->stream);
-    (void)hipFree(xd);
-    (void)hipFree(yd);
-    return rc;
+    const hipError_t e = hipStreamSynchronize(ctx->stream);
+    if (rc) return rc;
+    if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+    memcpy(y_host, P + xb, (size_t)y_len * 4);
+    return SPT_OK;
 }
 
 int spt_mul_q80_argmax_host(spt_ctx *ctx, const spt_tensor *w, const float *x_host, int64_t x_len,
                             int64_t *best_token, float *best_logit) {
     int rc;
-    if ((rc = check_ctx(ctx))) return rc;
-    if (!w) return fail(SPT_ERR_INVALID, "nil reader");
     int64_t in, out;
-    if ((rc = q80_shape(w, &in, &out))) return rc;
-    if (x_len != in)
-        return fail(SPT_ERR_INVALID, "\"%s\": expected %lld input elements, got %lld", tname(w), (long long)in,
-                    (long long)x_len);
-    if (!x_host || !best_token || !best_logit) return fail(SPT_ERR_INVALID, "nil input or output");
+    if ((rc = validate_q80_argmax(ctx, w, x_host, x_len, best_token, best_logit, &in, &out))) return rc;
     if ((rc = check_device(ctx))) return rc;
-    void *xd = nullptr;
-    if ((rc = spt_alloc(ctx, (uint64_t)x_len * 4, &xd))) return rc;
-    rc = spt_copy_h2d(ctx, xd, x_host, (uint64_t)x_len * 4);
-    if (!rc) rc = spt_mul_q80_argmax(ctx, w, (const float *)xd, x_len, best_token, best_logit);
-    (void)hipStreamSynchronize(ctx->stream);
-    (void)hipFree(xd);
-    return rc;
+    const size_t xb = align256((size_t)x_len * 4);
+    size_t total;
+    const Q80ArgmaxPlan L = q80_argmax_plan(ctx, in, out, xb, &total);
+    char *S, *P;
+    if ((rc = scratch(ctx, total, &S)) || (rc = staging(ctx, xb + 256, &P))) return rc;
+    memcpy(P, x_host, (size_t)x_len * 4);
+    SPT_HIP(hipMemcpyAsync(S, P, (size_t)x_len * 4, hipMemcpyHostToDevice, ctx->stream));
+    rc = q80_argmax_at(ctx, w, in, out, (const float *)S, S, L);
+    if (!rc) {
+        SPT_HIP(hipMemcpyAsync(P + xb, S + L.o_out, 8, hipMemcpyDeviceToHost, ctx->stream));
+    }
+    const hipError_t e = hipStreamSynchronize(ctx->stream);
+    if (rc) return rc;
+    if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+    float v;
+    int32_t i;
+    memcpy(&v, P + xb, 4);
+    memcpy(&i, P + xb + 4, 4);
+    *best_token = i;
+    *best_logit = v;
+    return SPT_OK;
 }
 
 int spt_rmsnorm_into(spt_ctx *ctx, const spt_tensor *weight, const float *x_dev, int64_t x_len, float *y_dev,
@@ -1111,7 +1394,14 @@ int spt_forward_moe_batch(spt_ctx *ctx, const spt_moe_config *cfg, const spt_moe
 int spt_forward_moe(spt_ctx *ctx, const spt_moe_config *cfg, const spt_moe_layer *lw, const float *x_dev,
                     int64_t x_len, float *out_dev, int64_t out_len) {
     if (!cfg) return fail(SPT_ERR_INVALID, "nil MoE configuration");
-    return spt_forward_moe_batch_ex(ctx, cfg, lw, x_dev, x_len, out_dev, out_len, 1, nullptr);
+    if (!lw) return spt_forward_moe_batch_ex(ctx, cfg, lw, x_dev, x_len, out_dev, out_len, 1, nullptr);
+    // Decode callers disable an optional expert bias with an empty name: such
+    // a descriptor is replaced by the absent tensor whatever its other fields
+    // hold (forward/moe.go:57-62).  The router bias is left as given.
+    spt_moe_layer w = *lw;
+    for (spt_tensor *b : {&w.ffn_gate_exps_bias, &w.ffn_up_exps_bias, &w.ffn_down_exps_bias})
+        if (!named(*b)) *b = spt_tensor{};
+    return spt_forward_moe_batch_ex(ctx, cfg, &w, x_dev, x_len, out_dev, out_len, 1, nullptr);
 }
 
 int spt_forward_moe_batch_host(spt_ctx *ctx, const spt_moe_config *cfg, const spt_moe_layer *lw,
@@ -1121,19 +1411,39 @@ int spt_forward_moe_batch_host(spt_ctx *ctx, const spt_moe_config *cfg, const sp
     int rc;
     if ((rc = validate_moe(ctx, cfg, lw, x_host, x_len, out_host, out_len, batch, &m))) return rc;
     if ((rc = check_cancel(ctx)) || (rc = check_device(ctx))) return rc;
-    void *xd = nullptr, *od = nullptr;
-    if ((rc = spt_alloc(ctx, (uint64_t)x_len * 4, &xd))) return rc;
-    if ((rc = spt_alloc(ctx, (uint64_t)out_len * 4, &od))) {
-        (void)hipFree(xd);
-        return rc;
+    // x and out travel through the context's pinned staging buffer and the
+    // head of its device arena; nothing is allocated once both have grown
+    const size_t xb = align256((size_t)x_len * 4), ob = align256((size_t)out_len * 4);
+    const MoELayout L = moe_layout(ctx, m, false, xb + ob);
+    char *S, *P;
+    if ((rc = scratch(ctx, L.total, &S)) || (rc = staging(ctx, xb + ob, &P))) return rc;
+    memcpy(P, x_host, (size_t)x_len * 4);
+    SPT_HIP(hipMemcpyAsync(S, P, (size_t)x_len * 4, hipMemcpyHostToDevice, ctx->stream));
+    rc = run_moe_at(ctx, lw, (const float *)S, (float *)(S + xb), m, nullptr, S, L);
+    if (!rc) {
+        SPT_HIP(hipMemcpyAsync(P + xb, S + xb, (size_t)out_len * 4, hipMemcpyDeviceToHost, ctx->stream));
     }
-    rc = spt_copy_h2d(ctx, xd, x_host, (uint64_t)x_len * 4);
-    if (!rc) rc = run_moe(ctx, lw, (const float *)xd, (float *)od, m, nullptr);
-    if (!rc) rc = spt_copy_d2h(ctx, out_host, od, (uint64_t)out_len * 4);
-    (void)hipStreamSynchronize(ctx->stream);
-    (void)hipFree(xd);
-    (void)hipFree(od);
-    return rc;
+    const hipError_t e = hipStreamSynchronize(ctx->stream);
+    if (rc) return rc;
+    if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+    memcpy(out_host, P + xb, (size_t)out_len * 4);
+    return SPT_OK;
+}
+
+int spt_forward_moe_batch_q8(spt_ctx *ctx, const spt_moe_config *cfg, const spt_moe_layer *lw, const float *x_dev,
+                             const void *xq_dev, int64_t x_len, float *out_dev, int64_t out_len, int64_t batch) {
+    MoEDims m;
+    int rc;
+    if ((rc = validate_moe(ctx, cfg, lw, x_dev, x_len, out_dev, out_len, batch, &m))) return rc;
+    if (!xq_dev) return fail(SPT_ERR_INVALID, "nil Q8_0 input");
+    if ((uintptr_t)xq_dev & 1) return fail(SPT_ERR_INVALID, "Q8_0 input must be 2-byte aligned");
+    if (ranges_overlap(xq_dev, (uint64_t)x_len / 32 * 34, out_dev, (uint64_t)out_len * 4))
+        return fail(SPT_ERR_INVALID, "MoE Q8_0 input and output overlap");
+    if ((rc = check_cancel(ctx)) || (rc = check_device(ctx))) return rc;
+    const MoELayout L = moe_layout(ctx, m, false, 0);
+    char *S;
+    if ((rc = scratch(ctx, L.total, &S))) return rc;
+    return run_moe_at(ctx, lw, x_dev, out_dev, m, nullptr, S, L, (const uint8_t *)xq_dev);
 }
 
 int spt_block_sums(spt_ctx *ctx, const spt_tensor *w, int32_t expert, const void *xq_dev, int64_t rows,

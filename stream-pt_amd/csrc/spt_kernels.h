@@ -43,13 +43,16 @@ struct SelectOut {
     int32_t *gm_tile_off;  // [E+1] prefix over GEMM experts of ceil(count / kGemmTokens)
 };
 
-// Optional Q8_0 outputs of a quantized activation (see write_q8_block).
+// Optional Q8_0 outputs of a quantized activation (see write_q8_block);
+// with src34 set, the router's launch unpacks these GGML Q8_0 blocks of the
+// input instead of quantizing it.
 struct QuantOut {
     int8_t *codes;
     float *scales;
     uint8_t *mxtab;
     uint8_t *blocks34;
     uint32_t *btab;
+    const uint8_t *src34;
 };
 
 enum GemvMode { kGateUp = 0, kDown = 1, kRows = 2 };
@@ -119,6 +122,18 @@ struct MxGemmArgs {
     uint32_t *act_btab;
 };
 
+// One more Q4_0 matrix of a GEMV launch over several projections of the
+// same input (the fields of Q40Args with the same names).
+struct Q40Mat {
+    const uint8_t *w;
+    uint64_t nbytes;
+    int rows;
+    float *y;
+    const void *bias;
+    int bias_type;
+    float *resid;
+};
+
 struct Q40Args {
     const uint8_t *w;
     uint64_t nbytes;
@@ -137,6 +152,13 @@ struct Q40Args {
     // optional scratch of kQ40SplitK * ntok * rows floats: narrow projections
     // of large batches then run on the GEMM with K split kQ40SplitK ways
     float *part;
+    // GEMV only: the activations as GGML Q8_0 blocks ([ntok][nb] x 34 bytes,
+    // 2-byte aligned) in place of codes / scales / sumq
+    const uint8_t *xq34;
+    // GEMV only: up to two more matrices with the same input; their row
+    // tiles follow this matrix's in the grid
+    int nmore;
+    Q40Mat more[2];
 };
 
 // The projection epilogue of forward/layer.go:120-165 and
@@ -190,7 +212,16 @@ constexpr int kQ40GemmMinRows = 1024;
 // order), when the caller provides the scratch.
 constexpr int kQ40SplitK = 4;
 constexpr int kQ40SplitMinTokens = 256;
+// The GEMV stages its tokens' activations (40 bytes per block) in at most
+// kQ40GemvLds bytes of LDS, at least one token per pass: inputs up to
+// kQ40MaxInput elements.
+constexpr int kQ40GemvLds = 160 * 1024;
+constexpr int kQ40MaxInput = kQ40GemvLds / 40 * 32;
 hipError_t launch_q40_gemv(hipStream_t s, const Q40Args &a);
+// GGML Q8_0 blocks -> codes, widened scales and per-block code sums (the
+// views launch_quantize writes), for nblocks blocks.
+hipError_t launch_q8_unpack(hipStream_t s, const uint8_t *blocks34, int64_t nblocks, int8_t *codes,
+                            float *scales, int32_t *sumq, uint8_t *mxtab);
 hipError_t launch_q40_gemm(hipStream_t s, const Q40Args &a);
 int q80_grid_waves(int rows, int nb, int n_cu);
 // RMSNorm of `batch` rows of n (spt_rmsnorm.hip): y = x * w * factor in the

@@ -49,6 +49,34 @@ hipError_t launch_quantize(hipStream_t s, const float *x, int64_t nblocks, int8_
     return hipGetLastError();
 }
 
+// GGML Q8_0 blocks -> the quantizer's views: one half-wave per block, lane i
+// holding code i (the layouts of write_q8_lane) and its code sum by shuffles.
+__global__ __launch_bounds__(kWG) void k_q8_unpack(const uint8_t *__restrict__ blocks34, int64_t nblocks,
+                                                   int8_t *__restrict__ codes, float *__restrict__ scales,
+                                                   int32_t *__restrict__ sumq, uint8_t *__restrict__ mxtab) {
+    const int tid = threadIdx.x, lane = tid & 63, i = tid & 31;
+    const int64_t b = (int64_t)blockIdx.x * (kWG / 32) + (tid >> 5);
+    if (b >= nblocks) return;  // whole half-waves
+    const uint8_t *blk = blocks34 + b * kQ80Block;
+    const int q = (int)(int8_t)blk[2 + i];
+    const uint16_t dh = (uint16_t)(blk[0] | (blk[1] << 8));
+    write_q8_lane(q, dh, lane & 31, (size_t)b, codes, scales, mxtab, nullptr, nullptr);
+    if (sumq) {
+        int s = q;
+#pragma unroll
+        for (int off = 16; off >= 1; off >>= 1) s += __shfl_xor(s, off, 32);
+        if (i == 0) sumq[b] = s;
+    }
+}
+
+hipError_t launch_q8_unpack(hipStream_t s, const uint8_t *blocks34, int64_t nblocks, int8_t *codes,
+                            float *scales, int32_t *sumq, uint8_t *mxtab) {
+    if (nblocks <= 0) return hipSuccess;
+    dim3 grid((unsigned)((nblocks + kWG / 32 - 1) / (kWG / 32)));
+    hipLaunchKernelGGL(k_q8_unpack, grid, dim3(kWG), 0, s, blocks34, nblocks, codes, scales, sumq, mxtab);
+    return hipGetLastError();
+}
+
 // ---------------------------------------------------------------------------
 // Router (forward/vector_amd64.go:11-56) and selection/packing
 // (forward/moe_batch.go:142-159,305-342).
@@ -309,9 +337,16 @@ __global__ __launch_bounds__(kWG) void k_route(const float *__restrict__ router,
         const int nbh = H / 32;
         for (int b0 = blockIdx.x * (kWG / 32); b0 < nbh; b0 += gridDim.x * (kWG / 32)) {
             const int b = b0 + (tid >> 5), i = tid & 31;
-            const float v = b < nbh ? xt[b * 32 + i] : 0.0f;
             uint16_t dh;
-            const int qv = q8_quantize_half(v, lane, &dh);  // every lane takes part
+            int qv;
+            if (q.src34) {
+                const uint8_t *blk = q.src34 + ((size_t)t * nbh + (b < nbh ? b : 0)) * kQ80Block;
+                qv = (int)(int8_t)blk[2 + i];
+                dh = (uint16_t)(blk[0] | (blk[1] << 8));
+            } else {
+                const float v = b < nbh ? xt[b * 32 + i] : 0.0f;
+                qv = q8_quantize_half(v, lane, &dh);  // every lane takes part
+            }
             if (b < nbh) write_q8_lane(qv, dh, i, (size_t)t * nbh + b, q.codes, q.scales, q.mxtab, q.blocks34, q.btab);
         }
     }
@@ -424,15 +459,38 @@ hipError_t launch_select(hipStream_t s, const float *logits, int batch, int expe
 // ---------------------------------------------------------------------------
 // Q4_0 x Q8_0 GEMV / small GEMM: y[t][row] for consecutive tokens.
 // ---------------------------------------------------------------------------
+// The matrix of row tile `tile` of a launch over several matrices with the
+// same input (Q40Args::more): its fields in place of the first's, and the
+// tile rebased to it.
+__device__ inline Q40Args q40_matrix(const Q40Args &args, int *tile) {
+    Q40Args a = args;
+    for (int i = 0; i < args.nmore; i++) {
+        const int tiles = (a.rows + kRowsPerWG - 1) / kRowsPerWG;
+        if (*tile < tiles) break;
+        *tile -= tiles;
+        const Q40Mat &m = args.more[i];
+        a.w = m.w;
+        a.nbytes = m.nbytes;
+        a.rows = m.rows;
+        a.y = m.y;
+        a.bias = m.bias;
+        a.bias_type = m.bias_type;
+        a.resid = m.resid;
+    }
+    return a;
+}
+
 template <int MAXP, int NT>
-__global__ __launch_bounds__(kWG) void k_q40_gemv(Q40Args a) {
+__global__ __launch_bounds__(kWG) void k_q40_gemv(Q40Args args) {
     extern __shared__ uint32_t smem_u[];
+    int tile = blockIdx.x;
+    const Q40Args a = q40_matrix(args, &tile);
     const int nb = a.nb, words = nb * 8;
     uint32_t *s_codes = smem_u;
     float *s_scales = reinterpret_cast<float *>(smem_u + NT * words);
     int32_t *s_sumq = reinterpret_cast<int32_t *>(s_scales + NT * nb);
     const int tid = threadIdx.x, j = tid & 15, g = tid >> 4;
-    const int r = blockIdx.x * kRowsPerWG + g;
+    const int r = tile * kRowsPerWG + g;
     const bool row_ok = r < a.rows;
     const uint32_t row_pos = (uint32_t)(row_ok ? r : 0) * (uint32_t)(nb * kQ40Block);
     const ByteView view = make_view(a.w, a.nbytes);
@@ -440,7 +498,26 @@ __global__ __launch_bounds__(kWG) void k_q40_gemv(Q40Args a) {
     // token passes of NT tokens: workgroup (x, y) takes passes y, y + G, ...
     for (int c0 = blockIdx.y * NT; c0 < a.ntok; c0 += gridDim.y * NT) {
         const int nt = min(NT, a.ntok - c0);
-        {
+        if (a.xq34) {
+            // GGML Q8_0 blocks (34 bytes, 2-byte aligned): one thread per
+            // block unpacks codes, the widened scale and the code sum
+            for (int i = tid; i < nt * nb; i += kWG) {
+                const uint16_t *blk = reinterpret_cast<const uint16_t *>(a.xq34 + ((size_t)c0 * nb + i) * kQ80Block);
+                uint16_t h[17];
+#pragma unroll
+                for (int k = 0; k < 17; k++) h[k] = blk[k];
+                int32_t sq = 0;
+                const int t = i / nb, b = i - t * nb;
+#pragma unroll
+                for (int k = 0; k < 8; k++) {
+                    const uint32_t w = (uint32_t)h[1 + 2 * k] | ((uint32_t)h[2 + 2 * k] << 16);
+                    s_codes[t * words + b * 8 + k] = w;
+                    sq += __builtin_amdgcn_sdot4((int)w, 0x01010101, 0, false);
+                }
+                s_scales[i] = f16_bits_to_f32(h[0]);
+                s_sumq[i] = sq;
+            }
+        } else {
             // the pass's codes (consecutive tokens: one contiguous run),
             // scales and code sums; every load issued before the stores
             typedef uint32_t u4 __attribute__((ext_vector_type(4)));
@@ -515,12 +592,18 @@ __global__ __launch_bounds__(kWG) void k_q40_gemv(Q40Args a) {
     }
 }
 
-template <int MAXP>
-static hipError_t launch_q40_maxp(hipStream_t s, const Q40Args &a) {
-    constexpr int NT = 8;
-    size_t lds = (size_t)NT * a.nb * (32 + 4 + 4);
-    // row tiles x token passes, up to about four workgroups per CU
-    const int tiles = (a.rows + kRowsPerWG - 1) / kRowsPerWG;
+template <int MAXP, int NT>
+static hipError_t launch_q40_nt(hipStream_t s, const Q40Args &a) {
+    const size_t lds = (size_t)NT * a.nb * (32 + 4 + 4);
+    if (lds > 64 * 1024) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_q40_gemv<MAXP, NT>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+    }
+    // row tiles (of every matrix) x token passes, up to about four
+    // workgroups per CU
+    int tiles = (a.rows + kRowsPerWG - 1) / kRowsPerWG;
+    for (int i = 0; i < a.nmore; i++) tiles += (a.more[i].rows + kRowsPerWG - 1) / kRowsPerWG;
     const int passes = (a.ntok + NT - 1) / NT;
     int gy = (1024 + tiles - 1) / tiles;
     gy = gy < 1 ? 1 : (gy > passes ? passes : gy);
@@ -528,8 +611,30 @@ static hipError_t launch_q40_maxp(hipStream_t s, const Q40Args &a) {
     return hipGetLastError();
 }
 
+// Eight tokens per pass while their activations fit the LDS, fewer for wider
+// inputs (kQ40MaxInput: one token of 40 bytes per block).
+template <int MAXP>
+static hipError_t launch_q40_maxp(hipStream_t s, const Q40Args &a) {
+    const size_t per_tok = (size_t)a.nb * (32 + 4 + 4);
+    if (8 * per_tok <= kQ40GemvLds) return launch_q40_nt<MAXP, 8>(s, a);
+    if (4 * per_tok <= kQ40GemvLds) return launch_q40_nt<MAXP, 4>(s, a);
+    if (2 * per_tok <= kQ40GemvLds) return launch_q40_nt<MAXP, 2>(s, a);
+    if (per_tok <= kQ40GemvLds) return launch_q40_nt<MAXP, 1>(s, a);
+    return hipErrorInvalidValue;  // beyond kQ40MaxInput, rejected by the ABI
+}
+
 hipError_t launch_q40_gemv(hipStream_t s, const Q40Args &a) {
     if (a.rows <= 0 || a.ntok <= 0) return hipSuccess;
+    if (a.nmore > 0 || a.xq34) {
+        // several matrices, or Q8_0 blocks in: the GEMV (the caller runs the
+        // GEMM forms one matrix at a time on unpacked activations)
+        const int per_lane = (a.nb + 15) / 16;
+        if (per_lane <= 1) return launch_q40_maxp<1>(s, a);
+        if (per_lane <= 2) return launch_q40_maxp<2>(s, a);
+        if (per_lane <= 4) return launch_q40_maxp<4>(s, a);
+        if (per_lane <= 6) return launch_q40_maxp<6>(s, a);
+        return launch_q40_maxp<8>(s, a);
+    }
     if (a.ntok >= kQ40GemmMinTokens && a.rows >= kQ40GemmMinRows) {
         Q40Args g = a;
         g.part = nullptr;

@@ -32,6 +32,7 @@ EXPORTED = (
     "spt_ctx_enable_timing", "spt_ctx_read_timing", "spt_ctx_set_gemm_min_group",
     "spt_mul_q80_into", "spt_mul_q80_argmax", "spt_mul_q80_into_host", "spt_mul_q80_argmax_host",
     "spt_rmsnorm_into", "spt_rmsnorm_batch_into", "spt_mul_q40_batch_bias_into",
+    "spt_mul_q40_batch_q8_into", "spt_mul_q40_qkv_batch_into", "spt_forward_moe_batch_q8",
 )
 KERNEL_KINDS = ("quantize", "route", "gate_up", "down", "combine", "q40", "select", "gate_up_gemm", "down_gemm",
                 "q80", "rmsnorm")
@@ -113,6 +114,8 @@ def lib():
         "spt_mul_q40_batch_into": ([vp, T, vp, i64, vp, i64, i64], C.c_int),
         "spt_mul_q40_batch_into_host": ([vp, T, vp, i64, vp, i64, i64], C.c_int),
         "spt_mul_q40_batch_bias_into": ([vp, T, T, vp, i64, vp, i64, i64, vp], C.c_int),
+        "spt_mul_q40_batch_q8_into": ([vp, T, T, vp, i64, vp, i64, vp], C.c_int),
+        "spt_mul_q40_qkv_batch_into": ([vp, T, T, vp, vp, i64, i64, C.POINTER(vp), C.POINTER(i64)], C.c_int),
         "spt_mul_q80_into": ([vp, T, vp, i64, vp, i64], C.c_int),
         "spt_mul_q80_argmax": ([vp, T, vp, i64, C.POINTER(C.c_int64), C.POINTER(C.c_float)], C.c_int),
         "spt_mul_q80_into_host": ([vp, T, vp, i64, vp, i64], C.c_int),
@@ -128,6 +131,8 @@ def lib():
                                       C.POINTER(MoETaps)], C.c_int),
         "spt_forward_moe_batch_host": ([vp, C.POINTER(MoEConfig), C.POINTER(MoELayer), vp, i64, vp, i64,
                                         i64], C.c_int),
+        "spt_forward_moe_batch_q8": ([vp, C.POINTER(MoEConfig), C.POINTER(MoELayer), vp, vp, i64, vp, i64, i64],
+                                     C.c_int),
         "spt_block_sums": ([vp, T, i32, vp, i64, vp], C.c_int),
         "spt_synth_mxfp4": ([vp, vp, u64, u64, u64, i32, i32], C.c_int),
         "spt_ctx_enable_timing": ([vp, C.c_int], C.c_int),
@@ -236,6 +241,24 @@ class Context:
         _check(lib().spt_mul_q40_batch_bias_into(self.handle, C.byref(w), C.byref(b), _ptr(x), _numel(x), _ptr(y),
                                                  _numel(y), batch, _ptr(resid)))
 
+    def mul_q40_batch_q8_into(self, w: Tensor, bias, xq, y, batch: int, resid=None):
+        """MulQ40BatchInto (+ bias, + residual) on an input given as GGML Q8_0
+        blocks (a uint8 buffer of batch * in/32 * 34 bytes)."""
+        b = bias if bias is not None else Tensor.absent()
+        _check(lib().spt_mul_q40_batch_q8_into(self.handle, C.byref(w), C.byref(b), _ptr(xq), batch, _ptr(y),
+                                               _numel(y), _ptr(resid)))
+
+    def mul_q40_qkv_batch_into(self, ws, biases, x, ys, batch: int, xq=None, x_len=None):
+        """The Q, K, V projections of one input: ws / biases / ys are three
+        Tensors / Tensors-or-None / output buffers; the input is the fp32 x
+        or, with x None, the GGML Q8_0 blocks xq (x_len elements)."""
+        wa = (Tensor * 3)(*ws)
+        ba = (Tensor * 3)(*[b if b is not None else Tensor.absent() for b in biases]) if biases else None
+        ya = (C.c_void_p * 3)(*[_ptr(y) for y in ys])
+        yl = (C.c_int64 * 3)(*[_numel(y) for y in ys])
+        n = _numel(x) if x is not None else int(x_len)
+        _check(lib().spt_mul_q40_qkv_batch_into(self.handle, wa, ba, _ptr(x), _ptr(xq), n, batch, ya, yl))
+
     def mul_q40_batch_into_host(self, w: Tensor, x, y, batch: int):
         _check(lib().spt_mul_q40_batch_into_host(self.handle, C.byref(w), _ptr(x), _numel(x), _ptr(y),
                                                  _numel(y), batch))
@@ -293,6 +316,10 @@ class Context:
     def forward_moe_batch_host(self, cfg: MoEConfig, lw: MoELayer, x, out, batch: int):
         _check(lib().spt_forward_moe_batch_host(self.handle, _ref(cfg), _ref(lw), _ptr(x), _numel(x),
                                                 _ptr(out), _numel(out), batch))
+
+    def forward_moe_batch_q8(self, cfg: MoEConfig, lw: MoELayer, x, xq, out, batch: int):
+        _check(lib().spt_forward_moe_batch_q8(self.handle, _ref(cfg), _ref(lw), _ptr(x), _ptr(xq), _numel(x),
+                                              _ptr(out), _numel(out), batch))
 
     def block_sums(self, w: Tensor, expert: int, xq, rows: int, sums):
         _check(lib().spt_block_sums(self.handle, C.byref(w), expert, _ptr(xq), rows, _ptr(sums)))

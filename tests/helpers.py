@@ -35,3 +35,13 @@ def assert_close(got, want, tol=REL_TOL, what=""):
 def bits(a):
     a = np.ascontiguousarray(a)
     return a.view(np.uint32) if a.dtype == np.float32 else a
+
+
+def tie_block():
+    """A Q8_0 block whose amax is 127 (d = 1, id = 1) holding exact .5
+    values of both signs, small and near the top of the code range."""
+    v = np.array([127.0, 0.5, -0.5, 1.5, -1.5, 2.5, -2.5, 3.5, -3.5, 4.5, -4.5, 10.5, -10.5, 63.5, -63.5,
+                  64.5, -64.5, 100.5, -100.5, 125.5, -125.5, 126.5, -126.5, 0.0, -0.0, 7.5, -7.5, 8.5,
+                  -8.5, 31.5, -31.5, -127.0], np.float32)
+    assert v.size == 32
+    return v

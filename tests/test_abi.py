@@ -162,6 +162,12 @@ def test_q40_validation(vctx):
         assert msg in spt.lib().spt_last_error(), spt.lib().spt_last_error()
     assert _call_q40(vctx, _q40(), 64, 3, 1, x=X, y=X + 8) == spt.ERR_INVALID
     assert b"overlap" in spt.lib().spt_last_error()
+    # the device GEMV's input limit (131072: one token's Q8_0 in LDS)
+    wide = spt.Tensor.make("q", spt.TYPE_Q4_0, [131072, 2], 0x40000000, 131072 // 32 * 18 * 2)
+    assert _call_q40(vctx, wide, 131072, 2, 1) == spt.ERR_DEVICE
+    wider = spt.Tensor.make("q", spt.TYPE_Q4_0, [131104, 2], 0x40000000, 131104 // 32 * 18 * 2)
+    assert _call_q40(vctx, wider, 131104, 2, 1) == spt.ERR_INVALID
+    assert b"exceeds the supported 131072" in spt.lib().spt_last_error()
 
 
 def _q80(inp=64, out=3, nbytes=None, shape=None, typ=None):
@@ -295,3 +301,34 @@ def test_gemm_min_group_setting(vctx):
     for v in (0, 1, 9, 1 << 30):
         assert L.spt_ctx_set_gemm_min_group(vctx.handle, v) == spt.OK
     assert L.spt_ctx_set_gemm_min_group(None, 1) == spt.ERR_INVALID
+
+
+def _call_moe_single(ctx, cfg, lw, x_ptr, x_len, out_ptr, out_len):
+    return spt.lib().spt_forward_moe(ctx.handle, C.byref(cfg), C.byref(lw), x_ptr, x_len, out_ptr, out_len)
+
+
+@pytest.mark.parametrize("which", ["ffn_gate_exps_bias", "ffn_up_exps_bias", "ffn_down_exps_bias"])
+def test_forward_moe_unnamed_expert_bias_disabled(vctx, which):
+    """forwardMoE (forward/moe.go:57-62) replaces an expert bias with an empty
+    name by the absent tensor before validating, so an unnamed descriptor
+    that still carries a byte range runs there; forwardMoEBatch rejects it
+    (moe_batch.go:196-200)."""
+    cfg, lw = _moe_descriptors()
+    t = getattr(lw, which)
+    t.name = None  # unnamed, nbytes and data left as they were
+    rc = _call_moe_single(vctx, cfg, lw, X, 32, OUT, 32)
+    assert rc == spt.ERR_DEVICE and b"validation-only" in spt.lib().spt_last_error()
+    rc = _call_moe(vctx, cfg, lw, X, 32, OUT, 32, 1)
+    assert rc == spt.ERR_INVALID and b"unnamed MoE bias has nonempty range" in spt.lib().spt_last_error()
+    t.name = b""  # an empty string is unnamed too
+    assert _call_moe_single(vctx, cfg, lw, X, 32, OUT, 32) == spt.ERR_DEVICE
+    assert getattr(lw, which).nbytes != 0  # the caller's descriptor is not modified
+
+
+def test_forward_moe_unnamed_router_bias_still_checked(vctx):
+    """The router bias is not cleared by forwardMoE: an unnamed one with a
+    byte range fails through both entry points."""
+    cfg, lw = _moe_descriptors()
+    lw.ffn_gate_inp_bias.name = None
+    assert _call_moe_single(vctx, cfg, lw, X, 32, OUT, 32) == spt.ERR_INVALID
+    assert b"unnamed MoE bias has nonempty range" in spt.lib().spt_last_error()

@@ -4,7 +4,7 @@ within helpers.REL_TOL."""
 import numpy as np
 import pytest
 
-from helpers import assert_close
+from helpers import assert_close, tie_block
 
 pytestmark = pytest.mark.gpu
 
@@ -50,9 +50,10 @@ def test_quantize_q8_0_bit_exact(gpu_ctx, O, case):
         x[2, 7] = np.inf                   # Inf block
         x[3] = np.float32(1e-30)           # subnormal fp16 scale
         x[4] = np.float32(6e4) * np.sign(x[4])   # scale overflows fp16
-        x[5] = np.arange(32, dtype=np.float32) - 15.5   # exact .5 ties after scaling
+        x[5] = tie_block()                 # amax 127: d = id = 1, exact .5 ties
         x[6] = -0.0
-        x[7, :] = np.float32(127.0) * np.arange(32) / 31  # integer codes
+        x[7, :] = np.arange(32, dtype=np.float32) * 4 - 62  # amax 62: codes 127*x/62, no ties
+        x[8] = tie_block() * np.float32(0.5)  # amax 63.5: id = 2, the same ties
         x = x.reshape(-1)
     xd = _dev(x.astype(np.float32))
     out = torch.zeros(n // 32 * 34, dtype=torch.uint8, device="cuda")
@@ -61,6 +62,12 @@ def test_quantize_q8_0_bit_exact(gpu_ctx, O, case):
     want = O.quantize_q8_0(x)
     got = out.cpu().numpy()
     assert np.array_equal(got, want), np.nonzero(got != want)[0][:10]
+    if case == "edge":
+        # the tie rows against half-away-from-zero worked out directly
+        for row in (5, 8):
+            t = tie_block()
+            codes = got.reshape(-1, 34)[row, 2:].view(np.int8)
+            assert np.array_equal(codes, (np.sign(t) * np.floor(np.abs(t) + 0.5)).astype(np.int8)), row
 
 
 def _q8_of(O, x):
@@ -184,6 +191,9 @@ def test_mxfp4_expert_gemv_odd_half_bias(gpu_ctx, O, bias_type):
     # narrow projections of 256 tokens and up: the GEMM with K split four
     # ways (fewer ways when the input has fewer blocks)
     (96, 70, 300), (32, 17, 256), (4096, 512, 257),
+    # wide inputs: the GEMV's activation staging above 64 KB of LDS (eight
+    # tokens per pass at 8192 inputs, two at 40960)
+    (8192, 300, 1), (8192, 300, 9), (40960, 40, 3),
 ])
 def test_q40_gemv(gpu_ctx, O, input_dim, output_dim, batch):
     import torch

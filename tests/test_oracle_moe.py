@@ -18,6 +18,7 @@ import numpy as np
 import pytest
 
 from fixtures import ROUTER_MODES, moe_batch_fixture, moe_batch_x
+from helpers import tie_block
 
 LEVELS64 = np.array([0, .5, 1, 1.5, 2, 3, 4, 6, 0, -.5, -1, -1.5, -2, -3, -4, -6], np.float64)
 
@@ -169,9 +170,15 @@ def test_quantize_q8_0_properties(O):
     # reconstruction error is half a step plus 127 * |fp16(d) - d|
     err = np.abs(codes * d[:, None] - x.reshape(-1, 32))
     assert np.all(err <= d[:, None] * (0.5 * (1 + 1e-3) + 127 * 2.0 ** -11) + 1e-7)
-    ties = np.arange(32, dtype=np.float32) - 15.5  # exact .5 after scaling rounds away from zero
-    qt = O.quantize_q8_0(ties * np.float32(127 / 15.5)).reshape(34)
-    assert qt[2:].view(np.int8)[0] == -127 and qt[2:].view(np.int8)[31] == 127
+    # amax 127 gives d = 1 and id = 1 exactly, so every x * id below is an
+    # exact .5 tie, where half-away-from-zero (GGML roundf) and half-even
+    # (rint) disagree
+    ties = tie_block()
+    qt = O.quantize_q8_0(ties).reshape(34)
+    assert qt[0] == 0x00 and qt[1] == 0x3C  # fp16(1.0)
+    want = (np.sign(ties) * np.floor(np.abs(ties) + 0.5)).astype(np.int8)
+    assert np.array_equal(qt[2:].view(np.int8), want)
+    assert not np.array_equal(want, np.rint(ties).astype(np.int8))  # the rule is pinned
     z = O.quantize_q8_0(np.zeros(32, np.float32))
     assert np.all(z == 0)
     nan = np.zeros(32, np.float32)
