@@ -37,15 +37,15 @@ struct spt_ctx {
 
 namespace {
 
-thread_local std::string g_error;
+// The calling thread's last error message (a fixed buffer: reporting an
+// error allocates nothing).
+thread_local char g_error[512];
 
 int fail(int code, const char *fmt, ...) {
-    char buf[512];
     va_list ap;
     va_start(ap, fmt);
-    vsnprintf(buf, sizeof buf, fmt, ap);
+    vsnprintf(g_error, sizeof g_error, fmt, ap);
     va_end(ap);
-    g_error = buf;
     return code;
 }
 
@@ -122,8 +122,8 @@ hipError_t timed(spt_ctx *ctx, int kind, F &&launch) {
     return hipSuccess;
 }
 
-// Grow-only device scratch; returns a pointer to at least `bytes` bytes.
-int scratch(spt_ctx *ctx, size_t bytes, char **out) {
+// Grow-only device scratch arena; returns a pointer to at least `bytes` bytes.
+int arena(spt_ctx *ctx, size_t bytes, char **out) {
     if (bytes > ctx->scratch_bytes) {
         if (ctx->scratch) {
             hipError_t e = hipStreamSynchronize(ctx->stream);
@@ -587,7 +587,7 @@ int run_moe(spt_ctx *ctx, const spt_moe_layer *lw, const float *x, float *out, c
     const MoELayout L = moe_layout(ctx, m, taps && taps->act, 0);
     char *S;
     int rc;
-    if ((rc = scratch(ctx, L.total, &S))) return rc;
+    if ((rc = arena(ctx, L.total, &S))) return rc;
     return run_moe_at(ctx, lw, x, out, m, taps, S, L);
 }
 
@@ -598,7 +598,7 @@ int quantize_into_scratch(spt_ctx *ctx, const float *x, int64_t rows, int64_t nb
     size_t o_c = c.take(rows * nb * 32), o_s = c.take(rows * nb * 4), o_q = c.take(rows * nb * 4);
     size_t o_m = c.take(mxtab ? rows * nb * 64 : 0);
     int rc;
-    if ((rc = scratch(ctx, c.off, S))) return rc;
+    if ((rc = arena(ctx, c.off, S))) return rc;
     *codes = (int8_t *)(*S + o_c);
     *scales = (float *)(*S + o_s);
     *sumq = (int32_t *)(*S + o_q);
@@ -868,7 +868,7 @@ int q80_argmax_at(spt_ctx *ctx, const spt_tensor *w, int64_t in, int64_t out, co
 
 extern "C" {
 
-const char *spt_last_error(void) { return g_error.c_str(); }
+const char *spt_last_error(void) { return g_error; }
 
 int spt_ctx_create(int device, void *hip_stream, spt_ctx **out) {
     if (!out) return fail(SPT_ERR_INVALID, "nil output pointer");
@@ -1054,7 +1054,7 @@ int spt_mul_q40_batch_bias_into(spt_ctx *ctx, const spt_tensor *w, const spt_ten
     p.resid = resid_dev;
     const Q40Plan plan = q40_plan(&p, 1, in / 32, batch, false, 0);
     char *S;
-    if ((rc = scratch(ctx, plan.total, &S))) return rc;
+    if ((rc = arena(ctx, plan.total, &S))) return rc;
     return run_q40_at(ctx, &p, 1, plan, S, x_dev, nullptr);
 }
 
@@ -1073,7 +1073,7 @@ int spt_mul_q40_batch_q8_into(spt_ctx *ctx, const spt_tensor *w, const spt_tenso
     p.resid = resid_dev;
     const Q40Plan plan = q40_plan(&p, 1, in / 32, batch, true, 0);
     char *S;
-    if ((rc = scratch(ctx, plan.total, &S))) return rc;
+    if ((rc = arena(ctx, plan.total, &S))) return rc;
     return run_q40_at(ctx, &p, 1, plan, S, nullptr, (const uint8_t *)xq_dev);
 }
 
@@ -1114,7 +1114,7 @@ int spt_mul_q40_qkv_batch_into(spt_ctx *ctx, const spt_tensor *w, const spt_tens
     if ((rc = check_device(ctx))) return rc;
     const Q40Plan plan = q40_plan(p, 3, in / 32, batch, xq_dev != nullptr, 0);
     char *S;
-    if ((rc = scratch(ctx, plan.total, &S))) return rc;
+    if ((rc = arena(ctx, plan.total, &S))) return rc;
     return run_q40_at(ctx, p, 3, plan, S, x_dev, (const uint8_t *)xq_dev);
 }
 
@@ -1135,7 +1135,7 @@ int spt_mul_q40_batch_into_host(spt_ctx *ctx, const spt_tensor *w, const float *
     p.resid = nullptr;
     const Q40Plan plan = q40_plan(&p, 1, in / 32, batch, false, xb + yb);
     char *S, *P;
-    if ((rc = scratch(ctx, plan.total, &S)) || (rc = staging(ctx, xb + yb, &P))) return rc;
+    if ((rc = arena(ctx, plan.total, &S)) || (rc = staging(ctx, xb + yb, &P))) return rc;
     p.y = (float *)(S + xb);
     memcpy(P, x_host, (size_t)x_len * 4);
     SPT_HIP(hipMemcpyAsync(S, P, (size_t)x_len * 4, hipMemcpyHostToDevice, ctx->stream));
@@ -1185,7 +1185,7 @@ int spt_mul_q80_argmax(spt_ctx *ctx, const spt_tensor *w, const float *x_dev, in
     size_t total;
     const Q80ArgmaxPlan L = q80_argmax_plan(ctx, in, out, 0, &total);
     char *S;
-    if ((rc = scratch(ctx, total, &S))) return rc;
+    if ((rc = arena(ctx, total, &S))) return rc;
     if ((rc = q80_argmax_at(ctx, w, in, out, x_dev, S, L))) return rc;
     struct {
         float v;
@@ -1214,7 +1214,7 @@ int spt_mul_q80_into_host(spt_ctx *ctx, const spt_tensor *w, const float *x_host
     // the head of its device arena
     const size_t xb = align256((size_t)x_len * 4), yb = align256((size_t)y_len * 4);
     char *S, *P;
-    if ((rc = scratch(ctx, xb + yb, &S)) || (rc = staging(ctx, xb + yb, &P))) return rc;
+    if ((rc = arena(ctx, xb + yb, &S)) || (rc = staging(ctx, xb + yb, &P))) return rc;
     memcpy(P, x_host, (size_t)x_len * 4);
     SPT_HIP(hipMemcpyAsync(S, P, (size_t)x_len * 4, hipMemcpyHostToDevice, ctx->stream));
     rc = spt_mul_q80_into(ctx, w, (const float *)S, x_len, (float *)(S + xb), y_len);
@@ -1238,7 +1238,7 @@ int spt_mul_q80_argmax_host(spt_ctx *ctx, const spt_tensor *w, const float *x_ho
     size_t total;
     const Q80ArgmaxPlan L = q80_argmax_plan(ctx, in, out, xb, &total);
     char *S, *P;
-    if ((rc = scratch(ctx, total, &S)) || (rc = staging(ctx, xb + 256, &P))) return rc;
+    if ((rc = arena(ctx, total, &S)) || (rc = staging(ctx, xb + 256, &P))) return rc;
     memcpy(P, x_host, (size_t)x_len * 4);
     SPT_HIP(hipMemcpyAsync(S, P, (size_t)x_len * 4, hipMemcpyHostToDevice, ctx->stream));
     rc = q80_argmax_at(ctx, w, in, out, (const float *)S, S, L);
@@ -1416,7 +1416,7 @@ int spt_forward_moe_batch_host(spt_ctx *ctx, const spt_moe_config *cfg, const sp
     const size_t xb = align256((size_t)x_len * 4), ob = align256((size_t)out_len * 4);
     const MoELayout L = moe_layout(ctx, m, false, xb + ob);
     char *S, *P;
-    if ((rc = scratch(ctx, L.total, &S)) || (rc = staging(ctx, xb + ob, &P))) return rc;
+    if ((rc = arena(ctx, L.total, &S)) || (rc = staging(ctx, xb + ob, &P))) return rc;
     memcpy(P, x_host, (size_t)x_len * 4);
     SPT_HIP(hipMemcpyAsync(S, P, (size_t)x_len * 4, hipMemcpyHostToDevice, ctx->stream));
     rc = run_moe_at(ctx, lw, (const float *)S, (float *)(S + xb), m, nullptr, S, L);
@@ -1442,7 +1442,7 @@ int spt_forward_moe_batch_q8(spt_ctx *ctx, const spt_moe_config *cfg, const spt_
     if ((rc = check_cancel(ctx)) || (rc = check_device(ctx))) return rc;
     const MoELayout L = moe_layout(ctx, m, false, 0);
     char *S;
-    if ((rc = scratch(ctx, L.total, &S))) return rc;
+    if ((rc = arena(ctx, L.total, &S))) return rc;
     return run_moe_at(ctx, lw, x_dev, out_dev, m, nullptr, S, L, (const uint8_t *)xq_dev);
 }
 
