@@ -317,6 +317,21 @@ int spt_forward_moe_batch_q8(struct spt_ctx *ctx, const spt_moe_config *cfg, con
                              const float *x_dev, const void *xq_dev, int64_t x_len, float *out_dev,
                              int64_t out_len, int64_t batch);
 
+/* forwardMoEBatch (spt_forward_moe_batch, same results bit for bit) for
+ * callers that cannot allocate: code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc.  No reference counterpart.  It
+ * calls no hipMalloc / hipFree and records no timing events: its scratch is
+ * a fixed 32 MiB device array, one per GPU, held until the process ends
+ * (about 91 KB per token at GPT-OSS-120B shape below 256 tokens, 120 KB from
+ * there: batches up to about 270 tokens); larger batches fail with
+ * SPT_ERR_INVALID.  Every call on a GPU uses that GPU's one array, so calls
+ * that overlap on one GPU (several contexts, streams or threads) race; a
+ * call may start after the previous one on the same stream without any
+ * clearing, since the path needs no zeroed scratch. */
+int spt_forward_moe_batch_noalloc(struct spt_ctx *ctx, const spt_moe_config *cfg,
+                                  const spt_moe_layer *lw, const float *x_dev, int64_t x_len,
+                                  float *out_dev, int64_t out_len, int64_t batch);
+
 /* Host-slice form of forwardMoEBatch for a cgo caller holding Go slices,
  * staged like spt_mul_q40_batch_into_host (no allocation once grown). */
 int spt_forward_moe_batch_host(struct spt_ctx *ctx, const spt_moe_config *cfg,

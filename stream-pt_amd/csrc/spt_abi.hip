@@ -10,6 +10,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <utility>
 #include <vector>
@@ -26,6 +27,8 @@ struct spt_ctx {
     size_t scratch_bytes = 0;
     void *pinned = nullptr;  // host staging of the *_host entry points
     size_t pinned_bytes = 0;
+    void *noalloc = nullptr;          // this device's copy of `scratch` (below)
+    hipError_t noalloc_err = hipSuccess;
     bool timing = false;
     std::vector<std::pair<int, std::pair<hipEvent_t, hipEvent_t>>> pending;
     std::vector<hipEvent_t> free_events;
@@ -35,7 +38,41 @@ struct spt_ctx {
     int n_cu = 0;                // compute units of the device
 };
 
+// Scratch of spt_forward_moe_batch_noalloc: a fixed device array, one copy
+// per GPU the library runs on, held until the process ends.  Host code
+// never passes this name to a kernel (on the host it is only a stand-in for
+// the symbol): the context looks up the device address of the current
+// device's copy once per device (noalloc_scratch_of) and uses that address.
+constexpr size_t kNoAllocScratchBytes = size_t(32) << 20;
+static __device__ __align__(256) char scratch[kNoAllocScratchBytes];
+
 namespace {
+
+// Device address of `scratch` on each device, looked up once per device
+// with that device current.
+constexpr int kMaxDevices = 64;
+struct NoAllocSlot {
+    std::once_flag once;
+    void *ptr = nullptr;
+    hipError_t err = hipSuccess;
+};
+NoAllocSlot g_noalloc[kMaxDevices];
+
+void noalloc_scratch_of(int device, void **ptr, hipError_t *err) {
+    if (device < 0 || device >= kMaxDevices) {
+        *ptr = nullptr;
+        *err = hipErrorInvalidDevice;
+        return;
+    }
+    NoAllocSlot &slot = g_noalloc[device];
+    std::call_once(slot.once, [&] {
+        void *p = nullptr;
+        slot.err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        slot.ptr = slot.err == hipSuccess ? p : nullptr;
+    });
+    *ptr = slot.ptr;
+    *err = slot.err;
+}
 
 // The calling thread's last error message (a fixed buffer: reporting an
 // error allocates nothing).
@@ -885,6 +922,8 @@ int spt_ctx_create(int device, void *hip_stream, spt_ctx **out) {
         if (hipDeviceGetAttribute(&ctx->n_cu, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess ||
             ctx->n_cu <= 0)
             ctx->n_cu = 256;
+        // with the device current: its copy of the no-allocation scratch
+        noalloc_scratch_of(device, &ctx->noalloc, &ctx->noalloc_err);
     }
     *out = ctx;
     return SPT_OK;
@@ -1444,6 +1483,30 @@ int spt_forward_moe_batch_q8(spt_ctx *ctx, const spt_moe_config *cfg, const spt_
     char *S;
     if ((rc = arena(ctx, L.total, &S))) return rc;
     return run_moe_at(ctx, lw, x_dev, out_dev, m, nullptr, S, L, (const uint8_t *)xq_dev);
+}
+
+int spt_forward_moe_batch_noalloc(spt_ctx *ctx, const spt_moe_config *cfg, const spt_moe_layer *lw,
+                                  const float *x_dev, int64_t x_len, float *out_dev, int64_t out_len,
+                                  int64_t batch) {
+    MoEDims m;
+    int rc;
+    if ((rc = validate_moe(ctx, cfg, lw, x_dev, x_len, out_dev, out_len, batch, &m))) return rc;
+    if ((rc = check_cancel(ctx)) || (rc = check_device(ctx))) return rc;
+    const MoELayout L = moe_layout(ctx, m, false, 0);
+    if (L.total > kNoAllocScratchBytes)
+        return fail(SPT_ERR_INVALID,
+                    "MoE batch of %lld tokens needs %zu bytes of scratch; the no-allocation form holds %zu",
+                    (long long)batch, L.total, kNoAllocScratchBytes);
+    if (!ctx->noalloc)
+        return fail(SPT_ERR_DEVICE, "no-allocation scratch unavailable on device %d: %s", ctx->device,
+                    hipGetErrorString(ctx->noalloc_err));
+    // the same launches as spt_forward_moe_batch over the fixed array; no
+    // timing events are recorded (creating them would allocate)
+    const bool timing = ctx->timing;
+    ctx->timing = false;
+    rc = run_moe_at(ctx, lw, x_dev, out_dev, m, nullptr, static_cast<char *>(ctx->noalloc), L);
+    ctx->timing = timing;
+    return rc;
 }
 
 int spt_block_sums(spt_ctx *ctx, const spt_tensor *w, int32_t expert, const void *xq_dev, int64_t rows,

@@ -33,6 +33,7 @@ EXPORTED = (
     "spt_mul_q80_into", "spt_mul_q80_argmax", "spt_mul_q80_into_host", "spt_mul_q80_argmax_host",
     "spt_rmsnorm_into", "spt_rmsnorm_batch_into", "spt_mul_q40_batch_bias_into",
     "spt_mul_q40_batch_q8_into", "spt_mul_q40_qkv_batch_into", "spt_forward_moe_batch_q8",
+    "spt_forward_moe_batch_noalloc",
 )
 KERNEL_KINDS = ("quantize", "route", "gate_up", "down", "combine", "q40", "select", "gate_up_gemm", "down_gemm",
                 "q80", "rmsnorm")
@@ -133,6 +134,8 @@ def lib():
                                         i64], C.c_int),
         "spt_forward_moe_batch_q8": ([vp, C.POINTER(MoEConfig), C.POINTER(MoELayer), vp, vp, i64, vp, i64, i64],
                                      C.c_int),
+        "spt_forward_moe_batch_noalloc": ([vp, C.POINTER(MoEConfig), C.POINTER(MoELayer), vp, i64, vp, i64, i64],
+                                          C.c_int),
         "spt_block_sums": ([vp, T, i32, vp, i64, vp], C.c_int),
         "spt_synth_mxfp4": ([vp, vp, u64, u64, u64, i32, i32], C.c_int),
         "spt_ctx_enable_timing": ([vp, C.c_int], C.c_int),
