@@ -8,7 +8,10 @@ sequence) through the 36 layers; routing is independent per token (router
 N(0,0.02) over RMS-normalised N(0,1) tokens, logits ~N(0,1)).
 
 Timed region: K steps bracketed by torch.cuda.synchronize(); value =
-MoE-layer tokens/s = B * 36 / step time.  A second, event-instrumented pass
+MoE-layer tokens/s = B * 36 / step time.  The step's launches are captured
+once into a HIP graph and the K steps are graph replays (every kernel of
+every layer runs each step; the eager time is reported beside it, and the
+replayed outputs are checked against the eager step's).  A second, event-instrumented pass
 of the same steps measures the average duration of each kernel launch on the
 library's stream; the roofline object is computed for the dominant kernel
 (grouped gate/up GEMV) from its algorithmic bytes per launch.  The CPU
@@ -89,6 +92,10 @@ def parse():
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the prefill workloads (one layer resident; for counter passes)")
     ap.add_argument("--no-lm-head", action="store_true", help="skip the Q8_0 LM head")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="time the decode step with eager launches only (no HIP graph replay)")
+    ap.add_argument("--decode-max-selections", type=int, default=0,
+                    help="decode-path limit of the library (0: its default, negative: off)")
     ap.add_argument("--lm-head-only", action="store_true", help="only the Q8_0 LM head (for profiles)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run a 1 GiB elementwise copy kernel three times (known "
@@ -124,7 +131,10 @@ def main():
     from spt import workloads as W
 
     torch.cuda.set_device(0)
-    stream = torch.cuda.current_stream()
+    # a stream of its own (graph capture cannot use the device's null stream),
+    # made current so torch's own work is ordered with the library's
+    stream = torch.cuda.Stream()
+    torch.cuda.set_stream(stream)
     if args.copy_calibration:
         src = torch.ones(1 << 28, dtype=torch.float32, device="cuda")
         dst = torch.empty_like(src)
@@ -134,6 +144,7 @@ def main():
         log("copy calibration: 3 x 1 GiB elementwise copies done")
         del src, dst
     ctx = spt.Context(0, stream.cuda_stream)
+    ctx.set_decode_max_selections(args.decode_max_selections)
     shp = W.MoEShape()
     if args.lm_head_only:
         print(json.dumps({"lm_head": lm_head(ctx, stream), "rmsnorm_q8": rmsnorm_rows(ctx, stream)}), flush=True)
@@ -183,8 +194,32 @@ def main():
             step()
         end.record(stream)
         torch.cuda.synchronize()
-        wall = time.perf_counter() - wall0
-        ms_step = start.elapsed_time(end) / args.steps
+        eager_ms = start.elapsed_time(end) / args.steps
+        eager_wall = time.perf_counter() - wall0
+        ms_step, wall = eager_ms, eager_wall
+        graph_ok = None
+        if not args.no_graph:
+            # the step's launches captured once into a HIP graph and replayed:
+            # the same kernels, without the host's per-launch cost
+            ref = [o.clone() for o in outs]
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=stream):
+                step()
+            for _ in range(args.warmup):
+                g.replay()
+            torch.cuda.synchronize()
+            graph_ok = all(bool(torch.equal(a_, b_)) for a_, b_ in zip(outs, ref))
+            wall0 = time.perf_counter()
+            start.record(stream)
+            for _ in range(args.steps):
+                g.replay()
+            end.record(stream)
+            torch.cuda.synchronize()
+            wall = time.perf_counter() - wall0
+            ms_step = start.elapsed_time(end) / args.steps
+            del g
+            if not graph_ok:
+                log(f"B={B}: graph replay output differs from the eager step")
         # instrumented pass: per-kernel durations from HIP events
         ctx.enable_timing(True)
         ctx.read_timing()
@@ -201,6 +236,9 @@ def main():
             "batch": B,
             "ms_per_step": ms_step,
             "wall_ms_per_step": wall * 1e3 / args.steps,
+            "launch": "hip graph replay" if graph_ok is not None else "eager",
+            "graph_matches_eager": graph_ok,
+            "eager_ms_per_step": eager_ms,
             "moe_layer_tokens_per_s": B * L / (ms_step / 1e3),
             "decode_tokens_per_s": B / (ms_step / 1e3),
             "distinct_experts_per_layer": float(np.mean(distinct)),

@@ -136,6 +136,18 @@ int spt_ctx_set_cancel_flag(struct spt_ctx *ctx, const volatile int32_t *flag);
  * size (forward/mxfp4_batch.go:55-95). */
 int spt_ctx_set_gemm_min_group(struct spt_ctx *ctx, int32_t min_group);
 
+/* Batches of up to max_selections selections (batch * experts used; experts
+ * used <= 4, and no group on the grouped GEMM) take the decode path: the
+ * top-k inside the gate/up launch (a workgroup per selection) and the
+ * weighted combine inside the down launch, two launches after the router.
+ * 0 restores the default (16 selections: the measured crossover with the
+ * grouped GEMV is between 4 and 8 tokens at top-4); a negative value turns the path
+ * off (every batch through select, the grouped GEMV and combine).  Results
+ * are the same within the fp32 tolerance either way; ids, weights, lists
+ * and the Q8_0 stages are identical.  No reference counterpart (a launch
+ * policy). */
+int spt_ctx_set_decode_max_selections(struct spt_ctx *ctx, int32_t max_selections);
+
 /* Per-kernel timing with HIP events recorded on the context's stream around
  * each launch (measurement instrumentation, off by default).  Kernel kinds: */
 enum {

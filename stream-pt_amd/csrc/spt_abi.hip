@@ -35,6 +35,7 @@ struct spt_ctx {
     double total_ms[SPT_KERNEL_KINDS] = {};
     int64_t launches[SPT_KERNEL_KINDS] = {};
     int32_t gemm_min_group = 0;  // 0: the default policy (kGemmMinGroup)
+    int32_t decode_max_selections = 0;  // 0: kDecodeMaxSelections; < 0: decode path off
     int n_cu = 0;                // compute units of the device
 };
 
@@ -394,10 +395,15 @@ int copy_tap(spt_ctx *ctx, void *dst, const void *src, size_t bytes) {
 // dimension serially, so a few large groups leave most CUs idle).
 constexpr int kGemmMinGroup = 9;
 constexpr int kGemmMinSelections = 1024;
+// Batches of up to this many selections (topk <= 4, no GEMM group) take the
+// decode path: top-k inside the gate/up launch, combine inside the down
+// launch, a workgroup per selection (spt_mx_decode.hip).
+constexpr int kDecodeMaxSelections = 16;
 
 // Scratch layout of one forwardMoEBatch call (offsets into the arena).
 struct MoELayout {
     bool use_gemm;
+    bool decode;  // the two-launch decode path (spt_mx_decode.hip)
     int gemm_min;
     bool forced;
     size_t o_xc, o_xs, o_xm, o_xb, o_logits, o_ids, o_w, o_cnt, o_off, o_list, o_act_list, o_na;
@@ -417,6 +423,8 @@ MoELayout moe_layout(const spt_ctx *ctx, const MoEDims &m, bool act_tap, size_t 
     L.forced = ctx->gemm_min_group > 0;
     L.gemm_min = L.forced ? ctx->gemm_min_group : kGemmMinGroup;
     L.use_gemm = n >= L.gemm_min && (L.forced || n >= kGemmMinSelections);
+    const int dec_max = ctx->decode_max_selections == 0 ? kDecodeMaxSelections : ctx->decode_max_selections;
+    L.decode = !L.use_gemm && m.k <= spt::kDecMaxTopK && n <= dec_max;
     Carve c;
     c.off = base;
     L.o_xc = c.take(B * h), L.o_xs = c.take(B * nbh * 4), L.o_xm = c.take(B * nbh * 64);
@@ -429,7 +437,7 @@ MoELayout moe_layout(const spt_ctx *ctx, const MoEDims &m, bool act_tap, size_t 
     L.o_act = c.take(act_tap ? n * d * 4 : 0), L.o_ac = c.take(n * d), L.o_as = c.take(n * nbd * 4);
     L.o_am = c.take(n * nbd * 64);
     L.o_ab = c.take(L.use_gemm ? n * nbd * 64 : 0);
-    L.o_res = c.take(n * h * 4);
+    L.o_res = c.take(L.decode ? 0 : n * h * 4);  // the decode path combines in its down launch
     L.total = c.off;
     return L;
 }
@@ -476,7 +484,8 @@ int run_moe_at(spt_ctx *ctx, const spt_moe_layer *lw, const float *x, float *out
         SPT_HIP(timed(ctx, SPT_KERNEL_QUANTIZE, [&] {
             return spt::launch_quantize(s, x, B * nbh, xq.codes, xq.scales, nullptr, xq.mxtab, xq.blocks34, xq.btab);
         }));
-        SPT_HIP(timed(ctx, SPT_KERNEL_SELECT, [&] { return spt::launch_select(s, taps->logits_in, (int)B, (int)E, (int)k, so); }));
+        if (!L.decode)
+            SPT_HIP(timed(ctx, SPT_KERNEL_SELECT, [&] { return spt::launch_select(s, taps->logits_in, (int)B, (int)E, (int)k, so); }));
         if ((rc = copy_tap(ctx, taps->logits, taps->logits_in, B * E * 4))) return rc;
     } else {
         // router logits + Q8_0 of x in one launch, then top-k + lists
@@ -485,8 +494,77 @@ int run_moe_at(spt_ctx *ctx, const spt_moe_layer *lw, const float *x, float *out
                                      bias_type(lw->ffn_gate_inp_bias), x, (int)B, (int)h, (int)E, logits, xq);
         }));
         if ((rc = check_cancel(ctx))) return rc;
-        SPT_HIP(timed(ctx, SPT_KERNEL_SELECT, [&] { return spt::launch_select(s, logits, (int)B, (int)E, (int)k, so); }));
+        if (!L.decode)
+            SPT_HIP(timed(ctx, SPT_KERNEL_SELECT, [&] { return spt::launch_select(s, logits, (int)B, (int)E, (int)k, so); }));
         if (taps && (rc = copy_tap(ctx, taps->logits, logits, B * E * 4))) return rc;
+    }
+    if (L.decode) {
+        // gate/up with the top-k of each workgroup's token inside, then down
+        // with the combine inside
+        spt::DecGateUpArgs gu{};
+        gu.g.w[0] = (const uint8_t *)lw->ffn_gate_exps.data;
+        gu.g.w[1] = (const uint8_t *)lw->ffn_up_exps.data;
+        gu.g.expert_bytes = (uint64_t)nbh * 17 * d;
+        gu.g.rows = (int)d;
+        gu.g.nb = (int)nbh;
+        gu.g.bias[0] = bias_ptr(lw->ffn_gate_exps_bias);
+        gu.g.bias_type[0] = bias_type(lw->ffn_gate_exps_bias);
+        gu.g.bias_bytes[0] = bias_bytes(lw->ffn_gate_exps_bias);
+        gu.g.bias[1] = bias_ptr(lw->ffn_up_exps_bias);
+        gu.g.bias_type[1] = bias_type(lw->ffn_up_exps_bias);
+        gu.g.bias_bytes[1] = bias_bytes(lw->ffn_up_exps_bias);
+        gu.g.mxtab = xm;
+        gu.g.scales = xs;
+        gu.g.codes = xc;
+        gu.g.topk = (int)k;
+        gu.g.out = act;
+        gu.g.tap[0] = taps ? taps->gate : nullptr;
+        gu.g.tap[1] = taps ? taps->up : nullptr;
+        gu.g.act_codes = ac;
+        gu.g.act_scales = as;
+        gu.g.act_mxtab = am;
+        gu.g.act_blocks34 = taps ? (uint8_t *)taps->actq : nullptr;
+        gu.logits = taps && taps->logits_in ? taps->logits_in : logits;
+        gu.experts = (int)E;
+        gu.tab_rows = (int)B;
+        gu.ids = so.ids;
+        gu.weights = so.weights;
+        if ((rc = check_cancel(ctx))) return rc;
+        SPT_HIP(timed(ctx, SPT_KERNEL_GATE_UP, [&] { return spt::launch_dec_gate_up(s, gu, (int)n); }));
+        const bool lists = taps && (taps->counts || taps->offsets || taps->list || taps->active || taps->n_active);
+        if (lists) SPT_HIP(timed(ctx, SPT_KERNEL_SELECT, [&] { return spt::launch_pack(s, (int)B, (int)E, (int)k, so); }));
+        spt::DecDownArgs dn{};
+        dn.g.w[0] = (const uint8_t *)lw->ffn_down_exps.data;
+        dn.g.expert_bytes = (uint64_t)nbd * 17 * h;
+        dn.g.rows = (int)h;
+        dn.g.nb = (int)nbd;
+        dn.g.bias[0] = bias_ptr(lw->ffn_down_exps_bias);
+        dn.g.bias_type[0] = bias_type(lw->ffn_down_exps_bias);
+        dn.g.bias_bytes[0] = bias_bytes(lw->ffn_down_exps_bias);
+        dn.g.mxtab = am;
+        dn.g.scales = as;
+        dn.g.codes = ac;
+        dn.g.topk = (int)k;
+        dn.tab_rows = (int)n;
+        dn.ids = so.ids;
+        dn.weights = so.weights;
+        dn.out = out;
+        dn.results = taps ? taps->results : nullptr;
+        if ((rc = check_cancel(ctx))) return rc;
+        SPT_HIP(timed(ctx, SPT_KERNEL_DOWN, [&] { return spt::launch_dec_down(s, dn, (int)B); }));
+        if (taps) {
+            if ((rc = copy_tap(ctx, taps->ids, so.ids, n * 4))) return rc;
+            if ((rc = copy_tap(ctx, taps->weights, so.weights, n * 4))) return rc;
+            if (lists) {
+                if ((rc = copy_tap(ctx, taps->counts, so.counts, E * 4))) return rc;
+                if ((rc = copy_tap(ctx, taps->offsets, so.offsets, (E + 1) * 4))) return rc;
+                if ((rc = copy_tap(ctx, taps->list, so.list, n * 4))) return rc;
+                if ((rc = copy_tap(ctx, taps->active, so.active, E * 4))) return rc;
+                if ((rc = copy_tap(ctx, taps->n_active, so.n_active, 4))) return rc;
+            }
+            if ((rc = copy_tap(ctx, taps->act, act, n * d * 4))) return rc;
+        }
+        return SPT_OK;
     }
     const int slots = (int)(n < E ? n : E);
     spt::MxMfmaArgs ga{};
@@ -989,6 +1067,13 @@ int spt_ctx_set_gemm_min_group(spt_ctx *ctx, int32_t min_group) {
     if ((rc = check_ctx(ctx))) return rc;
     if (min_group < 0) return fail(SPT_ERR_INVALID, "negative GEMM group threshold %d", (int)min_group);
     ctx->gemm_min_group = min_group;
+    return SPT_OK;
+}
+
+int spt_ctx_set_decode_max_selections(spt_ctx *ctx, int32_t max_selections) {
+    int rc;
+    if ((rc = check_ctx(ctx))) return rc;
+    ctx->decode_max_selections = max_selections;
     return SPT_OK;
 }
 

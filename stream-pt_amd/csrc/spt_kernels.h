@@ -91,6 +91,30 @@ struct MxMfmaArgs {
     uint8_t *act_blocks34;
 };
 
+// The decode path (spt_mx_decode.hip) for batches of a few tokens with
+// topk <= kDecMaxTopK: gate/up with the top-k inside, then down with the
+// combine inside.
+constexpr int kDecMaxTopK = 4;
+struct DecGateUpArgs {
+    MxMfmaArgs g;          // the kGateUp fields; g.out the optional fp32 act tap
+    const float *logits;   // [batch][experts] router logits
+    int experts;
+    int tab_rows;          // rows of the x tables (batch)
+    int32_t *ids;          // [batch][topk] selections written by the launch
+    float *weights;
+};
+struct DecDownArgs {
+    MxMfmaArgs g;          // the kDown fields over the act tables
+    int tab_rows;          // rows of the act tables (batch * topk)
+    const int32_t *ids;    // [batch][topk]
+    const float *weights;
+    float *out;            // [batch][rows] combined output
+    float *results;        // optional [batch*topk][rows] per-selection tap
+};
+// n_sel = batch * topk selections (a workgroup per selection and 32 rows).
+hipError_t launch_dec_gate_up(hipStream_t s, const DecGateUpArgs &a, int n_sel);
+hipError_t launch_dec_down(hipStream_t s, const DecDownArgs &a, int batch);
+
 // Grouped MXFP4 x Q8_0 GEMM on the bf16 MFMA (spt_mx_gemm.hip) for the
 // experts of the GEMM list (SelectOut.gm_*): the kGateUp and kDown
 // semantics of MxMfmaArgs, with the activations read as bf16 code tables
@@ -194,6 +218,9 @@ hipError_t launch_quantize(hipStream_t s, const float *x, int64_t nblocks, int8_
 hipError_t launch_route(hipStream_t s, const float *router, const void *bias, int bias_type,
                         const float *x, int batch, int hidden, int experts, float *logits,
                         const QuantOut &q);
+// The per-expert lists of SelectOut from the ids and weights already in it
+// (one workgroup).
+hipError_t launch_pack(hipStream_t s, int batch, int experts, int topk, const SelectOut &o);
 // Top-k + softmax per token, then the per-expert lists (one workgroup).
 hipError_t launch_select(hipStream_t s, const float *logits, int batch, int experts, int topk,
                          const SelectOut &o);

@@ -8,6 +8,7 @@
 // The MXFP4 GEMV lives in spt_mx_mfma.hip.
 #include "spt_device.h"
 #include "spt_kernels.h"
+#include "spt_select.h"
 
 namespace spt {
 
@@ -97,106 +98,6 @@ __device__ inline float router_reduce(float a, int lane) {
     float p = v + w;
     float p1 = __shfl(p, lane + 1), p2 = __shfl(p, lane + 2), p3 = __shfl(p, lane + 3);
     return (p + p1) + (p2 + p3);
-}
-
-// Largest of the wave's 64 values (every lane gets it); NaN operands lose
-// (v_max_f32 returns the other operand), so the result is NaN only when all
-// are.  DPP within rows of 16 (lane ^ 1, ^ 2, half-row and row mirrors), then
-// the four row results through readlane.
-__device__ __attribute__((always_inline)) inline float wave_max(float v) {
-    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false)));
-    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false)));
-    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false)));
-    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false)));
-    const int b = __builtin_bit_cast(int, v);
-    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0));
-    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16));
-    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32));
-    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
-    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
-}
-
-// selectMoEBatch (forward/moe_batch.go:305-342) for one token by one
-// wavefront: k rounds of a strict '>' scan where the lowest index wins ties,
-// NaN and -Inf never win and picked experts are excluded.  Lane L owns
-// experts L, L+64, ...; excluded experts (picked, or past E) hold NaN.  A
-// round takes the largest value m (NaN candidates lose), and if m > -Inf the
-// lowest expert holding a value equal to m (ballots by slot; -0 and +0 tie,
-// as under '>'); otherwise nothing is selectable and the round falls back to
-// Index = round, logit 0.  Then the softmax
-// over the k logits: w = f32(exp(f64(l - max))) (lane r computes rank r's),
-// summed in f32 in rank order, scaled by 1/sum when sum > 0.  Results go to
-// LDS (s_ids/s_w, the token's k slots) and to global ids/weights.
-struct TokenLogits {
-    float v[kMaxExperts / 64];
-};
-
-// Lane L's logits of a token (experts L, L+64, ...; NaN past E).
-__device__ inline TokenLogits load_token_logits(const float *lg, int E) {
-    const int lane = threadIdx.x & 63;
-    TokenLogits tl;
-#pragma unroll
-    for (int i = 0; i < kMaxExperts / 64; i++) {
-        const int ex = lane + 64 * i;
-        tl.v[i] = ex < E ? lg[ex] : __builtin_nanf("");
-    }
-    return tl;
-}
-
-__device__ void select_token(TokenLogits tl, int E, int k, int32_t *ids, float *weights,
-                             int32_t *s_ids, float *s_w) {
-    const int lane = threadIdx.x & 63;
-    const float qnan = __builtin_nanf("");
-    float *v = tl.v;
-    const int nslot = (E + 63) / 64;
-    int my_id = 0;
-    float my_val = 0.0f;
-    for (int r = 0; r < k; r++) {
-        float lm = qnan;
-#pragma unroll
-        for (int i = 0; i < kMaxExperts / 64; i++) lm = fmaxf(lm, v[i]);
-        const float m = wave_max(lm);
-        int bi = r;
-        float bv = 0.0f;
-        if (m > -__builtin_inff()) {
-            bv = m;
-#pragma unroll
-            for (int i = 0; i < kMaxExperts / 64; i++) {
-                if (i >= nslot) break;
-                const uint64_t hit = __ballot(v[i] == m);
-                if (hit) {
-                    bi = 64 * i + __builtin_ctzll(hit);
-                    break;
-                }
-            }
-        }
-        // exclude the pick (in the fallback, expert `round`)
-#pragma unroll
-        for (int i = 0; i < kMaxExperts / 64; i++)
-            if (bi == lane + 64 * i) v[i] = qnan;
-        if (lane == r) {
-            my_id = bi;
-            my_val = bv;
-        }
-    }
-    // max over ranks in order (NaN never replaces: strict '>')
-    float mx = -__builtin_inff();
-    for (int r = 0; r < k; r++) {
-        const float l = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_val), r));
-        if (l > mx) mx = l;
-    }
-    const float e = lane < k ? static_cast<float>(exp(static_cast<double>(my_val - mx))) : 0.0f;
-    float sum = 0.0f;
-    for (int r = 0; r < k; r++) sum += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, e), r));
-    if (lane < k) {
-        const float w = sum > 0.0f ? e * (1.0f / sum) : e;
-        if (s_ids) {
-            s_ids[lane] = my_id;
-            s_w[lane] = w;
-        }
-        ids[lane] = my_id;
-        weights[lane] = w;
-    }
 }
 
 // Inclusive prefix sum over the 64 lanes of a wavefront: Hillis-Steele by
@@ -321,54 +222,71 @@ static size_t select_lds(int n, int E) {
     return sizeof(int32_t) * (2 * (size_t)n + 3 * (size_t)E + 1) + sizeof(uint32_t) * kSelWords * (size_t)E;
 }
 
-// Router logits: one workgroup per (4 experts, 1 token); wave w computes the
-// logit of expert 4*blockIdx.x + w for token blockIdx.y (16 chunk loads in
-// flight per lane).  With q set, the workgroups of token t also quantize its
-// row of x to Q8_0, eight blocks each (a half-wave per block).
-__global__ __launch_bounds__(kWG) void k_route(const float *__restrict__ router,
-                                               const void *bias, int bias_type,
-                                               const float *__restrict__ x, int H, int E,
-                                               float *__restrict__ logits, QuantOut q) {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int e = blockIdx.x * 4 + wave;
-    const int t = blockIdx.y;
+// Router logits: one wavefront per (expert, token), a workgroup each, so a
+// decode step's 128 logits spread over 128 CUs.  The router row and x arrive
+// in LDS through 16-byte loads (segments of kRouteSeg floats, every load of a
+// segment in flight at once; loads past a row read zeros), then lane L runs
+// dotF32AVX2's chain for its accumulator from LDS.  While the loads fly, the
+// wavefronts e < H/64 quantize two blocks of x each (a half-wave per block).
+constexpr int kRouteSeg = 4096;
+template <bool MULTI>  // MULTI: H > kRouteSeg, segments in a loop; else one segment, straight-line
+__global__ __launch_bounds__(64) void k_route(const float *__restrict__ router, const void *bias, int bias_type,
+                                              const float *__restrict__ x, int H, int E,
+                                              float *__restrict__ logits, QuantOut q) {
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    __shared__ __align__(16) float s_w[kRouteSeg], s_x[kRouteSeg];
+    const int lane = threadIdx.x;
+    const int e = blockIdx.x, t = blockIdx.y;
     const float *xt = x + (size_t)t * H;
-    if (q.codes || q.blocks34) {
-        const int nbh = H / 32;
-        for (int b0 = blockIdx.x * (kWG / 32); b0 < nbh; b0 += gridDim.x * (kWG / 32)) {
-            const int b = b0 + (tid >> 5), i = tid & 31;
-            uint16_t dh;
-            int qv;
-            if (q.src34) {
-                const uint8_t *blk = q.src34 + ((size_t)t * nbh + (b < nbh ? b : 0)) * kQ80Block;
-                qv = (int)(int8_t)blk[2 + i];
-                dh = (uint16_t)(blk[0] | (blk[1] << 8));
-            } else {
-                const float v = b < nbh ? xt[b * 32 + i] : 0.0f;
-                qv = q8_quantize_half(v, lane, &dh);  // every lane takes part
-            }
-            if (b < nbh) write_q8_lane(qv, dh, i, (size_t)t * nbh + b, q.codes, q.scales, q.mxtab, q.blocks34, q.btab);
+    // wavefronts past the experts only quantize (their router range is empty)
+    const rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(router + (size_t)(e < E ? e : 0) * H), (short)0,
+                                                        e < E ? H * 4 : 0, kRsrcWord3);
+    const rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(xt), (short)0, H * 4, kRsrcWord3);
+    const int nfull = H / 64, nbh = H / 32;
+    // this wavefront's share of the Q8_0 of x, read before the segment loads
+    const bool qon = (q.codes || q.blocks34) && 2 * e < nbh;
+    const int qb = 2 * e + (lane >> 5), qi = lane & 31;
+    float qin = 0.0f;
+    int qcode = 0;
+    uint16_t qdh = 0;
+    if (qon && qb < nbh) {
+        if (q.src34) {
+            const uint8_t *blk = q.src34 + ((size_t)t * nbh + qb) * kQ80Block;
+            qcode = (int)(int8_t)blk[2 + qi];
+            qdh = (uint16_t)(blk[0] | (blk[1] << 8));
+        } else {
+            qin = xt[qb * 32 + qi];
         }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    constexpr int kLoads = kRouteSeg / 256;  // 16-byte loads per lane per segment and row
+    float acc = 0.0f;
+    for (int s0 = 0; s0 == 0 || (MULTI && s0 < nfull * 64); s0 += kRouteSeg) {
+        u32x4 wv[kLoads], xv[kLoads];
+#pragma unroll
+        for (int j = 0; j < kLoads; j++) {
+            const uint32_t off = (uint32_t)(s0 + 4 * (lane + 64 * j)) * 4u;
+            wv[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, off, 0, 0));
+            xv[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0));
+        }
+        if (s0 == 0 && qon) {
+            uint16_t dh = qdh;
+            const int qv = q.src34 ? qcode : q8_quantize_half(qin, lane, &dh);  // every lane takes part
+            if (qb < nbh) write_q8_lane(qv, dh, qi, (size_t)t * nbh + qb, q.codes, q.scales, q.mxtab, q.blocks34, q.btab);
+        }
+        __syncthreads();  // the previous segment's LDS reads are done
+#pragma unroll
+        for (int j = 0; j < kLoads; j++) {
+            reinterpret_cast<u32x4 *>(s_w)[lane + 64 * j] = wv[j];
+            reinterpret_cast<u32x4 *>(s_x)[lane + 64 * j] = xv[j];
+        }
+        __syncthreads();
+        // chunks of 64 of this segment, in order (dotF32AVX2's FMA chains)
+        const int c1 = min(nfull, (s0 + kRouteSeg) / 64);
+        for (int c = s0 / 64; c < c1; c++) acc = __builtin_fmaf(s_w[c * 64 - s0 + lane], s_x[c * 64 - s0 + lane], acc);
     }
     if (e >= E) return;
-    const float *w = router + (size_t)e * H;
-    const int nfull = H / 64;
-    float acc = 0.0f;
-    for (int c0 = 0; c0 < nfull; c0 += 16) {
-        float wv[16], xv[16];
-#pragma unroll
-        for (int u = 0; u < 16; u++) {
-            const int cc = c0 + u;
-            if (cc < nfull) {
-                wv[u] = w[cc * 64 + lane];
-                xv[u] = xt[cc * 64 + lane];
-            }
-        }
-#pragma unroll
-        for (int u = 0; u < 16; u++)
-            if (c0 + u < nfull) acc = __builtin_fmaf(wv[u], xv[u], acc);
-    }
-    if (nfull * 64 < H && lane < 32) acc = __builtin_fmaf(w[nfull * 64 + lane], xt[nfull * 64 + lane], acc);
+    if (nfull * 64 < H && lane < 32) acc = __builtin_fmaf(router[(size_t)e * H + nfull * 64 + lane], xt[nfull * 64 + lane], acc);
     const float r = router_reduce(acc, lane);
     if (lane == 0) logits[(size_t)t * E + e] = r + bias_at(bias, bias_type, e);
 }
@@ -433,9 +351,18 @@ __global__ __launch_bounds__(kSelWG) void k_pack(int batch, int E, int topk, Sel
 hipError_t launch_route(hipStream_t s, const float *router, const void *bias, int bias_type,
                         const float *x, int batch, int hidden, int experts, float *logits,
                         const QuantOut &q) {
-    dim3 grid((experts + 3) / 4, batch);
-    hipLaunchKernelGGL(k_route, grid, dim3(kWG), 0, s, router, bias, bias_type, x, hidden, experts,
-                       logits, q);
+    // a wavefront per (expert, token); the Q8_0 of x needs H/64 of them per token
+    const int ex = experts > (hidden / 32 + 1) / 2 ? experts : (hidden / 32 + 1) / 2;
+    dim3 grid(ex, batch);
+    if (hidden > kRouteSeg)
+        hipLaunchKernelGGL(k_route<true>, grid, dim3(64), 0, s, router, bias, bias_type, x, hidden, experts, logits, q);
+    else
+        hipLaunchKernelGGL(k_route<false>, grid, dim3(64), 0, s, router, bias, bias_type, x, hidden, experts, logits, q);
+    return hipGetLastError();
+}
+
+hipError_t launch_pack(hipStream_t s, int batch, int experts, int topk, const SelectOut &o) {
+    hipLaunchKernelGGL(k_pack, dim3(1), dim3(kSelWG), select_lds(batch * topk, experts), s, batch, experts, topk, o);
     return hipGetLastError();
 }
 

@@ -33,7 +33,7 @@ EXPORTED = (
     "spt_mul_q80_into", "spt_mul_q80_argmax", "spt_mul_q80_into_host", "spt_mul_q80_argmax_host",
     "spt_rmsnorm_into", "spt_rmsnorm_batch_into", "spt_mul_q40_batch_bias_into",
     "spt_mul_q40_batch_q8_into", "spt_mul_q40_qkv_batch_into", "spt_forward_moe_batch_q8",
-    "spt_forward_moe_batch_noalloc",
+    "spt_forward_moe_batch_noalloc", "spt_ctx_set_decode_max_selections",
 )
 KERNEL_KINDS = ("quantize", "route", "gate_up", "down", "combine", "q40", "select", "gate_up_gemm", "down_gemm",
                 "q80", "rmsnorm")
@@ -105,6 +105,7 @@ def lib():
         "spt_ctx_synchronize": ([vp], C.c_int),
         "spt_ctx_set_cancel_flag": ([vp, vp], C.c_int),
         "spt_ctx_set_gemm_min_group": ([vp, i32], C.c_int),
+        "spt_ctx_set_decode_max_selections": ([vp, i32], C.c_int),
         "spt_alloc": ([vp, u64, C.POINTER(vp)], C.c_int),
         "spt_free": ([vp, vp], C.c_int),
         "spt_copy_h2d": ([vp, vp, vp, u64], C.c_int),
@@ -222,6 +223,11 @@ class Context:
         """Expert groups of at least min_group selections use the grouped
         GEMM, smaller ones the grouped GEMV; 0 restores the default."""
         _check(lib().spt_ctx_set_gemm_min_group(self.handle, int(min_group)))
+
+    def set_decode_max_selections(self, max_selections: int):
+        """Batches of up to max_selections selections take the two-launch
+        decode path; 0 restores the default, a negative value turns it off."""
+        _check(lib().spt_ctx_set_decode_max_selections(self.handle, int(max_selections)))
 
     def set_cancel_flag(self, flag_array):
         """flag_array: a host int32 numpy array of one element, or None."""

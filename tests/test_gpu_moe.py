@@ -74,9 +74,11 @@ def _bias_vec(lay, name, e, dim, O):
     return np.array([O.fp16_to_f32(int(h)) for h in seg], np.float32)
 
 
-# Expert-group thresholds of the grouped GEMM: every group through the GEMM,
-# every group through the GEMV, or the library's default split.
-PATHS = {"default": 0, "gemm": 1, "gemv": 1 << 30}
+# (grouped-GEMM threshold, decode-path limit) of each path: the library's
+# default (small batches on the two-launch decode path), every group through
+# the grouped GEMM, every group through GEMVs (the decode path where it
+# applies), and the grouped GEMV with the decode path off.
+PATHS = {"default": (0, 0), "gemm": (1, 0), "gemv": (1 << 30, 0), "grouped": (1 << 30, -1)}
 
 
 class gemm_path:
@@ -86,10 +88,13 @@ class gemm_path:
         self.ctx, self.path = ctx, path
 
     def __enter__(self):
-        self.ctx.set_gemm_min_group(PATHS[self.path])
+        gm, dec = PATHS[self.path]
+        self.ctx.set_gemm_min_group(gm)
+        self.ctx.set_decode_max_selections(dec)
 
     def __exit__(self, *exc):
         self.ctx.set_gemm_min_group(0)
+        self.ctx.set_decode_max_selections(0)
 
 
 def check_stagewise(O, lay, x, B, g, logits_in=None, sample=None):
@@ -151,15 +156,18 @@ def _nan_equal(a, b):
     return np.array_equal(np.isnan(a), np.isnan(b)) and np.array_equal(a[~np.isnan(a)], b[~np.isnan(b)])
 
 
-def test_moe_decode_gpt_oss_layer(gpu_ctx, O):
+@pytest.mark.parametrize("path", ["default", "grouped"])
+def test_moe_decode_gpt_oss_layer(gpu_ctx, O, path):
     """One GPT-OSS-120B MoE layer, decode of 1 token (128 experts, top-4,
-    MXFP4 experts with E8M0 in [118,124], N(0,0.02) router and biases)."""
+    MXFP4 experts with E8M0 in [118,124], N(0,0.02) router and biases), on
+    the decode path and on the grouped GEMV."""
     from spt import workloads as W
 
     shp = W.MoEShape()
     dl = W.device_layer(gpu_ctx, seed=0, layer=0, shp=shp)
     x = W.x_tokens(0, 0, 1, shp.hidden)
-    g = _run(gpu_ctx, dl.config, dl.layer, x, 1)
+    with gemm_path(gpu_ctx, path):
+        g = _run(gpu_ctx, dl.config, dl.layer, x, 1)
     lay = W.host_layer(0, 0, shp, experts=g["ids"])
     err = check_stagewise(O, lay, x, 1, g)
     want = O.forward_moe_batch(lay, x, 1, q8=True, threads=8)
@@ -218,7 +226,7 @@ def test_moe_prefill_hot_expert(gpu_ctx, O):
     check_stagewise(O, lay, x, batch, g, logits_in=logits, sample=sorted(sample))
 
 
-@pytest.mark.parametrize("path", ["default", "gemm", "gemv"])
+@pytest.mark.parametrize("path", ["default", "gemm", "gemv", "grouped"])
 @pytest.mark.parametrize("experts,topk", [(1, 1), (4, 2), (7, 7), (8, 2)])
 @pytest.mark.parametrize("bias_type", [-1, 0, 1, 30])
 @pytest.mark.parametrize("mode", ROUTER_MODES)
@@ -237,7 +245,7 @@ def test_moe_reference_fixture(gpu_ctx, O, experts, topk, bias_type, mode, path)
             assert_close(g["out"], want, what=f"{mode} batch {batch}")
 
 
-@pytest.mark.parametrize("path", ["gemm", "gemv"])
+@pytest.mark.parametrize("path", ["gemm", "gemv", "grouped"])
 @pytest.mark.parametrize("scale", [0, 2, 241, 248, 254, 255])
 def test_moe_special_scales(gpu_ctx, O, scale, path):
     """moeBatchFixture (hidden 320, expert dim 256: several K segments and row
@@ -263,8 +271,8 @@ def test_moe_special_scales(gpu_ctx, O, scale, path):
             assert_close(g["out"], want, what=f"scale {scale} batch {batch}")
 
 
-@pytest.mark.parametrize("batch", [8, 64])
-def test_moe_decode_continuous_batching(gpu_ctx, O, batch):
+@pytest.mark.parametrize("batch,path", [(8, "default"), (8, "grouped"), (16, "default"), (64, "default")])
+def test_moe_decode_continuous_batching(gpu_ctx, O, batch, path):
     """The continuous-batching decode step at GPT-OSS-120B shape: two MoE
     layers resident at once, `batch` tokens (one per sequence) each routed
     by the layer's own router (N(0,0.02) weights over RMS-normalised N(0,1)
@@ -285,9 +293,10 @@ def test_moe_decode_continuous_batching(gpu_ctx, O, batch):
     taps = [_taps(batch, H, D, E, k) for _ in range(layers)]
     xd = [torch.from_numpy(x).cuda() for x in xs]
     outs = [torch.full((batch * H,), 999.0, dtype=torch.float32, device="cuda") for _ in range(layers)]
-    for l in range(layers):
-        gpu_ctx.forward_moe_batch(dls[l].config, dls[l].layer, xd[l], outs[l], batch, spt.make_taps(**taps[l]))
-    torch.cuda.synchronize()
+    with gemm_path(gpu_ctx, path):
+        for l in range(layers):
+            gpu_ctx.forward_moe_batch(dls[l].config, dls[l].layer, xd[l], outs[l], batch, spt.make_taps(**taps[l]))
+        torch.cuda.synchronize()
     for l in range(layers):
         g = _host(taps[l])
         g["out"] = outs[l].cpu().numpy()
