@@ -92,6 +92,7 @@ def parse():
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the prefill workloads (one layer resident; for counter passes)")
     ap.add_argument("--no-lm-head", action="store_true", help="skip the Q8_0 LM head")
+    ap.add_argument("--q40-only", action="store_true", help="only the Q4_0 attention projections (for profiles)")
     ap.add_argument("--no-graph", action="store_true",
                     help="time the decode step with eager launches only (no HIP graph replay)")
     ap.add_argument("--decode-max-selections", type=int, default=0,
@@ -148,6 +149,10 @@ def main():
     shp = W.MoEShape()
     if args.lm_head_only:
         print(json.dumps({"lm_head": lm_head(ctx, stream), "rmsnorm_q8": rmsnorm_rows(ctx, stream)}), flush=True)
+        ctx.close()
+        return
+    if args.q40_only:
+        print(json.dumps({str(B): q40_projections(ctx, B, W, stream, 20) for B in (1, 32)}), flush=True)
         ctx.close()
         return
     if args.prefill_only:
@@ -413,7 +418,53 @@ def q40_projections(ctx, B, W, stream, reps):
         res[name] = round(us, 1)
         total += us
     res["total_us"] = round(total, 1)
+    res.update(q40_fused(ctx, B, W, stream, reps))
     return res
+
+
+def q40_fused(ctx, B, W, stream, reps):
+    """The same four projections as a layer runs them on the device: Q, K
+    and V in one call on the GGML Q8_0 blocks of the normed input (as the
+    fused RMSNorm writes them), then O on the Q8_0 of the attention context
+    (one quantization of it), microseconds for the whole sequence, and the
+    weight bytes it moves over that time."""
+    import torch
+
+    import spt
+    from spt import synth
+
+    shapes = W.q40_projection_shapes()
+    ts, keep = [], []
+    for i, (name, din, dout) in enumerate(shapes):
+        wb = torch.from_numpy(synth.q40_bytes(synth.stream_key(40 + i, dout), dout, din)).cuda()
+        keep.append(wb)
+        ts.append(spt.Tensor.make(name, spt.TYPE_Q4_0, [din, dout], wb.data_ptr(), wb.numel()))
+    H, QD = shapes[0][1], shapes[3][1]
+    x = torch.from_numpy(synth.normal(synth.stream_key(50, B), B * H)).cuda()
+    ctxv = torch.from_numpy(synth.normal(synth.stream_key(53, B), B * QD)).cuda()
+    xq = torch.empty(B * H // 32 * 34, dtype=torch.uint8, device="cuda")
+    cq = torch.empty(B * QD // 32 * 34, dtype=torch.uint8, device="cuda")
+    ctx.quantize_q8_0(x, xq)
+    ys = [torch.empty(B * d, dtype=torch.float32, device="cuda") for _, _, d in shapes[:3]]
+    yo = torch.empty(B * shapes[3][2], dtype=torch.float32, device="cuda")
+
+    def run():
+        ctx.mul_q40_qkv_batch_into(ts[:3], None, None, ys, B, xq=xq, x_len=B * H)
+        ctx.quantize_q8_0(ctxv, cq)
+        ctx.mul_q40_batch_q8_into(ts[3], None, cq, yo, B)
+
+    for _ in range(3):
+        run()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(reps):
+        run()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) / reps * 1e3
+    wbytes = sum(t.nbytes for t in ts)
+    return {"fused_qkv_o_us": round(us, 1), "fused_weights_gbps": round(wbytes / (us * 1e-6) / 1e9, 1)}
 
 
 def lm_head(ctx, stream, reps=20, rows=201088, input_dim=2880):
