@@ -425,9 +425,9 @@ def q40_projections(ctx, B, W, stream, reps):
 def q40_fused(ctx, B, W, stream, reps):
     """The same four projections as a layer runs them on the device: Q, K
     and V in one call on the GGML Q8_0 blocks of the normed input (as the
-    fused RMSNorm writes them), then O on the Q8_0 of the attention context
-    (one quantization of it), microseconds for the whole sequence, and the
-    weight bytes it moves over that time."""
+    fused RMSNorm writes them), then O on the fp32 attention context (the
+    call quantizes it), microseconds for the whole sequence, and the weight
+    bytes it moves over that time."""
     import torch
 
     import spt
@@ -443,15 +443,13 @@ def q40_fused(ctx, B, W, stream, reps):
     x = torch.from_numpy(synth.normal(synth.stream_key(50, B), B * H)).cuda()
     ctxv = torch.from_numpy(synth.normal(synth.stream_key(53, B), B * QD)).cuda()
     xq = torch.empty(B * H // 32 * 34, dtype=torch.uint8, device="cuda")
-    cq = torch.empty(B * QD // 32 * 34, dtype=torch.uint8, device="cuda")
     ctx.quantize_q8_0(x, xq)
     ys = [torch.empty(B * d, dtype=torch.float32, device="cuda") for _, _, d in shapes[:3]]
     yo = torch.empty(B * shapes[3][2], dtype=torch.float32, device="cuda")
 
     def run():
         ctx.mul_q40_qkv_batch_into(ts[:3], None, None, ys, B, xq=xq, x_len=B * H)
-        ctx.quantize_q8_0(ctxv, cq)
-        ctx.mul_q40_batch_q8_into(ts[3], None, cq, yo, B)
+        ctx.mul_q40_batch_into(ts[3], ctxv, yo, B)
 
     for _ in range(3):
         run()
@@ -464,7 +462,28 @@ def q40_fused(ctx, B, W, stream, reps):
     torch.cuda.synchronize()
     us = e0.elapsed_time(e1) / reps * 1e3
     wbytes = sum(t.nbytes for t in ts)
-    return {"fused_qkv_o_us": round(us, 1), "fused_weights_gbps": round(wbytes / (us * 1e-6) / 1e9, 1)}
+    # the two launches of each of the 36 layers captured into a HIP graph
+    # and replayed, as a decode step replays them
+    layers = 36
+    ref = [y.clone() for y in ys + [yo]]
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        for _ in range(layers):
+            run()
+    for _ in range(3):
+        g.replay()
+    torch.cuda.synchronize()
+    same = all(bool(torch.equal(a, b)) for a, b in zip(ys + [yo], ref))
+    greps = max(1, reps // 10)
+    e0.record(stream)
+    for _ in range(greps):
+        g.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    gus = e0.elapsed_time(e1) / (greps * layers) * 1e3
+    del g
+    return {"fused_qkv_o_us": round(us, 1), "fused_weights_gbps": round(wbytes / (us * 1e-6) / 1e9, 1),
+            "fused_qkv_o_graph_us": round(gus, 1), "graph_matches_eager": same}
 
 
 def lm_head(ctx, stream, reps=20, rows=201088, input_dim=2880):

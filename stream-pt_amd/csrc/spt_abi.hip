@@ -854,8 +854,10 @@ bool q40_gemm_form(int64_t out, int64_t batch) {
 // Arena layout of a Q4_0 call over np projections sharing one input.  The
 // activation views (codes, widened scales, code sums) exist unless the input
 // is GGML Q8_0 blocks that every projection's GEMV reads directly.
+// A call of a few tokens (spt::q40_dec_form) runs as one launch that
+// quantizes or unpacks its input itself: no views.
 struct Q40Plan {
-    bool views;
+    bool views, dec;
     int64_t nb, batch;
     size_t o_c, o_s, o_q, o_part, total;
 };
@@ -864,13 +866,15 @@ Q40Plan q40_plan(const Q40Proj *p, int np, int64_t nb, int64_t batch, bool q8_in
     Q40Plan L{};
     bool gemm = false;
     size_t part = 0;
+    L.dec = spt::q40_dec_form(batch, nb);
     for (int i = 0; i < np; i++) {
+        if (p[i].w->nbytes >= spt::kQ40DecMaxBytes) L.dec = false;
         if (!q40_gemm_form(p[i].out, batch)) continue;
         gemm = true;
         if (p[i].out < spt::kQ40GemmMinRows)
             part = std::max(part, (size_t)spt::kQ40SplitK * batch * p[i].out * 4);
     }
-    L.views = !q8_in || gemm;
+    L.views = !L.dec && (!q8_in || gemm);
     L.nb = nb;
     L.batch = batch;
     Carve c;
@@ -924,7 +928,12 @@ int run_q40_at(spt_ctx *ctx, const Q40Proj *p, int np, const Q40Plan &L, char *S
         g.nmore = ng - 1;
         g.xq34 = L.views ? nullptr : xq34;
         if ((rc = check_cancel(ctx))) return rc;
-        SPT_HIP(timed(ctx, SPT_KERNEL_Q40, [&] { return spt::launch_q40_gemv(ctx->stream, g); }));
+        if (L.dec) {
+            g.xf = x;
+            SPT_HIP(timed(ctx, SPT_KERNEL_Q40, [&] { return spt::launch_q40_dec(ctx->stream, g); }));
+        } else {
+            SPT_HIP(timed(ctx, SPT_KERNEL_Q40, [&] { return spt::launch_q40_gemv(ctx->stream, g); }));
+        }
     }
     return SPT_OK;
 }

@@ -104,6 +104,15 @@ __device__ inline void load_block5_raw(const ByteView &v, uint32_t pos, uint32_t
     d[4] = __builtin_amdgcn_raw_buffer_load_b32(v.r, base + 16, 0, 0);
 }
 
+// Workgroup barrier ordering LDS only: kernels whose waves communicate
+// through LDS alone use it in place of __syncthreads(), which would also wait
+// for every outstanding global load (draining the loads kept in flight).
+__device__ inline void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // ---- fp16 -----------------------------------------------------------------
 __device__ inline float f16_bits_to_f32(uint32_t h) {
     return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h)));

@@ -183,7 +183,31 @@ struct Q40Args {
     // tiles follow this matrix's in the grid
     int nmore;
     Q40Mat more[2];
+    // few-token form only (q40_dec_form): the fp32 activations, quantized to
+    // Q8_0 inside the launch, in place of codes / scales / sumq and xq34
+    const float *xf;
 };
+
+// The matrix of row tile `tile` (of `per_tile` rows) of a launch over
+// several matrices with the same input (Q40Args::more): its fields in place
+// of the first's, and the tile rebased to it.
+__device__ inline Q40Args q40_matrix(const Q40Args &args, int *tile, int per_tile) {
+    Q40Args a = args;
+    for (int i = 0; i < args.nmore; i++) {
+        const int tiles = (a.rows + per_tile - 1) / per_tile;
+        if (*tile < tiles) break;
+        *tile -= tiles;
+        const Q40Mat &m = args.more[i];
+        a.w = m.w;
+        a.nbytes = m.nbytes;
+        a.rows = m.rows;
+        a.y = m.y;
+        a.bias = m.bias;
+        a.bias_type = m.bias_type;
+        a.resid = m.resid;
+    }
+    return a;
+}
 
 // The projection epilogue of forward/layer.go:120-165 and
 // layer_batch.go:68-100: addBias (one f32 add of the decoded bias element),
@@ -245,6 +269,15 @@ constexpr int kQ40SplitMinTokens = 256;
 constexpr int kQ40GemvLds = 160 * 1024;
 constexpr int kQ40MaxInput = kQ40GemvLds / 40 * 32;
 hipError_t launch_q40_gemv(hipStream_t s, const Q40Args &a);
+// Few tokens (spt_q40_dec.hip): up to kQ40DecTokens tokens of inputs up to
+// kQ40DecMaxNb blocks, matrices under 2 GiB, in one launch per call from
+// the fp32 input (Q40Args::xf) or its GGML Q8_0 blocks (xq34); the activation
+// views are not used.
+constexpr int kQ40DecTokens = 4;
+constexpr int kQ40DecMaxNb = 128;
+constexpr uint64_t kQ40DecMaxBytes = 0x80000000ull;
+inline bool q40_dec_form(int64_t batch, int64_t nb) { return batch <= kQ40DecTokens && nb <= kQ40DecMaxNb; }
+hipError_t launch_q40_dec(hipStream_t s, const Q40Args &a);
 // GGML Q8_0 blocks -> codes, widened scales and per-block code sums (the
 // views launch_quantize writes), for nblocks blocks.
 hipError_t launch_q8_unpack(hipStream_t s, const uint8_t *blocks34, int64_t nblocks, int8_t *codes,

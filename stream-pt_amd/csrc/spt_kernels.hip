@@ -386,32 +386,11 @@ hipError_t launch_select(hipStream_t s, const float *logits, int batch, int expe
 // ---------------------------------------------------------------------------
 // Q4_0 x Q8_0 GEMV / small GEMM: y[t][row] for consecutive tokens.
 // ---------------------------------------------------------------------------
-// The matrix of row tile `tile` of a launch over several matrices with the
-// same input (Q40Args::more): its fields in place of the first's, and the
-// tile rebased to it.
-__device__ inline Q40Args q40_matrix(const Q40Args &args, int *tile) {
-    Q40Args a = args;
-    for (int i = 0; i < args.nmore; i++) {
-        const int tiles = (a.rows + kRowsPerWG - 1) / kRowsPerWG;
-        if (*tile < tiles) break;
-        *tile -= tiles;
-        const Q40Mat &m = args.more[i];
-        a.w = m.w;
-        a.nbytes = m.nbytes;
-        a.rows = m.rows;
-        a.y = m.y;
-        a.bias = m.bias;
-        a.bias_type = m.bias_type;
-        a.resid = m.resid;
-    }
-    return a;
-}
-
 template <int MAXP, int NT>
 __global__ __launch_bounds__(kWG) void k_q40_gemv(Q40Args args) {
     extern __shared__ uint32_t smem_u[];
     int tile = blockIdx.x;
-    const Q40Args a = q40_matrix(args, &tile);
+    const Q40Args a = q40_matrix(args, &tile, kRowsPerWG);
     const int nb = a.nb, words = nb * 8;
     uint32_t *s_codes = smem_u;
     float *s_scales = reinterpret_cast<float *>(smem_u + NT * words);

@@ -61,15 +61,6 @@ __host__ __device__ constexpr int tile_region(int nb) {
            1024;
 }
 
-// Workgroup barrier ordering LDS only.  All communication between the
-// waves of k_mx_mfma goes through LDS, and __syncthreads() would also wait
-// for every outstanding global load, draining the next tile in flight.
-__device__ inline void lds_barrier() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
 // Static lane roles.  MFMA A: row i = lane & 15, block gb = lane >> 4 of each
 // chunk.  MFMA B: column c = 8*slot + 4*part + gc holds digit `part` of token
 // `slot`'s block gc; its non-zero half is lo (A blocks gb>>1) or hi (A

@@ -82,7 +82,43 @@ def test_q40_q8_input_equals_fp32_input(gpu_ctx, O, din, dout, batch):
     assert_close(yb.cpu().numpy(), want.reshape(-1), what="q8-input projection")
 
 
-@pytest.mark.parametrize("batch", [1, 32, 300])
+@pytest.mark.parametrize("batch", [1, 2, 3, 4])
+def test_q40_few_tokens_quantize_in_launch(gpu_ctx, O, batch):
+    """Up to four tokens run as one launch that quantizes the fp32 input
+    itself: bit-equal to the same call on the input's Q8_0 blocks from the
+    quantizer (pinned to the oracle bit for bit), on blocks that exercise
+    every rule of the quantization -- all-zero, NaN, Inf, subnormal fp16
+    scale, exact .5 ties, -0 -- in the last token, normal blocks before."""
+    import torch
+
+    from helpers import tie_block
+    from spt import synth
+
+    din, dout = 2880, 512
+    w, wd, t = _q40("attn_k", din, dout, 70)
+    x = synth.normal(synth.stream_key(71, batch), batch * din) * np.float32(3)
+    last = x.reshape(batch, -1, 32)[batch - 1]
+    last[0] = 0.0
+    last[1, 5] = np.nan
+    last[2, 7] = np.inf
+    last[3] = np.float32(1e-30)
+    last[4] = tie_block()
+    last[5] = -0.0
+    last[6] = tie_block() * np.float32(0.5)
+    xd = _dev(x)
+    xq = _q8(gpu_ctx, xd)
+    ya, yb = _zeros(batch * dout), _zeros(batch * dout)
+    gpu_ctx.mul_q40_batch_into(t, xd, ya, batch)
+    gpu_ctx.mul_q40_batch_q8_into(t, None, xq, yb, batch)
+    torch.cuda.synchronize()
+    assert np.array_equal(xq.cpu().numpy(), O.quantize_q8_0(x))
+    assert np.array_equal(bits(ya.cpu().numpy()), bits(yb.cpu().numpy()))
+    if batch > 1:  # the tokens of normal blocks against the oracle
+        want = O.mul_q40_q8(w, x[:(batch - 1) * din], din, dout, batch - 1)
+        assert_close(ya.cpu().numpy()[:(batch - 1) * dout], want, what="few-token projection")
+
+
+@pytest.mark.parametrize("batch", [1, 3, 32, 300])
 @pytest.mark.parametrize("form", ["fp32", "q8"])
 def test_q40_qkv_fused(gpu_ctx, O, batch, form):
     """The Q, K, V projections of one normed input in one call (one

@@ -182,6 +182,10 @@ def test_mxfp4_expert_gemv_odd_half_bias(gpu_ctx, O, bias_type):
 
 @pytest.mark.parametrize("input_dim,output_dim,batch", [
     (2880, 4096, 1), (2880, 512, 1), (4096, 2880, 1), (32, 17, 1),
+    # up to four tokens: one launch quantizing its input itself, every
+    # weight-block count per lane (inputs of 1 to 128 blocks)
+    (2880, 4096, 2), (2880, 512, 3), (4096, 2880, 4), (96, 70, 2), (160, 33, 4), (1024, 100, 3),
+    (2048, 64, 1),
     (2880, 4096, 32), (2880, 512, 32), (4096, 2880, 32), (32, 17, 32),
     # the int8-MFMA GEMM (64 tokens and up): full and ragged token tiles,
     # row counts off the 64-row tile and the 4-row stores, inputs shorter
