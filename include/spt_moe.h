@@ -41,7 +41,9 @@ enum {
     SPT_ERR_INVALID = 1,  /* validation failed; nothing was launched       */
     SPT_ERR_DEVICE = 2,   /* HIP runtime error, or a context without device */
     SPT_ERR_NOMEM = 3,    /* device allocation failed                       */
-    SPT_ERR_CANCELED = 4  /* cancellation flag was set                      */
+    SPT_ERR_CANCELED = 4, /* cancellation flag was set                      */
+    SPT_ERR_IO = 5,       /* a GGUF file could not be opened or read        */
+    SPT_ERR_NOT_FOUND = 6 /* no tensor / metadata key / span of that name   */
 };
 
 /* GGML type ids used on this path (ggufindex/index.go:540-551). */

@@ -15,6 +15,8 @@
 #include <utility>
 #include <vector>
 
+#include "spt_gguf.h"
+#include "spt_gguf_index.h"
 #include "spt_kernels.h"
 #include "spt_moe.h"
 
@@ -990,6 +992,100 @@ int q80_argmax_at(spt_ctx *ctx, const spt_tensor *w, int64_t in, int64_t out, co
 
 }  // namespace
 
+// ---------------------------------------------------------------------------
+// GGUF residency loader
+// ---------------------------------------------------------------------------
+// An opened model: the index and its tensors in the order of Layers then
+// Shared.
+struct spt_gguf {
+    spt::gguf::Model model;
+    std::vector<const spt::gguf::Tensor *> order;
+};
+
+namespace {
+
+void gguf_info(const spt::gguf::Tensor &t, spt_gguf_tensor *o) {
+    memset(o, 0, sizeof *o);
+    o->name = t.name.c_str();
+    o->type = t.type;
+    o->n_dims = (uint32_t)t.shape.size();
+    for (size_t i = 0; i < t.shape.size() && i < 8; i++) o->shape[i] = t.shape[i];
+    o->file = t.range.file;
+    o->layer = t.layer;
+    o->start = t.range.start;
+    o->end = t.range.end;
+}
+
+// Bytes [start, start + n) of a file into device memory at dst: chunks read
+// into the two halves of the pinned staging in turn, each half refilled only
+// after the copy out of it has completed.
+constexpr size_t kLoadChunk = size_t(8) << 20;
+
+int load_range(spt_ctx *ctx, const std::string &path, uint64_t start, uint64_t n, char *dst) {
+    char *buf;
+    int rc;
+    if ((rc = staging(ctx, 2 * kLoadChunk, &buf))) return rc;
+    FILE *f = fopen(path.c_str(), "rb");
+    if (!f) return fail(SPT_ERR_IO, "open %s: %s", path.c_str(), strerror(errno));
+    hipEvent_t ev[2] = {nullptr, nullptr};
+    bool used[2] = {false, false};
+    rc = SPT_OK;
+    if (fseeko(f, (off_t)start, SEEK_SET) != 0) rc = fail(SPT_ERR_IO, "seek %s: %s", path.c_str(), strerror(errno));
+    for (int h = 0; h < 2 && rc == SPT_OK; h++)
+        if (hipEventCreateWithFlags(&ev[h], hipEventDisableTiming) != hipSuccess)
+            rc = fail(SPT_ERR_DEVICE, "cannot create an event");
+    for (uint64_t off = 0, i = 0; rc == SPT_OK && off < n; off += kLoadChunk, i++) {
+        const int h = (int)(i & 1);
+        if (used[h] && hipEventSynchronize(ev[h]) != hipSuccess) {
+            rc = fail(SPT_ERR_DEVICE, "copy to the device failed");
+            break;
+        }
+        const size_t c = (size_t)std::min<uint64_t>(kLoadChunk, n - off);
+        char *half = buf + (size_t)h * kLoadChunk;
+        if (fread(half, 1, c, f) != c) {
+            rc = fail(SPT_ERR_IO, "read %s: unexpected end of file", path.c_str());
+            break;
+        }
+        hipError_t e = hipMemcpyAsync(dst + off, half, c, hipMemcpyHostToDevice, ctx->stream);
+        if (e == hipSuccess) e = hipEventRecord(ev[h], ctx->stream);
+        if (e != hipSuccess) {
+            rc = hip_fail(e, "hipMemcpyAsync");
+            break;
+        }
+        used[h] = true;
+    }
+    const hipError_t se = hipStreamSynchronize(ctx->stream);  // the staging is free again
+    if (rc == SPT_OK && se != hipSuccess) rc = hip_fail(se, "hipStreamSynchronize");
+    for (int h = 0; h < 2; h++)
+        if (ev[h]) (void)hipEventDestroy(ev[h]);
+    fclose(f);
+    return rc;
+}
+
+int gguf_upload(spt_ctx *ctx, const spt_gguf *g, const spt::gguf::Tensor &t, spt_tensor *out) {
+    if (t.shape.size() > 4)
+        return fail(SPT_ERR_INVALID, "\"%s\": %zu dimensions (at most 4 are supported)", t.name.c_str(),
+                    t.shape.size());
+    const uint64_t n = t.range.end - t.range.start;
+    void *d = nullptr;
+    int rc;
+    if ((rc = spt_alloc(ctx, n, &d))) return rc;
+    if ((rc = load_range(ctx, g->model.paths[t.range.file], t.range.start, n, (char *)d))) {
+        (void)hipFree(d);
+        return rc;
+    }
+    memset(out, 0, sizeof *out);
+    out->name = t.name.c_str();
+    out->type = t.type;
+    out->n_dims = (uint32_t)t.shape.size();
+    for (size_t i = 0; i < t.shape.size(); i++) out->shape[i] = t.shape[i];
+    out->nbytes = n;
+    out->data = d;
+    return SPT_OK;
+}
+
+}  // namespace
+
 extern "C" {
 
 const char *spt_last_error(void) { return g_error; }
@@ -1638,6 +1734,131 @@ int spt_synth_mxfp4(spt_ctx *ctx, void *dst_dev, uint64_t key, uint64_t first_bl
         return fail(SPT_ERR_INVALID, "invalid E8M0 range [%d, %d]", scale_lo, scale_hi);
     if ((rc = check_device(ctx))) return rc;
     SPT_HIP(spt::launch_synth_mxfp4(ctx->stream, (uint8_t *)dst_dev, key, first_block, nblocks, scale_lo, scale_hi));
+    return SPT_OK;
+}
+
+
+int spt_gguf_open(const char *const *paths, int32_t n_paths, spt_gguf **out) {
+    if (!out) return fail(SPT_ERR_INVALID, "nil output pointer");
+    *out = nullptr;
+    if (n_paths < 0 || (n_paths > 0 && !paths)) return fail(SPT_ERR_INVALID, "nil path list");
+    std::vector<std::string> ps;
+    for (int32_t i = 0; i < n_paths; i++) {
+        if (!paths[i]) return fail(SPT_ERR_INVALID, "nil path");
+        ps.emplace_back(paths[i]);
+    }
+    spt_gguf *g = new (std::nothrow) spt_gguf;
+    if (!g) return fail(SPT_ERR_NOMEM, "cannot allocate the index");
+    std::string err;
+    if (!spt::gguf::open(ps, &g->model, &err)) {
+        delete g;
+        const bool io = err.find(": open ") != std::string::npos || err.compare(0, 5, "open ") == 0;
+        return fail(io ? SPT_ERR_IO : SPT_ERR_INVALID, "%s", err.c_str());
+    }
+    for (const auto &layer : g->model.layers)
+        for (const auto &t : layer) g->order.push_back(&t);
+    for (const auto &t : g->model.shared) g->order.push_back(&t);
+    *out = g;
+    return SPT_OK;
+}
+
+int spt_gguf_close(spt_gguf *g) {
+    delete g;
+    return SPT_OK;
+}
+
+int spt_gguf_info(const spt_gguf *g, int64_t *layer_count, int64_t *n_tensors, uint64_t *alignment) {
+    if (!g) return fail(SPT_ERR_INVALID, "nil model");
+    if (layer_count) *layer_count = g->model.layer_count;
+    if (n_tensors) *n_tensors = (int64_t)g->order.size();
+    if (alignment) *alignment = g->model.alignment;
+    return SPT_OK;
+}
+
+int spt_gguf_tensor_at(const spt_gguf *g, int64_t i, spt_gguf_tensor *out) {
+    if (!g || !out) return fail(SPT_ERR_INVALID, "nil model or output");
+    if (i < 0 || i >= (int64_t)g->order.size()) return fail(SPT_ERR_NOT_FOUND, "tensor index %lld out of range", (long long)i);
+    gguf_info(*g->order[i], out);
+    return SPT_OK;
+}
+
+int spt_gguf_find(const spt_gguf *g, const char *name, spt_gguf_tensor *out) {
+    if (!g || !name || !out) return fail(SPT_ERR_INVALID, "nil model, name or output");
+    const spt::gguf::Tensor *t = spt::gguf::find(g->model, name);
+    if (!t) return fail(SPT_ERR_NOT_FOUND, "tensor \"%s\" not found", name);
+    gguf_info(*t, out);
+    return SPT_OK;
+}
+
+int spt_gguf_layer_span(const spt_gguf *g, int64_t layer, int32_t i, int32_t *file, uint64_t *start,
+                        uint64_t *end) {
+    if (!g || !file || !start || !end) return fail(SPT_ERR_INVALID, "nil model or output");
+    if (layer < 0 || layer >= (int64_t)g->model.spans.size()) return fail(SPT_ERR_NOT_FOUND, "no layer %lld", (long long)layer);
+    const auto &sp = g->model.spans[(size_t)layer];
+    if (i < 0 || i >= (int32_t)sp.size()) return fail(SPT_ERR_NOT_FOUND, "no span %d of layer %lld", i, (long long)layer);
+    *file = sp[(size_t)i].file;
+    *start = sp[(size_t)i].start;
+    *end = sp[(size_t)i].end;
+    return SPT_OK;
+}
+
+int spt_gguf_metadata(const spt_gguf *g, const char *key, uint32_t *type, int32_t *file, uint64_t *start,
+                      uint64_t *end) {
+    if (!g || !key || !type || !file || !start || !end) return fail(SPT_ERR_INVALID, "nil model, key or output");
+    auto it = g->model.metadata.find(key);
+    if (it == g->model.metadata.end()) return fail(SPT_ERR_NOT_FOUND, "metadata key \"%s\" not found", key);
+    *type = it->second.type;
+    *file = it->second.range.file;
+    *start = it->second.range.start;
+    *end = it->second.range.end;
+    return SPT_OK;
+}
+
+int spt_gguf_upload(spt_ctx *ctx, const spt_gguf *g, const char *name, spt_tensor *out) {
+    int rc;
+    if ((rc = check_ctx(ctx))) return rc;
+    if (!g || !name || !out) return fail(SPT_ERR_INVALID, "nil model, name or output");
+    if ((rc = check_device(ctx))) return rc;
+    const spt::gguf::Tensor *t = spt::gguf::find(g->model, name);
+    if (!t) return fail(SPT_ERR_NOT_FOUND, "tensor \"%s\" not found", name);
+    return gguf_upload(ctx, g, *t, out);
+}
+
+int spt_gguf_upload_moe_layer(spt_ctx *ctx, const spt_gguf *g, int64_t layer, spt_moe_layer *out) {
+    int rc;
+    if ((rc = check_ctx(ctx))) return rc;
+    if (!g || !out) return fail(SPT_ERR_INVALID, "nil model or output");
+    if ((rc = check_device(ctx))) return rc;
+    if (layer < 0 || layer >= (int64_t)g->model.layers.size()) return fail(SPT_ERR_NOT_FOUND, "no layer %lld", (long long)layer);
+    memset(out, 0, sizeof *out);
+    const std::pair<const char *, spt_tensor *> fields[] = {
+        {"ffn_gate_inp.weight", &out->ffn_gate_inp},       {"ffn_gate_inp.bias", &out->ffn_gate_inp_bias},
+        {"ffn_gate_exps.weight", &out->ffn_gate_exps},     {"ffn_gate_exps.bias", &out->ffn_gate_exps_bias},
+        {"ffn_up_exps.weight", &out->ffn_up_exps},         {"ffn_up_exps.bias", &out->ffn_up_exps_bias},
+        {"ffn_down_exps.weight", &out->ffn_down_exps},     {"ffn_down_exps.bias", &out->ffn_down_exps_bias},
+    };
+    // NewLayerWeights: the last tensor (in name order) with a field's suffix wins
+    const spt::gguf::Tensor *pick[8] = {};
+    for (const auto &t : g->model.layers[(size_t)layer])
+        for (int f = 0; f < 8; f++) {
+            const size_t ls = strlen(fields[f].first);
+            if (t.name.size() >= ls && t.name.compare(t.name.size() - ls, ls, fields[f].first) == 0) {
+                pick[f] = &t;
+                break;
+            }
+        }
+    for (int f = 0; f < 8; f++) {
+        if (!pick[f]) continue;
+        if ((rc = gguf_upload(ctx, g, *pick[f], fields[f].second))) {
+            char msg[sizeof g_error];
+            memcpy(msg, g_error, sizeof msg);
+            for (int k = 0; k < f; k++)
+                if (fields[k].second->data) (void)hipFree(const_cast<void *>(fields[k].second->data));
+            memset(out, 0, sizeof *out);
+            memcpy(g_error, msg, sizeof msg);
+            return rc;
+        }
+    }
     return SPT_OK;
 }
 

@@ -1,4 +1,4 @@
-"""CPU tests of the C ABI: every symbol include/spt_moe.h declares is
+"""CPU tests of the C ABI: every symbol include/*.h declares is
 exported, and argument validation follows the reference's rules (a
 validation-only context, device -1, runs every check without a GPU).
 
@@ -17,7 +17,8 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
 def _declared():
-    text = open(os.path.join(ROOT, "include", "spt_moe.h")).read()
+    inc = os.path.join(ROOT, "include")
+    text = "".join(open(os.path.join(inc, f)).read() for f in sorted(os.listdir(inc)) if f.endswith(".h"))
     return sorted(set(re.findall(r"\b(spt_[a-z0-9_]+)\s*\(", text)))
 
 
