@@ -256,6 +256,10 @@ def main():
             "down_gbps": float(dn_bytes / (dn_ms / dn_n / 1e3) / 1e9),
             "kernel_ms_per_step": {k: v[0] / args.steps for k, v in kt.items() if v[1]},
         }
+        res["step_hbm_frac"] = res["step_gbps"] / HBM_PEAK_GBPS
+        res["gate_up_hbm_frac"] = res["gate_up_gbps"] / HBM_PEAK_GBPS
+        res["down_hbm_frac"] = res["down_gbps"] / HBM_PEAK_GBPS
+        res["host_entry_us_per_layer"] = host_entry_us(ctx, layers, xs, B)
         results[B] = res
         log(f"B={B}: {json.dumps(res)}")
         del xs, outs
@@ -311,6 +315,24 @@ def main():
     }
     print(json.dumps(line), flush=True)
     ctx.close()
+
+
+def host_entry_us(ctx, layers, xs, B, reps=3):
+    """The host-slice entry point a cgo caller binds
+    (spt_forward_moe_batch_host): x copied in from pageable host memory and
+    out copied back, synchronised, per layer call -- microseconds per layer,
+    PCIe included (never the bench value)."""
+    import numpy as np
+
+    hx = [x.cpu().numpy() for x in xs]
+    ho = np.empty_like(hx[0])
+    for l in range(len(layers)):
+        ctx.forward_moe_batch_host(layers[l].config, layers[l].layer, hx[l], ho, B)
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        for l in range(len(layers)):
+            ctx.forward_moe_batch_host(layers[l].config, layers[l].layer, hx[l], ho, B)
+    return round((time.perf_counter() - t0) / (reps * len(layers)) * 1e6, 1)
 
 
 def prefill(args, ctx, dl, shp, W, stream, reps=20):
