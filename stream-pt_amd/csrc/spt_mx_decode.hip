@@ -17,13 +17,17 @@
 //     per-selection results never go through memory (they are written only
 //     for the parity tap).
 //
-// A unit is four 16-row tiles in two pairs.  Waves 4p..4p+3 hold pair p's
-// loads in registers (all issued at the start: about 98 KB per unit in
-// flight); pair 0 is written to an LDS image of two tiles and multiplied by
-// all eight waves (K split: wave w takes chunks w, w+8, w+16 of four MXFP4
-// blocks), then pair 1 replaces it.  A workgroup needs two tile images
-// (50 KB at 2880 inputs), so two run per CU and a batch-1 layer's 360 + 180
-// units are resident at once.  The MFMA arithmetic is that of the grouped
+// A unit is four 16-row tiles in two pairs, on W waves (8 for gate/up, 16
+// for down).  Waves W/2 p .. W/2 p + W/2 - 1 hold pair p's loads in
+// registers (all issued at the start: about 98 KB per unit in flight); pair
+// 0 is written to an LDS image of two tiles and multiplied by all W waves
+// (K split: wave w takes chunks w, w+W, ... of four MXFP4 blocks), then
+// pair 1 replaces it.  A workgroup needs two tile images (50 KB at 2880
+// inputs): two gate/up workgroups run per CU, so a batch-1 layer's 360
+// gate/up units are resident at once; its 180 down units take one CU each,
+// with twice the waves, which halves each wave's share of the multiply
+// (8.0 against 8.5 us per batch-1 launch, measured).  The MFMA arithmetic
+// is that of the grouped
 // GEMV (spt_mx_mfma.hip, spt_mx_tile.h): E2M1 weights as stored with their
 // E8M0 as the A scale, the Q8_0 codes split into two exact E4M3 digits, and
 // rows holding an E8M0 outside [4, 240] recomputed with the integer decode.
@@ -38,9 +42,14 @@ namespace {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-// 1 KB loads per wave: a pair's two tiles over four waves, every other load
-// of one tile.
-constexpr int kPairLoads = (tile_loads(kMaxNb) + 1) / 2;
+// A decode workgroup of W waves: W / 2 per pair of tiles, W / 4 per tile,
+// each taking every (W / 4)-th 1 KB load of its tile's image; the K chunks of
+// a multiply split over all W waves.
+template <int W>
+constexpr int pair_loads() { return (tile_loads(kMaxNb) + W / 4 - 1) / (W / 4); }
+template <int W>
+constexpr int dec_chunks() { return ((kMaxNb + 3) / 4 + W - 1) / W; }
+constexpr int kGateUpWaves = 8, kDownWaves = 16;
 
 // Where a tile's bytes come from: a descriptor over its expert matrix from
 // the 16-byte boundary at or below the matrix's first byte (loads past the
@@ -65,26 +74,29 @@ __device__ inline TileSrc tile_src(const uint8_t *matrix, uint64_t matrix_bytes,
 
 // This wave's loads of its tile (loads h0, h0 + 2, ... of nl), nontemporal:
 // each weight byte is read once.
+template <int W>
 struct PairRegs {
-    u32x4 v[kPairLoads];
+    u32x4 v[pair_loads<W>()];
 };
 
 // Issued unconditionally (a load this wave does not need reads past the
 // descriptor's range, which returns zeros), so the compiler's wait counts
 // stay exact: a wait for one of these loads never drains a later one.
-__device__ inline void pair_issue(PairRegs &pr, const TileSrc &s, int h0, int nl, bool on, int lane) {
+template <int W>
+__device__ inline void pair_issue(PairRegs<W> &pr, const TileSrc &s, int h0, int nl, bool on, int lane) {
 #pragma unroll
-    for (int j = 0; j < kPairLoads; j++) {
-        const int i = h0 + 2 * j;
+    for (int j = 0; j < pair_loads<W>(); j++) {
+        const int i = h0 + (W / 4) * j;
         const uint32_t off = (on && i < nl) ? s.start + 1024u * (uint32_t)i + 16u * (uint32_t)lane : 0xFFFFFFF0u;
         pr.v[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(s.rs, off, 0, 2 /* nt */));
     }
 }
 
-__device__ inline void pair_store(uint8_t *region, const PairRegs &pr, int h0, int nl, int lane) {
+template <int W>
+__device__ inline void pair_store(uint8_t *region, const PairRegs<W> &pr, int h0, int nl, int lane) {
 #pragma unroll
-    for (int j = 0; j < kPairLoads; j++) {
-        const int i = h0 + 2 * j;
+    for (int j = 0; j < pair_loads<W>(); j++) {
+        const int i = h0 + (W / 4) * j;
         if (i < nl) *reinterpret_cast<u32x4 *>(region + 1024 * i + 16 * lane) = pr.v[j];
     }
 }
@@ -167,18 +179,19 @@ __device__ __attribute__((always_inline)) inline void pair_chunk(TileView (&tv)[
 
 // The unit's per-tile partial row sums: [wave][tile][row], for the token
 // slot each tile is multiplied against.
+template <int W>
 struct DecShared {
-    float part[kWaves][4][16];
-    int special[kWaves];
+    float part[W][4][16];
+    int special[W];
 };
 
 // Multiplies the pair in the image (tiles 2p, 2p+1 with views tv) over this
 // wave's chunks and stores its partial sums for token slot slot_of(h);
 // returns the pair's special-scale tile bits (tile 2p + h) for rows in range.
-template <class SlotOf>
+template <int W, class SlotOf>
 __device__ __attribute__((always_inline)) inline int pair_multiply(TileView (&tv)[2], int p, int nb, int wave,
-                                                                  const LaneRole &L, const ChunkB (&cb)[kChunksPerWave],
-                                                                  DecShared &sh, SlotOf slot_of, const bool (&row_ok)[2]) {
+                                                                  const LaneRole &L, const ChunkB (&cb)[dec_chunks<W>()],
+                                                                  DecShared<W> &sh, SlotOf slot_of, const bool (&row_ok)[2]) {
     float acc[2][4];
 #pragma unroll
     for (int h = 0; h < 2; h++)
@@ -186,8 +199,8 @@ __device__ __attribute__((always_inline)) inline int pair_multiply(TileView (&tv
         for (int k = 0; k < 4; k++) acc[h][k] = 0.0f;
     const int nchunks = (nb + 3) >> 2;
 #pragma unroll
-    for (int j = 0; j < kChunksPerWave; j++) {
-        const int c = wave + kWaves * j;
+    for (int j = 0; j < dec_chunks<W>(); j++) {
+        const int c = wave + W * j;
         if (c < nchunks) pair_chunk(tv, c, 4 * c + 3 >= nb, nb, L, b_operand(cb[j].v, L), cb[j].dx, acc);
     }
     const int lane = threadIdx.x & 63, j8 = lane & 7;
@@ -211,10 +224,11 @@ __device__ __attribute__((always_inline)) inline int pair_multiply(TileView (&tv
 // ---------------------------------------------------------------------------
 // gate/up
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(4))) void k_dec_gate_up(DecGateUpArgs da) {
+__global__ __launch_bounds__(64 * kGateUpWaves) __attribute__((amdgpu_waves_per_eu(4))) void k_dec_gate_up(DecGateUpArgs da) {
     const MxMfmaArgs &a = da.g;
     extern __shared__ __align__(16) uint8_t smem_b[];
-    __shared__ DecShared sh;
+    constexpr int W = kGateUpWaves;
+    __shared__ DecShared<W> sh;
     __shared__ int32_t s_ids[kMaxTopK];
     __shared__ float s_w[kMaxTopK];
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -241,7 +255,7 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(4))) void k
     const int nb = a.nb;
     const uint32_t row_bytes = (uint32_t)nb * kMxBlock;
     const int nl = tile_loads(nb), region = tile_region(nb);
-    const int pair = wave >> 2, q = wave & 3, my_tile = 2 * pair + (q & 1), h0 = q >> 1;
+    const int pair = wave / (W / 2), q = wave % (W / 2), my_tile = 2 * pair + (q & 1), h0 = q >> 1;
     auto tile_row0 = [&](int T) { return 32 * u + 16 * (T >> 1); };
     auto tile_matrix = [&](int T) { return a.w[T & 1] + (uint64_t)e * a.expert_bytes; };
     LaneRole L;
@@ -259,9 +273,9 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(4))) void k
     // chunks and the biases (small, from L2), then the unit's weights, so
     // that waiting for the former never drains the latter.
     const ActTables xt = act_tables(a.mxtab, a.scales, da.tab_rows, nb);
-    ChunkB cb[kChunksPerWave];
+    ChunkB cb[dec_chunks<W>()];
 #pragma unroll
-    for (int j = 0; j < kChunksPerWave; j++) cb[j] = chunk_b(xt, nb, wave + kWaves * j, t, L.slot == 0, L);
+    for (int j = 0; j < dec_chunks<W>(); j++) cb[j] = chunk_b(xt, nb, wave + W * j, t, L.slot == 0, L);
     // the gate and up bias words of act row 32u + (lane & 31), kept in
     // registers until the epilogue (wave 0 adds them)
     const BiasView bv0 = make_bias_view(a.bias[0], a.bias_bytes[0], a.bias_type[0]);
@@ -269,7 +283,7 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(4))) void k
     const uint32_t bidx = (uint32_t)e * (uint32_t)a.rows + (uint32_t)(32 * u + (lane & 31));
     const uint32_t braw0 = bias_raw(bv0, bidx), braw1 = bias_raw(bv1, bidx);
     __builtin_amdgcn_sched_barrier(0);  // keep the small loads ahead of the weights
-    PairRegs pr;
+    PairRegs<W> pr;
     {
         const TileSrc src = tile_src(tile_matrix(my_tile), a.expert_bytes, tile_row0(my_tile), row_bytes);
         pair_issue(pr, src, h0, nl, tile_row0(my_tile) < a.rows, lane);
@@ -289,14 +303,14 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(4))) void k
             tv[h] = tile_view(smem_b + (size_t)h * region, lead + (uint32_t)L.i * row_bytes, L);
             row_ok[h] = tile_row0(T) + L.i < a.rows;
         }
-        smask |= pair_multiply(tv, p, nb, wave, L, cb, sh, slot0, row_ok);
+        smask |= pair_multiply<W>(tv, p, nb, wave, L, cb, sh, slot0, row_ok);
         lds_barrier();  // the image is free for the next pair; partial sums in place
     }
     if (lane == 0) sh.special[wave] = smask;
     lds_barrier();
     int spec = 0;
 #pragma unroll
-    for (int v = 0; v < kWaves; v++) spec |= sh.special[v];
+    for (int v = 0; v < W; v++) spec |= sh.special[v];
     if (spec) {
         // tiles with an E8M0 outside [kEMin, kEMax]: wave T recomputes tile
         // T's rows with the integer decode (four lanes per row)
@@ -309,7 +323,7 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(4))) void k
             if (sub == 0) {
                 sh.part[0][T][row_l] = v;
 #pragma unroll
-                for (int w = 1; w < kWaves; w++) sh.part[w][T][row_l] = 0.0f;
+                for (int w = 1; w < W; w++) sh.part[w][T][row_l] = 0.0f;
             }
         }
         lds_barrier();
@@ -321,7 +335,7 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(4))) void k
         const int el = lane & 31, Tg = el < 16 ? 0 : 2, ri = el & 15;
         float gv = sh.part[0][Tg][ri], uv = sh.part[0][Tg + 1][ri];
 #pragma unroll
-        for (int v = 1; v < kWaves; v++) {
+        for (int v = 1; v < W; v++) {
             gv += sh.part[v][Tg][ri];
             uv += sh.part[v][Tg + 1][ri];
         }
@@ -344,10 +358,11 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(4))) void k
 // ---------------------------------------------------------------------------
 // down + combine
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(4))) void k_dec_down(DecDownArgs da) {
+__global__ __launch_bounds__(64 * kDownWaves) __attribute__((amdgpu_waves_per_eu(4))) void k_dec_down(DecDownArgs da) {
     const MxMfmaArgs &a = da.g;
     extern __shared__ __align__(16) uint8_t smem_b[];
-    __shared__ DecShared sh;
+    constexpr int W = kDownWaves;
+    __shared__ DecShared<W> sh;
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int units = a.rows >> 4;
     const int t = blockIdx.x / units, u = blockIdx.x - t * units;
@@ -365,7 +380,7 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(4))) void k
     const int nb = a.nb;
     const uint32_t row_bytes = (uint32_t)nb * kMxBlock;
     const int nl = tile_loads(nb), region = tile_region(nb);
-    const int pair = wave >> 2, q = wave & 3, my_tile = 2 * pair + (q & 1), h0 = q >> 1;
+    const int pair = wave / (W / 2), q = wave % (W / 2), my_tile = 2 * pair + (q & 1), h0 = q >> 1;
     const int row0 = 16 * u;
     auto pick = [](const int (&v)[4], int T) { return T == 0 ? v[0] : T == 1 ? v[1] : T == 2 ? v[2] : v[3]; };
     auto pickb = [](const bool (&v)[4], int T) { return T == 0 ? v[0] : T == 1 ? v[1] : T == 2 ? v[2] : v[3]; };
@@ -386,9 +401,9 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(4))) void k
     // biases, the unit's weights, then pair 1's B operands (needed only
     // after pair 1's weights), so no wait drains a load issued after it.
     const ActTables at = act_tables(a.mxtab, a.scales, da.tab_rows, nb);
-    ChunkB cb[2][kChunksPerWave];
+    ChunkB cb[2][dec_chunks<W>()];
 #pragma unroll
-    for (int j = 0; j < kChunksPerWave; j++) cb[0][j] = chunk_b(at, nb, wave + kWaves * j, t * k + L.slot, pickb(on, L.slot), L);
+    for (int j = 0; j < dec_chunks<W>(); j++) cb[0][j] = chunk_b(at, nb, wave + W * j, t * k + L.slot, pickb(on, L.slot), L);
     // each rank's bias word of row row0 + (tid & 15), kept in registers until
     // the epilogue (threads tid < 16 add them)
     const BiasView bv = make_bias_view(a.bias[0], a.bias_bytes[0], a.bias_type[0]);
@@ -397,14 +412,14 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(4))) void k
 #pragma unroll
     for (int T = 0; T < 4; T++) braw[T] = bias_raw(bv, bias_index(T));
     __builtin_amdgcn_sched_barrier(0);  // keep the small loads ahead of the weights
-    PairRegs pr;
+    PairRegs<W> pr;
     {
         const TileSrc src = tile_src(tile_matrix(my_tile), a.expert_bytes, row0, row_bytes);
         pair_issue(pr, src, h0, nl, pickb(on, my_tile), lane);
     }
 #pragma unroll
-    for (int j = 0; j < kChunksPerWave; j++)
-        cb[1][j] = chunk_b(at, nb, wave + kWaves * j, t * k + 2 + L.slot, pickb(on, 2 + L.slot), L);
+    for (int j = 0; j < dec_chunks<W>(); j++)
+        cb[1][j] = chunk_b(at, nb, wave + W * j, t * k + 2 + L.slot, pickb(on, 2 + L.slot), L);
     auto slot_h = [](int h) { return h; };
     int smask = 0;
 #pragma unroll
@@ -420,14 +435,14 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(4))) void k
             tv[h] = tile_view(smem_b + (size_t)h * region, lead + (uint32_t)L.i * row_bytes, L);
             row_ok[h] = pickb(on, T) && row0 + L.i < a.rows;
         }
-        if (on[2 * p] || on[2 * p + 1]) smask |= pair_multiply(tv, p, nb, wave, L, cb[p], sh, slot_h, row_ok);
+        if (on[2 * p] || on[2 * p + 1]) smask |= pair_multiply<W>(tv, p, nb, wave, L, cb[p], sh, slot_h, row_ok);
         lds_barrier();
     }
     if (lane == 0) sh.special[wave] = smask;
     lds_barrier();
     int spec = 0;
 #pragma unroll
-    for (int v = 0; v < kWaves; v++) spec |= sh.special[v];
+    for (int v = 0; v < W; v++) spec |= sh.special[v];
     if (spec) {
         if (wave < 4 && ((spec >> wave) & 1)) {
             const int T = wave, row_l = lane >> 2, sub = lane & 3, row = row0 + row_l;
@@ -439,7 +454,7 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(4))) void k
             if (sub == 0) {
                 sh.part[0][T][row_l] = v;
 #pragma unroll
-                for (int w = 1; w < kWaves; w++) sh.part[w][T][row_l] = 0.0f;
+                for (int w = 1; w < W; w++) sh.part[w][T][row_l] = 0.0f;
             }
         }
         lds_barrier();
@@ -455,7 +470,7 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(4))) void k
             if (!on[T]) continue;
             float v = sh.part[0][T][tid];
 #pragma unroll
-            for (int w = 1; w < kWaves; w++) v += sh.part[w][T][tid];
+            for (int w = 1; w < W; w++) v += sh.part[w][T][tid];
             v += bias_value(bv, braw[T], bias_index(T));
             if (da.results) da.results[((size_t)t * k + T) * a.rows + row] = v;
             o = __builtin_fmaf(v, wt[T], o);
@@ -470,7 +485,7 @@ hipError_t launch_dec_gate_up(hipStream_t s, const DecGateUpArgs &a, int n_sel) 
     if (n_sel <= 0 || a.g.rows <= 0) return hipSuccess;
     if (a.g.nb <= 0 || a.g.nb > kMaxNb || a.g.topk > kDecMaxTopK || (a.g.rows & 31)) return hipErrorInvalidConfiguration;
     const int units = a.g.rows >> 5;
-    hipLaunchKernelGGL(k_dec_gate_up, dim3(n_sel * units), dim3(kWG), dec_lds(a.g.nb), s, a);
+    hipLaunchKernelGGL(k_dec_gate_up, dim3(n_sel * units), dim3(64 * kGateUpWaves), dec_lds(a.g.nb), s, a);
     return hipGetLastError();
 }
 
@@ -478,7 +493,7 @@ hipError_t launch_dec_down(hipStream_t s, const DecDownArgs &a, int batch) {
     if (batch <= 0 || a.g.rows <= 0) return hipSuccess;
     if (a.g.nb <= 0 || a.g.nb > kMaxNb || a.g.topk > kDecMaxTopK || (a.g.rows & 15)) return hipErrorInvalidConfiguration;
     const int units = a.g.rows >> 4;
-    hipLaunchKernelGGL(k_dec_down, dim3(batch * units), dim3(kWG), dec_lds(a.g.nb), s, a);
+    hipLaunchKernelGGL(k_dec_down, dim3(batch * units), dim3(64 * kDownWaves), dec_lds(a.g.nb), s, a);
     return hipGetLastError();
 }
 
