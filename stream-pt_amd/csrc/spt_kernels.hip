@@ -222,6 +222,61 @@ static size_t select_lds(int n, int E) {
     return sizeof(int32_t) * (2 * (size_t)n + 3 * (size_t)E + 1) + sizeof(uint32_t) * kSelWords * (size_t)E;
 }
 
+// Router logits for batches of more than kRouteLdsMaxBatch tokens: one
+// workgroup per (4 experts, 1 token); wave w computes the logit of expert
+// 4 blockIdx.x + w for token blockIdx.y straight from memory (16 chunk
+// loads in flight per lane), so a batch's 128 x B wavefronts keep many
+// loads in flight per CU.  With q set, the workgroups of token t also
+// quantize its row of x to Q8_0, eight blocks each (a half-wave per block).
+// The FMA chains and the reduction are those of k_route below: the logits
+// are the same bits.
+__global__ __launch_bounds__(kWG) void k_route_rows(const float *__restrict__ router, const void *bias,
+                                                    int bias_type, const float *__restrict__ x, int H, int E,
+                                                    float *__restrict__ logits, QuantOut q) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int e = blockIdx.x * 4 + wave;
+    const int t = blockIdx.y;
+    const float *xt = x + (size_t)t * H;
+    if (q.codes || q.blocks34) {
+        const int nbh = H / 32;
+        for (int b0 = blockIdx.x * (kWG / 32); b0 < nbh; b0 += gridDim.x * (kWG / 32)) {
+            const int b = b0 + (tid >> 5), i = tid & 31;
+            uint16_t dh;
+            int qv;
+            if (q.src34) {
+                const uint8_t *blk = q.src34 + ((size_t)t * nbh + (b < nbh ? b : 0)) * kQ80Block;
+                qv = (int)(int8_t)blk[2 + i];
+                dh = (uint16_t)(blk[0] | (blk[1] << 8));
+            } else {
+                const float v = b < nbh ? xt[b * 32 + i] : 0.0f;
+                qv = q8_quantize_half(v, lane, &dh);  // every lane takes part
+            }
+            if (b < nbh) write_q8_lane(qv, dh, i, (size_t)t * nbh + b, q.codes, q.scales, q.mxtab, q.blocks34, q.btab);
+        }
+    }
+    if (e >= E) return;
+    const float *w = router + (size_t)e * H;
+    const int nfull = H / 64;
+    float acc = 0.0f;
+    for (int c0 = 0; c0 < nfull; c0 += 16) {
+        float wv[16], xv[16];
+#pragma unroll
+        for (int u = 0; u < 16; u++) {
+            const int cc = c0 + u;
+            if (cc < nfull) {
+                wv[u] = w[cc * 64 + lane];
+                xv[u] = xt[cc * 64 + lane];
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < 16; u++)
+            if (c0 + u < nfull) acc = __builtin_fmaf(wv[u], xv[u], acc);
+    }
+    if (nfull * 64 < H && lane < 32) acc = __builtin_fmaf(w[nfull * 64 + lane], xt[nfull * 64 + lane], acc);
+    const float r = router_reduce(acc, lane);
+    if (lane == 0) logits[(size_t)t * E + e] = r + bias_at(bias, bias_type, e);
+}
+
 // Router logits: one wavefront per (expert, token), a workgroup each, so a
 // decode step's 128 logits spread over 128 CUs.  The router row and x arrive
 // in LDS through 16-byte loads (segments of kRouteSeg floats, every load of a
@@ -229,6 +284,9 @@ static size_t select_lds(int n, int E) {
 // dotF32AVX2's chain for its accumulator from LDS.  While the loads fly, the
 // wavefronts e < H/64 quantize two blocks of x each (a half-wave per block).
 constexpr int kRouteSeg = 4096;
+// Up to this many tokens the router spreads over one workgroup per (expert,
+// token) with LDS staging (latency); beyond, k_route_rows (throughput).
+constexpr int kRouteLdsMaxBatch = 4;
 template <bool MULTI>  // MULTI: H > kRouteSeg, segments in a loop; else one segment, straight-line
 __global__ __launch_bounds__(64) void k_route(const float *__restrict__ router, const void *bias, int bias_type,
                                               const float *__restrict__ x, int H, int E,
@@ -351,6 +409,12 @@ __global__ __launch_bounds__(kSelWG) void k_pack(int batch, int E, int topk, Sel
 hipError_t launch_route(hipStream_t s, const float *router, const void *bias, int bias_type,
                         const float *x, int batch, int hidden, int experts, float *logits,
                         const QuantOut &q) {
+    if (batch > kRouteLdsMaxBatch) {
+        dim3 grid((experts + 3) / 4, batch);
+        hipLaunchKernelGGL(k_route_rows, grid, dim3(kWG), 0, s, router, bias, bias_type, x, hidden, experts, logits,
+                           q);
+        return hipGetLastError();
+    }
     // a wavefront per (expert, token); the Q8_0 of x needs H/64 of them per token
     const int ex = experts > (hidden / 32 + 1) / 2 ? experts : (hidden / 32 + 1) / 2;
     dim3 grid(ex, batch);
