@@ -48,6 +48,13 @@ __device__ inline void dma16_nt(const u32x4v &rs, uint32_t lds, uint32_t voff, u
     asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, %2 offen nt lds" ::"v"(voff), "s"(rs), "s"(soff), "{m0}"(lds)
                  : "memory");
 }
+// dma16 without the memory clobber, for a load issued in the middle of the
+// reads of another stage: it writes only LDS that nothing reads before the
+// next full wait and barrier (which are memory clobbers themselves), so the
+// compiler may keep scheduling the surrounding LDS reads across it.
+__device__ inline void dma16_other_stage(const u32x4v &rs, uint32_t lds, uint32_t voff, uint32_t soff) {
+    asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(rs), "s"(soff), "{m0}"(lds));
+}
 __device__ inline void dma4(const u32x4v &rs, uint32_t lds, uint32_t voff, uint32_t soff) {
     asm volatile("s_nop 4\n\tbuffer_load_dword %0, %1, %2 offen lds" ::"v"(voff), "s"(rs), "s"(soff), "{m0}"(lds)
                  : "memory");
@@ -442,17 +449,27 @@ __device__ inline void write_q8_lane(int q, uint16_t dh, int lane, size_t blk, i
 // A double constant written into registers where it is used: the volatile
 // moves cannot be hoisted out of a loop, so a routine called once per
 // several iterations does not hold its constants in registers across the
-// whole loop (where a register-bound loop would spill them).
-template <uint64_t BITS>
+// whole loop (where a register-bound loop would spill them).  KREG picks the
+// registers: kConstVgpr, two vector moves per use; kConstSgpr, two scalar
+// moves per use (issued beside the vector instructions, and the double FMA
+// takes the scalar pair as an operand).
+enum KConst { kConstVgpr = 0, kConstSgpr = 1 };
+template <int KREG, uint64_t BITS>
 __device__ __attribute__((always_inline)) inline double kdouble() {
     uint32_t lo, hi;
-    asm volatile("v_mov_b32 %0, %2\n\tv_mov_b32 %1, %3"
-                 : "=v"(lo), "=v"(hi)
-                 : "i"((uint32_t)(BITS & 0xFFFFFFFFu)), "i"((uint32_t)(BITS >> 32)));
+    if constexpr (KREG == kConstSgpr)
+        asm volatile("s_mov_b32 %0, %2\n\ts_mov_b32 %1, %3"
+                     : "=s"(lo), "=s"(hi)
+                     : "i"((uint32_t)(BITS & 0xFFFFFFFFu)), "i"((uint32_t)(BITS >> 32)));
+    else
+        asm volatile("v_mov_b32 %0, %2\n\tv_mov_b32 %1, %3"
+                     : "=v"(lo), "=v"(hi)
+                     : "i"((uint32_t)(BITS & 0xFFFFFFFFu)), "i"((uint32_t)(BITS >> 32)));
     return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
 }
-#define SPT_KD(c) kdouble<__builtin_bit_cast(uint64_t, (double)(c))>()
+#define SPT_KD(c) kdouble<KREG, __builtin_bit_cast(uint64_t, (double)(c))>()
 
+template <int KREG = kConstVgpr>
 __device__ inline double exp_f64(double x) {
     if (!(x <= 709.78)) return x != x ? x : __builtin_inf();
     if (x < -745.2) return 0.0;
@@ -476,11 +493,12 @@ __device__ inline double exp_f64(double x) {
     return __builtin_ldexp(p, (int)k);
 }
 
+template <int KREG = kConstVgpr>
 __device__ inline float swiglu(float gate, float up) {
     float g = (gate > 7.0f) ? 7.0f : gate;
     float u = (up > 7.0f) ? 7.0f : up;
     u = (u < -7.0f) ? -7.0f : u;
-    float e = static_cast<float>(exp_f64(static_cast<double>(-1.702f * g)));
+    float e = static_cast<float>(exp_f64<KREG>(static_cast<double>(-1.702f * g)));
     return g / (1.0f + e) * (u + 1.0f);
 }
 

@@ -43,33 +43,35 @@ constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kBM = 256;               // weight rows per work item (gate/up: 128 gate + 128 up)
 constexpr int kBN = kGemmTokens;       // list entries per work item
-constexpr int kSeg = 8;                // 32-element blocks per K segment (136 bytes of a row)
-constexpr int kStages = 2;             // LDS stages; the next segment is in flight while one is multiplied
+constexpr int kSeg = 4;                // 32-element blocks per K segment (68 bytes of a row)
+constexpr int kStages = 3;             // LDS stages: two segments in flight while one is multiplied
+constexpr int kAhead = kStages - 1;    // segments issued ahead of the one multiplied
 // A stage: row r's window (the segment's bytes from the 16-byte boundary at
-// or below its first byte) in 10 slots of 16 bytes (16-byte aligned loads:
+// or below its first byte) in 6 slots of 16 bytes (16-byte aligned loads:
 // a load crossing the end of the descriptor's range would read zeros for all
 // its bytes).  The 64 lanes of a DMA load fill 64 consecutive slots, so a
-// stage's 256 x 10 slots take 40 loads per workgroup, five per wave; loads
-// 0-19 hold rows 0-127.
-constexpr int kAPieces = 10;
+// stage's 256 x 6 slots take 24 loads per workgroup, three per wave; loads
+// 0-11 hold rows 0-127.
+constexpr int kAPieces = (kSeg * kMxBlock + 15 + 15) / 16;
 constexpr int kASlots = kAPieces;
 constexpr int kARow = 16 * kASlots;
 constexpr int kAInstr = kBM * kASlots / 64;
-// B stage: per entry 32 slots of 16 bytes (8 blocks x 4 quarters of the bf16
-// code table); quarter piece p of entry t sits in slot p ^ (t & 15), so the
-// 16 entries of an MFMA fragment read 16 different bank groups.
+// B stage: per entry 4 * kSeg slots of 16 bytes (kSeg blocks x 4 quarters of
+// the bf16 code table); quarter piece p of entry t sits in slot p ^ (t & 15),
+// so the 16 entries of an MFMA fragment read 16 different bank groups.
 constexpr int kOffB = kBM * kARow;
-constexpr int kOffD = kOffB + kBN * kSeg * 64;  // d_x [entry][kSeg]
-constexpr int kStageBytes = kOffD + kBN * kSeg * 4;
+constexpr int kOffD = kOffB + kBN * kSeg * 64;  // d_x [entry][kSeg], then the waves without d_x entries
+constexpr int kStageBytes = kOffD + 64 * kWaves * 4;
 constexpr int kEMin = 4, kEMax = 240;
 constexpr int kXcds = 8;  // accelerator complex dies of an MI355X
 constexpr uint32_t kOOR = 0x80000000u;  // buffer offset past every range: reads zero
 static_assert(kSeg * kMxBlock + 15 <= 16 * kAPieces, "A window");
 static_assert(kAInstr % kWaves == 0 && kBN * kSeg * 4 % kThreads == 0, "stage loads");
 static_assert(kBM / 2 * kASlots % 64 == 0, "gate rows fill whole A loads");
-static_assert(kBN * kSeg == 64 * kWaves, "one d_x load per wave");
-constexpr int kALoads = kAInstr / kWaves;           // 5
-constexpr int kBLoads = kBN * kSeg * 4 / kThreads;  // 4
+static_assert(kBN * kSeg <= 64 * kWaves && 4 * kSeg <= 16, "one d_x load per wave; B swizzle within 16 slots");
+constexpr int kALoads = kAInstr / kWaves;           // 3
+constexpr int kBLoads = kBN * kSeg * 4 / kThreads;  // 2
+constexpr int kSegLoads = kALoads + kBLoads + 1;    // DMA loads per wave and segment
 
 
 // Integer-decode dot of one weight row with one entry's Q8_0 row (the
@@ -121,66 +123,71 @@ __device__ __attribute__((always_inline)) inline uint32_t nibble_word(const uint
     return __builtin_amdgcn_alignbyte(pw[1], pw[0], o & 3u);
 }
 
-// One full segment (kSeg blocks) with NTF token fragments, straight-line:
-// the A bytes of all blocks first, the B fragments and d_x one block ahead,
-// then per block its A decode, MFMAs and the FMAs that apply d_x (the two
-// waves of a SIMD overlap one's FMAs with the other's MFMAs).
-template <int NTF>
-__device__ __attribute__((always_inline)) inline void seg_full(const uint8_t *st, const uint32_t (&a_img)[2],
-                                                               const uint32_t (&b_lane)[kSeg], int g, int i16,
-                                                               float (&acc)[2][4][4], uint32_t (&emin)[2],
-                                                               uint32_t (&emax)[2]) {
-    uint32_t eb[kSeg][2], w4[kSeg][2];
+// Blocks [J0, J1) of a full segment with NTF token fragments, straight-line:
+// the A bytes of those blocks first, the B fragments and d_x one block
+// ahead, then per block its A decode, MFMAs and the FMAs that apply d_x (the
+// two waves of a SIMD overlap one's FMAs with the other's MFMAs).  A full
+// segment is two such halves, so the rest of the next segment's loads can
+// go out between them without stretching the live ranges of either.
+template <int NTF, int J0, int J1>
+__device__ __attribute__((always_inline)) inline void seg_blocks(const uint8_t *st, const uint32_t (&a_img)[2],
+                                                                 const uint32_t (&b_lane)[kSeg], int g, int i16,
+                                                                 float (&acc)[2][4][4], uint32_t (&emin)[2],
+                                                                 uint32_t (&emax)[2]) {
+    constexpr int NJ = J1 - J0;
+    uint32_t eb[NJ][2], w4[NJ][2];
 #pragma unroll
-    for (int j = 0; j < kSeg; j++)
+    for (int jj = 0; jj < NJ; jj++)
 #pragma unroll
         for (int rf = 0; rf < 2; rf++) {
-            eb[j][rf] = st[a_img[rf] + 17 * j];
-            w4[j][rf] = nibble_word(st, a_img[rf] + 17u * (uint32_t)j + 1u + 4u * (uint32_t)g);
+            const int j = J0 + jj;
+            eb[jj][rf] = st[a_img[rf] + 17 * j];
+            w4[jj][rf] = nibble_word(st, a_img[rf] + 17u * (uint32_t)j + 1u + 4u * (uint32_t)g);
         }
     bf16x8 Bv[2][NTF];
     float dx[2][NTF];
-    auto load_b = [&](int j) {
+    auto load_b = [&](int jj) {
+        const int j = J0 + jj;
 #pragma unroll
         for (int tf = 0; tf < NTF; tf++) {
-            Bv[j & 1][tf] = *reinterpret_cast<const bf16x8 *>(st + kOffB + tf * (16 * kSeg * 64) + b_lane[j]);
-            dx[j & 1][tf] = *reinterpret_cast<const float *>(st + kOffD + ((16 * tf + i16) * kSeg + j) * 4);
+            Bv[jj & 1][tf] = *reinterpret_cast<const bf16x8 *>(st + kOffB + tf * (16 * kSeg * 64) + b_lane[j]);
+            dx[jj & 1][tf] = *reinterpret_cast<const float *>(st + kOffD + ((16 * tf + i16) * kSeg + j) * 4);
         }
     };
     load_b(0);
 #pragma unroll
-    for (int j = 0; j < kSeg; j++) {
-        if (j + 1 < kSeg) load_b(j + 1);
+    for (int jj = 0; jj < NJ; jj++) {
+        if (jj + 1 < NJ) load_b(jj + 1);
         v4f D[2][NTF];
 #pragma unroll
         for (int rf = 0; rf < 2; rf++) {
-            const float sc = __uint_as_float(eb[j][rf] << 23);
+            const float sc = __uint_as_float(eb[jj][rf] << 23);
             u32x4 av;
-            av.x = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w4[j][rf], sc, 0));
-            av.y = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w4[j][rf], sc, 1));
-            av.z = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w4[j][rf], sc, 2));
-            av.w = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w4[j][rf], sc, 3));
+            av.x = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w4[jj][rf], sc, 0));
+            av.y = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w4[jj][rf], sc, 1));
+            av.z = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w4[jj][rf], sc, 2));
+            av.w = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w4[jj][rf], sc, 3));
             const bf16x8 A = __builtin_bit_cast(bf16x8, av);
 #pragma unroll
             for (int tf = 0; tf < NTF; tf++)
-                D[rf][tf] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, Bv[j & 1][tf], v4f{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+                D[rf][tf] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, Bv[jj & 1][tf], v4f{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
         }
 #pragma unroll
         for (int rf = 0; rf < 2; rf++)
 #pragma unroll
             for (int tf = 0; tf < NTF; tf++)
 #pragma unroll
-                for (int r = 0; r < 4; r++) acc[rf][tf][r] = __builtin_fmaf(D[rf][tf][r], dx[j & 1][tf], acc[rf][tf][r]);
+                for (int r = 0; r < 4; r++) acc[rf][tf][r] = __builtin_fmaf(D[rf][tf][r], dx[jj & 1][tf], acc[rf][tf][r]);
     }
 #pragma unroll
     for (int rf = 0; rf < 2; rf++)
 #pragma unroll
-        for (int j = 0; j < kSeg; j += 2) {
-            emin[rf] = min(emin[rf], min(eb[j][rf], eb[j + 1][rf]));
-            emax[rf] = max(emax[rf], max(eb[j][rf], eb[j + 1][rf]));
+        for (int jj = 0; jj < NJ; jj += 2) {
+            emin[rf] = min(emin[rf], min(eb[jj][rf], eb[jj + 1][rf]));
+            emax[rf] = max(emax[rf], max(eb[jj][rf], eb[jj + 1][rf]));
         }
 }
-static_assert(kSeg % 2 == 0, "seg_full's exponent reduction");
+static_assert(kSeg % 4 == 0, "seg_blocks' halves and exponent reduction");
 
 // The last segment when it holds jn < kSeg blocks.
 template <int NTF>
@@ -226,18 +233,30 @@ __device__ __attribute__((always_inline)) inline void seg_part(const uint8_t *st
 // unit are consecutive (they share the unit's weight rows through the
 // caches); workgroup b takes items b, b + G, b + 2G, ...  Gate/up units are
 // 128 output rows: weight rows 0-127 of the item are gate rows, 128-255 the
-// up rows of the same outputs, and wave w multiplies gate and up rows
-// 16w .. 16w+15, so the SwiGLU is local to the wave; the Q8_0 block of act
-// (32 rows) spans waves 2b and 2b+1.  Down units are 256 rows, wave w rows
-// 32w .. 32w+31.  Every wave takes all 64 entries: 2 x 4 MFMA tiles per block.
+// up rows of the same outputs, and wave w multiplies the gate and up rows of
+// the same 16 outputs, so the SwiGLU is local to the wave.  Those 16 outputs
+// are half of the Q8_0 block 32 * (w / 2) .. +31 of the unit: elements
+// 8 * (w % 2) + 0..7 and 16 + 8 * (w % 2) + 0..7 (the unit's local row with
+// bits 3 and 4 exchanged), so every dword j of the block's bf16 code table
+// (elements j and j + 16) is made by one wave.  Down units are 256 rows,
+// wave w rows 32w .. 32w+31.  Every wave takes all 64 entries: 2 x 4 MFMA
+// tiles per block.
 //
 // The K loop runs over segments of kSeg blocks through kStages LDS stages
-// filled by LDS DMA loads (global/buffer -> LDS, no registers): segment s+1
-// is loaded while segment s is multiplied.
+// filled by LDS DMA loads (global/buffer -> LDS, no registers): segments s+1
+// and s+2 are in flight while segment s is multiplied.  Segments are
+// numbered across the workgroup's items, so the first segments of the next
+// item go to the stages the current item's last segment does not use, and
+// their loads can be issued without waiting for the slower waves to finish
+// that last segment.
 template <int MODE>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void k_mx_gemm(MxGemmArgs a) {
     extern __shared__ __align__(16) uint8_t lds[];
     __shared__ float s_amax[kWaves][kBN];  // gate/up: per wave and entry, |act| max of its 16 rows (-1: NaN)
+    // per item parity: the bias of the item's rows (matrix order; gate/up:
+    // gate rows then up rows) and the item's list entries (-1 past its end)
+    __shared__ __align__(16) float s_bias[2][kBM];
+    __shared__ int s_ent[2][kBN];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -264,18 +283,21 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
     uint32_t b_lane[kSeg];
 #pragma unroll
     for (int j = 0; j < kSeg; j++) b_lane[j] = (uint32_t)i16 * (kSeg * 64) + 16u * (uint32_t)((4 * j + g) ^ i16);
+    typedef __attribute__((address_space(3))) uint8_t lds_u8;
+    const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>((lds_u8 *)lds);
 
-    for (int it = vb; it < total; it += G) {
-        // item -> (slot, unit, token tile)
-        int lo = 0, hi = n_slots - 1;
-        while (lo < hi) {
-            const int mid = (lo + hi + 1) >> 1;
-            if (a.gm_tile_off[mid] * units <= it)
-                lo = mid;
-            else
-                hi = mid - 1;
+    int seg0 = 0;   // stage of the item's first segment
+    int parity = 0; // item parity (s_bias / s_ent buffer)
+    for (int it = vb; it < total; it += G, seg0 = (seg0 + nseg) % kStages, parity ^= 1) {
+        // item -> slot: the number of slots i >= 1 whose first item is at or
+        // below it (gm_tile_off is increasing), 64 slots per ballot
+        int slot = 0;
+        for (int c = 1; c < n_slots; c += 64) {
+            const int i = c + lane;
+            const bool le = i < n_slots && a.gm_tile_off[i] * units <= it;
+            slot += __popcll(__ballot(le));
         }
-        const int slot = lo;
+        slot = __builtin_amdgcn_readfirstlane(slot);
         const int tile0 = a.gm_tile_off[slot], ntile = a.gm_tile_off[slot + 1] - tile0;
         const int rel = it - tile0 * units;
         const int u = rel / ntile, tt = rel - u * ntile;
@@ -288,12 +310,20 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
         const u32x4v rs0 = expert_rsrc(a.w[0], a.expert_bytes, e, &le0);
         const u32x4v rs1 = MODE == kGateUp ? expert_rsrc(a.w[1], a.expert_bytes, e, &le1) : rs0;
         if (MODE != kGateUp) le1 = le0;
-        // LDS row r -> matrix row
-        auto mrow = [&](int r) { return MODE == kGateUp ? u * (kBM / 2) + (r & (kBM / 2 - 1)) : u * kBM + r; };
+        // LDS row r -> matrix row (gate/up: bits 3 and 4 of the unit's local
+        // row exchanged, so a wave's 16 rows hold whole code-table dwords)
+        auto mrow = [&](int r) {
+            if (MODE == kGateUp) {
+                const int x = r & (kBM / 2 - 1);
+                return u * (kBM / 2) + ((x & ~0x18) | ((x & 8) << 1) | ((x >> 1) & 8));
+            }
+            return u * kBM + r;
+        };
 
         // this thread's DMA loads: A load i = wave + 8k fills slots 64i..64i+63
-        // (slot q: row q / 10, piece q % 10), B slots (entry (tid + 512k)/32),
-        // d_x (entry (64*wave + lane)/8)
+        // (slot q: row q / kASlots, piece q % kASlots), B slots (entry
+        // (tid + 512k) / (4 kSeg)), d_x (entry (64*wave + lane) / kSeg);
+        // entries past nt read nothing
         uint32_t a_pos[kALoads];
         bool a_ok[kALoads];
 #pragma unroll
@@ -307,31 +337,45 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
         uint32_t b_off[kBLoads];
 #pragma unroll
         for (int k = 0; k < kBLoads; k++) {
-            const int q = tid + kThreads * k, t = q >> 5, piece = (q & 31) ^ (t & 15);
-            int ar = 0;  // entries past nt load row 0 (unused)
+            const int q = tid + kThreads * k, t = q / (4 * kSeg), piece = (q % (4 * kSeg)) ^ (t & 15);
+            b_off[k] = kOOR;
             if (t < nt) {
                 const int ent = a.list[begin + t];
-                ar = MODE == kGateUp ? ent / a.topk : ent;
+                const int ar = MODE == kGateUp ? ent / a.topk : ent;
+                b_off[k] = ((uint32_t)ar * (uint32_t)nb + (uint32_t)(piece >> 2)) * 64u + 16u * (uint32_t)(piece & 3);
             }
-            b_off[k] = ((uint32_t)ar * (uint32_t)nb + (uint32_t)(piece >> 2)) * 64u + 16u * (uint32_t)(piece & 3);
         }
-        uint32_t d_off = 0;
+        uint32_t d_off = kOOR;
         {
             const int idx = 64 * wave + lane, t = idx / kSeg, j = idx % kSeg;
-            int ar = 0;
             if (t < nt) {
                 const int ent = a.list[begin + t];
-                ar = MODE == kGateUp ? ent / a.topk : ent;
+                const int ar = MODE == kGateUp ? ent / a.topk : ent;
+                d_off = ((uint32_t)ar * (uint32_t)nb + (uint32_t)j) * 4u;
             }
-            d_off = ((uint32_t)ar * (uint32_t)nb + (uint32_t)j) * 4u;
         }
-        typedef __attribute__((address_space(3))) uint8_t lds_u8;
-        const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>((lds_u8 *)lds);
-        // ten DMA loads per wave and stage (A x5, B x4, d_x x1).  The A
-        // window of segment s starts at the 16-byte boundary at or below
-        // the row's byte pos + 136s (a_pos holds pos + 16 * piece).
-        auto issue = [&](int s) {
-            const uint32_t st = lds0 + (uint32_t)(s % kStages) * kStageBytes;
+        // this thread's share of the item's bias and entries (staged in LDS
+        // once segment 0's loads have landed)
+        float bias_v = 0.0f;
+        int ent_v = -1;
+        if (tid < kBM) {
+            const int m = MODE == kGateUp ? tid / (kBM / 2) : 0;
+            const int row = MODE == kGateUp ? u * (kBM / 2) + (tid & (kBM / 2 - 1)) : u * kBM + tid;
+            if (row < a.rows) bias_v = bias_at(a.bias[m], a.bias_type[m], (uint64_t)e * a.rows + row);
+        } else if (tid < kBM + kBN) {
+            if (tid - kBM < nt) ent_v = a.list[begin + tid - kBM];
+        }
+        // kSegLoads DMA loads per wave and stage (A x3, B x2, d_x x1), in
+        // two parts: the weights and d_x, then the B codes (a wave stalls at
+        // a load's issue while its CU's memory queue is full; the second part
+        // goes out half a segment later, when the first has drained).  The
+        // A window of segment s starts at the 16-byte boundary at or below
+        // the row's byte pos + 68s (a_pos holds pos + 16 * piece).  Lanes
+        // whose entries are past nt read nothing (zeros); the d_x loads of
+        // waves 4-7 hold no entries and fill the stage's spare d_x slots.
+        auto stage_of = [&](int s) { return lds0 + (uint32_t)((seg0 + s) % kStages) * kStageBytes; };
+        auto issue_a = [&](int s) {
+            const uint32_t st = stage_of(s);
 #pragma unroll
             for (int k = 0; k < kALoads; k++) {
                 const int i = wave + kWaves * k;
@@ -340,10 +384,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
                 dma16((MODE == kGateUp && i >= kAInstr / 2) ? rs1 : rs0, st + 16u * 64u * (uint32_t)i,
                       a_ok[k] ? (pos & ~15u) : kOOR, 0u);
             }
+            dma4(rs_d, st + kOffD + 256u * wave, d_off, (uint32_t)(kSeg * 4) * (uint32_t)s);
+        };
+        auto issue_b = [&](int s) {
+            const uint32_t st = stage_of(s);
 #pragma unroll
             for (int k = 0; k < kBLoads; k++)
-                dma16(rs_b, st + kOffB + 16u * (64 * wave + kThreads * k), b_off[k], (uint32_t)(kSeg * 64) * (uint32_t)s);
-            dma4(rs_d, st + kOffD + 256u * wave, d_off, (uint32_t)(kSeg * 4) * (uint32_t)s);
+                dma16_other_stage(rs_b, st + kOffB + 16u * (64 * wave + kThreads * k), b_off[k],
+                                  (uint32_t)(kSeg * 64) * (uint32_t)s);
         };
 
         // this lane's A rows: LDS row and matrix byte position (the window of
@@ -368,28 +416,75 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
                 for (int r = 0; r < 4; r++) acc[rf][tf][r] = 0.0f;
         uint32_t emin[2] = {255u, 255u}, emax[2] = {0u, 0u};
 
+        // segment 0's loads, the bias and entries into LDS (waiting for
+        // their loads waits for segment 0's too, which the K loop would),
+        // then the loads of the other segments issued ahead
+        issue_a(0);
+        issue_b(0);
+        asm volatile("" ::: "memory");
+        if (tid < kBM)
+            s_bias[parity][tid] = bias_v;
+        else if (tid < kBM + kBN)
+            s_ent[parity][tid - kBM] = ent_v;
+        asm volatile("" ::: "memory");
+        for (int s = 1; s < kAhead && s < nseg; s++) {
+            issue_a(s);
+            issue_b(s);
+        }
+
         // The K loop, instantiated per number of token fragments (so the
-        // accumulators stay in place through it).
+        // accumulators stay in place through it): the segments whose loads
+        // issue a later segment's in a loop of its own (one straight-line
+        // body, so the accumulators keep their registers across iterations),
+        // then the last kAhead segments.
         auto kloop = [&](auto ntf_c) {
             constexpr int NTF = decltype(ntf_c)::value;
-            issue(0);
-            for (int s = 0; s < nseg; s++) {
-                // this wave's loads of segment s have landed; after the
-                // barrier every wave's have, and every wave is done with
-                // segment s-1, whose stage segment s+1 reuses
-                asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
-                stage_barrier();
-                if (s + 1 < nseg) issue(s + 1);
-                const uint8_t *st = lds + (size_t)(s % kStages) * kStageBytes;
-                const int jn = min(kSeg, nb - kSeg * s);
-                uint32_t a_img[2];
+            static_assert(kAhead == 2, "the waits below keep one segment in flight");
+            auto a_img_of = [&](int s, uint32_t(&a_img)[2]) {
 #pragma unroll
                 for (int rf = 0; rf < 2; rf++)
                     a_img[rf] = l_row[rf] + ((l_pos[rf] + (uint32_t)(kSeg * kMxBlock) * (uint32_t)s) & 15u);
-                if (jn == kSeg)
-                    seg_full<NTF>(st, a_img, b_lane, g, i16, acc, emin, emax);
-                else
-                    seg_part<NTF>(st, a_img, b_lane, g, i16, jn, acc, emin, emax);
+            };
+            const uint8_t *const st_base = lds;
+            int s = 0;
+            for (; s + kAhead < nseg; s++) {
+                // this wave's loads of segment s have landed (those of s+1,
+                // issued after them, may not have); after the barrier every
+                // wave's have, and every wave is done with segment s-1, whose
+                // stage segment s+2 reuses
+                asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(kSegLoads) : "memory");
+                stage_barrier();
+                issue_a(s + kAhead);
+                const uint8_t *st = st_base + (size_t)((seg0 + s) % kStages) * kStageBytes;
+                uint32_t a_img[2];
+                a_img_of(s, a_img);
+                seg_blocks<NTF, 0, kSeg / 2>(st, a_img, b_lane, g, i16, acc, emin, emax);
+                issue_b(s + kAhead);
+                seg_blocks<NTF, kSeg / 2, kSeg>(st, a_img, b_lane, g, i16, acc, emin, emax);
+            }
+            // the segment before the last (full: only the last can be partial)
+            if (s + 1 < nseg) {
+                asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(kSegLoads) : "memory");
+                stage_barrier();
+                const uint8_t *st = st_base + (size_t)((seg0 + s) % kStages) * kStageBytes;
+                uint32_t a_img[2];
+                a_img_of(s, a_img);
+                seg_blocks<NTF, 0, kSeg / 2>(st, a_img, b_lane, g, i16, acc, emin, emax);
+                seg_blocks<NTF, kSeg / 2, kSeg>(st, a_img, b_lane, g, i16, acc, emin, emax);
+                s++;
+            }
+            // the last segment
+            asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+            stage_barrier();
+            const uint8_t *st = st_base + (size_t)((seg0 + s) % kStages) * kStageBytes;
+            uint32_t a_img[2];
+            a_img_of(s, a_img);
+            const int jn = nb - kSeg * s;
+            if (jn == kSeg) {
+                seg_blocks<NTF, 0, kSeg / 2>(st, a_img, b_lane, g, i16, acc, emin, emax);
+                seg_blocks<NTF, kSeg / 2, kSeg>(st, a_img, b_lane, g, i16, acc, emin, emax);
+            } else {
+                seg_part<NTF>(st, a_img, b_lane, g, i16, jn, acc, emin, emax);
             }
         };
         if (ntf == 4)
@@ -404,10 +499,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
         // entries of this lane's token columns
         int ent[4];
 #pragma unroll
-        for (int tf = 0; tf < 4; tf++) {
-            const int t = 16 * tf + i16;
-            ent[tf] = t < nt ? a.list[begin + t] : -1;
-        }
+        for (int tf = 0; tf < 4; tf++) ent[tf] = s_ent[parity][16 * tf + i16];
 
         // rows with an E8M0 outside [kEMin, kEMax]: the integer decode, one
         // entry per lane, moved into the accumulators by lane shuffles
@@ -442,11 +534,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
         if constexpr (MODE == kDown) {
 #pragma unroll
             for (int rf = 0; rf < 2; rf++) {
-                const int row = u * kBM + 32 * wave + 16 * rf + 4 * g;
+                const int lrow = 32 * wave + 16 * rf + 4 * g, row = u * kBM + lrow;
                 if (row >= a.rows) continue;
-                float bsum[4];
-#pragma unroll
-                for (int r = 0; r < 4; r++) bsum[r] = bias_at(a.bias[0], a.bias_type[0], (uint64_t)e * a.rows + row + r);
+                const v4f bsum = *reinterpret_cast<const v4f *>(&s_bias[parity][lrow]);
 #pragma unroll
                 for (int tf = 0; tf < 4; tf++) {
                     if (ent[tf] < 0) continue;
@@ -456,21 +546,21 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
                     *reinterpret_cast<v4f *>(a.out + (size_t)ent[tf] * a.rows + row) = o;
                 }
             }
-            // every wave is done with the stages before the next item's loads
-            stage_barrier();
         } else {
-            // output rows u*128 + 16*wave + 4g + r: gate (rf 0), up (rf 1)
-            const int row = u * (kBM / 2) + 16 * wave + 4 * g;
+            // output rows row + r (r = 0..3): element el0 + r of the unit's
+            // Q8_0 block 32 * (wave / 2) .. +31; gate (rf 0), up (rf 1)
+            const int half = wave & 1;
+            const int el0 = 16 * (g >> 1) + 8 * half + 4 * (g & 1);
+            const int lrow = 32 * (wave >> 1) + el0, row = u * (kBM / 2) + lrow;
             const bool rok = row < a.rows;
-            float bg[4], bu[4];
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                bg[r] = rok ? bias_at(a.bias[0], a.bias_type[0], (uint64_t)e * a.rows + row + r) : 0.0f;
-                bu[r] = rok ? bias_at(a.bias[1], a.bias_type[1], (uint64_t)e * a.rows + row + r) : 0.0f;
-            }
+            const v4f bg = *reinterpret_cast<const v4f *>(&s_bias[parity][lrow]);
+            const v4f bu = *reinterpret_cast<const v4f *>(&s_bias[parity][kBM / 2 + lrow]);
+            // (token fragments past ntf hold no entries: their SwiGLU, the
+            // epilogue's main cost, is skipped)
             float act[4][4];
 #pragma unroll
             for (int tf = 0; tf < 4; tf++) {
+                if (tf >= ntf) continue;
                 float amax = 0.0f;
                 bool nan = false;
                 v4f gv, uv, av;
@@ -496,33 +586,46 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
                 const bool nan_any = ((__ballot(nan) >> i16) & 0x0001000100010001ull) != 0;
                 if (g == 0) s_amax[wave][16 * tf + i16] = nan_any ? -1.0f : amax;
             }
-            // every wave is also done with the stages before the next item's loads
+            // both halves of each block's |act| max are in LDS (the next
+            // item writes s_amax only after a barrier of its K loop, which
+            // every wave reaches after reading this item's)
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
             stage_barrier();
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
             const int blk_row = u * (kBM / 2) + 32 * (wave >> 1);  // first row of this wave pair's Q8_0 block
-            const int half = wave & 1;                             // elements 16*half .. 16*half+15 of it
             const int nbo = a.rows / 32;
 #pragma unroll
             for (int tf = 0; tf < 4; tf++) {
-                if (ent[tf] < 0 || blk_row >= a.rows) continue;
+                if (tf >= ntf) continue;
                 const float m0 = s_amax[wave][16 * tf + i16], m1 = s_amax[wave ^ 1][16 * tf + i16];
                 const bool nan_any = m0 < 0.0f || m1 < 0.0f;
                 const float d = nan_any ? __builtin_nanf("") : fmaxf(m0, m1) / 127.0f;
                 const float id = (d != 0.0f) ? 1.0f / d : 0.0f;
                 const uint16_t dh = f32_to_f16_bits(d);
-                int q[4];
+                uint32_t qw = 0;  // the four codes, element el0 + r in byte r
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
                     const float rq = __builtin_roundf(act[tf][r] * id);
-                    q[r] = (rq != rq) ? 0 : (rq > 127.0f ? 127 : (rq < -127.0f ? -127 : (int)rq));
+                    const int q = (rq != rq) ? 0 : (rq > 127.0f ? 127 : (rq < -127.0f ? -127 : (int)rq));
+                    qw |= (uint32_t)(q & 0xff) << (8 * r);
                 }
+                // the codes of elements el0 ^ 16 + r (lane ^ 32), for the
+                // code-table dwords: this lane writes r = 2 * (g >> 1) + 0..1
+                const uint32_t qp = (uint32_t)__shfl_xor((int)qw, 32);
+                if (ent[tf] < 0 || blk_row >= a.rows) continue;
                 const size_t blk = (size_t)ent[tf] * nbo + blk_row / 32;
-                const int el = 16 * half + 4 * g;  // element of q[0]
-                if (a.act_codes)
-                    *reinterpret_cast<uint32_t *>(a.act_codes + blk * 32 + el) =
-                        (uint32_t)(q[0] & 0xff) | ((uint32_t)(q[1] & 0xff) << 8) | ((uint32_t)(q[2] & 0xff) << 16) |
-                        ((uint32_t)(q[3] & 0xff) << 24);
+                if (a.act_codes) *reinterpret_cast<uint32_t *>(a.act_codes + blk * 32 + el0) = qw;
+                if (a.act_btab) {
+                    const uint32_t lo = (g >> 1) ? qp : qw, hi = (g >> 1) ? qw : qp;  // elements j and j + 16
+                    const int r0 = 2 * (g >> 1);
+                    uint32_t dw[2];
+#pragma unroll
+                    for (int k = 0; k < 2; k++) {
+                        const int ql = (int8_t)(lo >> (8 * (r0 + k))), qh = (int8_t)(hi >> (8 * (r0 + k)));
+                        dw[k] = (__float_as_uint((float)ql) >> 16) | (__float_as_uint((float)qh) & 0xFFFF0000u);
+                    }
+                    *reinterpret_cast<uint2 *>(a.act_btab + blk * 16 + (el0 & 15) + r0) = make_uint2(dw[0], dw[1]);
+                }
                 if (half == 0 && g == 0) {
                     if (a.act_scales) a.act_scales[blk] = f16_bits_to_f32(dh);
                     if (a.act_blocks34) {
@@ -532,20 +635,16 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
                 }
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
-                    // element 16*half + 4g + r: nibble position 2*(4g + r) + half
-                    const int p = 2 * (4 * g + r) + half;
+                    const int q = (int8_t)(qw >> (8 * r));
+                    // element el: nibble position 2 * (el & 15) + (el >> 4)
+                    const int p = 2 * ((el0 + r) & 15) + (el0 >> 4);
                     if (a.act_mxtab) {
-                        a.act_mxtab[blk * 64 + p] = (uint8_t)e4m3_small(q[r] >> 4);
-                        a.act_mxtab[blk * 64 + 32 + p] = (uint8_t)e4m3_small(q[r] & 15);
+                        a.act_mxtab[blk * 64 + p] = (uint8_t)e4m3_small(q >> 4);
+                        a.act_mxtab[blk * 64 + 32 + p] = (uint8_t)e4m3_small(q & 15);
                     }
-                    if (a.act_btab)
-                        reinterpret_cast<uint16_t *>(a.act_btab + blk * 16)[2 * (4 * g + r) + half] =
-                            (uint16_t)(__float_as_uint((float)q[r]) >> 16);
-                    if (a.act_blocks34) a.act_blocks34[blk * kQ80Block + 2 + el + r] = (uint8_t)q[r];
+                    if (a.act_blocks34) a.act_blocks34[blk * kQ80Block + 2 + el0 + r] = (uint8_t)q;
                 }
             }
-            // the partner wave has read this wave's s_amax before the next item writes it
-            stage_barrier();
         }
     }
 }
