@@ -435,7 +435,7 @@ MoELayout moe_layout(const spt_ctx *ctx, const MoEDims &m, bool act_tap, size_t 
     L.o_ids = c.take(n * 4), L.o_w = c.take(n * 4), L.o_cnt = c.take(E * 4), L.o_off = c.take((E + 1) * 4);
     L.o_list = c.take(n * 4), L.o_act_list = c.take(E * 4), L.o_na = c.take(4);
     L.o_gv = c.take(E * 4), L.o_gvn = c.take(4), L.o_gvp = c.take((E + 1) * 4);
-    L.o_gm = c.take(E * 4), L.o_gmn = c.take(4), L.o_gmt = c.take((E + 1) * 4);
+    L.o_gm = c.take(E * 4), L.o_gmn = c.take(12), L.o_gmt = c.take((E + 1) * 4);  // gm_n, then the two claim counters
     L.o_act = c.take(act_tap ? n * d * 4 : 0), L.o_ac = c.take(n * d), L.o_as = c.take(n * nbd * 4);
     L.o_am = c.take(n * nbd * 64);
     L.o_ab = c.take(L.use_gemm ? n * nbd * 64 : 0);
@@ -475,6 +475,7 @@ int run_moe_at(spt_ctx *ctx, const spt_moe_layer *lw, const float *x, float *out
     so.gv_pass_off = (int32_t *)(S + L.o_gvp);
     so.gm_active = (int32_t *)(S + L.o_gm);
     so.gm_n = (int32_t *)(S + L.o_gmn);
+    so.gm_claim = (int32_t *)(S + L.o_gmn) + 1;
     so.gm_tile_off = (int32_t *)(S + L.o_gmt);
     hipStream_t s = ctx->stream;
 
@@ -620,6 +621,7 @@ int run_moe_at(spt_ctx *ctx, const spt_moe_layer *lw, const float *x, float *out
         gg.codes = xc;
         gg.gm_active = so.gm_active;
         gg.gm_n = so.gm_n;
+        gg.claim = so.gm_claim;
         gg.gm_tile_off = so.gm_tile_off;
         gg.offsets = so.offsets;
         gg.list = so.list;
@@ -672,6 +674,7 @@ int run_moe_at(spt_ctx *ctx, const spt_moe_layer *lw, const float *x, float *out
         gd.codes = ac;
         gd.gm_active = so.gm_active;
         gd.gm_n = so.gm_n;
+        gd.claim = so.gm_claim + 1;
         gd.gm_tile_off = so.gm_tile_off;
         gd.offsets = so.offsets;
         gd.list = so.list;

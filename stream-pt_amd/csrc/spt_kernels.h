@@ -38,9 +38,10 @@ struct SelectOut {
     int32_t *gv_active;    // [E] GEMV experts, ascending
     int32_t *gv_n;
     int32_t *gv_pass_off;  // [E+1] prefix over GEMV experts of ceil(count / kGemvTokens)
-    int32_t *gm_active;    // [E] GEMM experts, ascending
+    int32_t *gm_active;    // [E] GEMM experts, by descending count (equal counts ascending)
     int32_t *gm_n;
     int32_t *gm_tile_off;  // [E+1] prefix over GEMM experts of ceil(count / kGemmTokens)
+    int32_t *gm_claim;     // [2] work-item counters of the two GEMM launches (zeroed)
 };
 
 // Optional Q8_0 outputs of a quantized activation (see write_q8_block);
@@ -134,6 +135,7 @@ struct MxGemmArgs {
     const int32_t *gm_active;
     const int32_t *gm_n;
     const int32_t *gm_tile_off;
+    int32_t *claim;          // work-item counter, zero at launch (items past the first G are claimed)
     const int32_t *offsets;
     const int32_t *list;
     int topk;

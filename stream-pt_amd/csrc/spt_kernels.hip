@@ -129,6 +129,7 @@ constexpr int kSelWords = kSelChunk / 32;
 
 __device__ void pack_lists(int n, int E, const SelectOut &o, const int32_t *s_ids, const float *s_w,
                            int32_t *s_cnt, int32_t *s_off, int32_t *s_run, uint32_t *s_bits) {
+    __shared__ int s_gemm_on;
     const int tid = threadIdx.x;
     for (int i = tid; i < E; i += blockDim.x) {
         s_cnt[i] = 0;
@@ -139,9 +140,9 @@ __device__ void pack_lists(int n, int E, const SelectOut &o, const int32_t *s_id
         if (!(s_w[i] <= 0.0f)) atomicAdd(&s_cnt[s_ids[i]], 1);
     __syncthreads();
     if (tid < 64) {
-        // offsets (scan of counts), the active list, and the GEMV and GEMM
-        // expert lists with their prefixes (passes of kGemvTokens, tiles of
-        // kGemmTokens) in ascending expert order
+        // offsets (scan of counts), the active list, and the GEMV expert
+        // list with its prefix (passes of kGemvTokens) in ascending expert
+        // order; the GEMM experts' count and tiles (ordered below)
         int pos = 0, na = 0, nv = 0, nm = 0, npass = 0, ntile = 0;
         const uint64_t below = (1ull << tid) - 1ull;
         // GEMM work items the threshold would give
@@ -169,11 +170,6 @@ __device__ void pack_lists(int n, int E, const SelectOut &o, const int32_t *s_id
                     o.gv_active[r] = e;
                     o.gv_pass_off[r] = npass + pincl - np;
                 }
-                if (big) {
-                    const int r = nm + __builtin_popcountll(actm & below);
-                    o.gm_active[r] = e;
-                    o.gm_tile_off[r] = ntile + tincl - ntl;
-                }
             }
             pos += lane63(incl);
             npass += lane63(pincl);
@@ -190,6 +186,32 @@ __device__ void pack_lists(int n, int E, const SelectOut &o, const int32_t *s_id
             o.gv_pass_off[nv] = npass;
             *o.gm_n = nm;
             o.gm_tile_off[nm] = ntile;
+            if (o.gm_claim) {
+                o.gm_claim[0] = 0;
+                o.gm_claim[1] = 0;
+            }
+            s_gemm_on = gemm_on;
+        }
+    }
+    // The GEMM experts by descending count (equal counts by ascending id), so
+    // the GEMM's work items, claimed in order by workgroups as they free up,
+    // end with the smallest: an expert's rank and tile prefix count the GEMM
+    // experts ordered before it.
+    __syncthreads();
+    if (s_gemm_on) {
+        for (int e = tid; e < E; e += blockDim.x) {
+            const int c = s_cnt[e];
+            if (!(c > 0 && c >= o.gemm_min)) continue;
+            int rank = 0, pre = 0;
+            for (int f = 0; f < E; f++) {
+                const int cf = s_cnt[f];
+                if (cf > 0 && cf >= o.gemm_min && (cf > c || (cf == c && f < e))) {
+                    rank++;
+                    pre += (cf + kGemmTokens - 1) / kGemmTokens;
+                }
+            }
+            o.gm_active[rank] = e;
+            o.gm_tile_off[rank] = pre;
         }
     }
     for (int p0 = 0; p0 < n; p0 += kSelChunk) {

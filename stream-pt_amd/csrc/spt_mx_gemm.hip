@@ -44,8 +44,6 @@ constexpr int kThreads = 64 * kWaves;
 constexpr int kBM = 256;               // weight rows per work item (gate/up: 128 gate + 128 up)
 constexpr int kBN = kGemmTokens;       // list entries per work item
 constexpr int kSeg = 4;                // 32-element blocks per K segment (68 bytes of a row)
-constexpr int kStages = 3;             // LDS stages: two segments in flight while one is multiplied
-constexpr int kAhead = kStages - 1;    // segments issued ahead of the one multiplied
 // A stage: row r's window (the segment's bytes from the 16-byte boundary at
 // or below its first byte) in 6 slots of 16 bytes (16-byte aligned loads:
 // a load crossing the end of the descriptor's range would read zeros for all
@@ -56,22 +54,40 @@ constexpr int kAPieces = (kSeg * kMxBlock + 15 + 15) / 16;
 constexpr int kASlots = kAPieces;
 constexpr int kARow = 16 * kASlots;
 constexpr int kAInstr = kBM * kASlots / 64;
-// B stage: per entry 4 * kSeg slots of 16 bytes (kSeg blocks x 4 quarters of
-// the bf16 code table); quarter piece p of entry t sits in slot p ^ (t & 15),
-// so the 16 entries of an MFMA fragment read 16 different bank groups.
+// B: per entry 4 * kSeg slots of 16 bytes (kSeg blocks x 4 quarters of the
+// bf16 code table); quarter piece p of entry t sits in slot p ^ (t & 15), so
+// the 16 entries of an MFMA fragment read 16 different bank groups.  A stage
+// holds the B slots of the item's token fragments only, then d_x
+// [entry][kSeg] and the slots of the d_x loads without entries, so items
+// with fewer fragments have smaller stages and keep more segments in flight.
 constexpr int kOffB = kBM * kARow;
-constexpr int kOffD = kOffB + kBN * kSeg * 64;  // d_x [entry][kSeg], then the waves without d_x entries
-constexpr int kStageBytes = kOffD + 64 * kWaves * 4;
+constexpr int kBFrag = 16 * kSeg * 64;            // B bytes of one token fragment
+constexpr int kDBytes = 64 * 8 * 4;               // d_x region: one 256-byte load per wave
+constexpr int kLdsDynamic = 155648;               // dynamic LDS of a workgroup (stages)
+constexpr int kMaxStages = 5;
 constexpr int kEMin = 4, kEMax = 240;
 constexpr int kXcds = 8;  // accelerator complex dies of an MI355X
 constexpr uint32_t kOOR = 0x80000000u;  // buffer offset past every range: reads zero
 static_assert(kSeg * kMxBlock + 15 <= 16 * kAPieces, "A window");
-static_assert(kAInstr % kWaves == 0 && kBN * kSeg * 4 % kThreads == 0, "stage loads");
+static_assert(kAInstr % kWaves == 0, "stage loads");
 static_assert(kBM / 2 * kASlots % 64 == 0, "gate rows fill whole A loads");
-static_assert(kBN * kSeg <= 64 * kWaves && 4 * kSeg <= 16, "one d_x load per wave; B swizzle within 16 slots");
-constexpr int kALoads = kAInstr / kWaves;           // 3
-constexpr int kBLoads = kBN * kSeg * 4 / kThreads;  // 2
-constexpr int kSegLoads = kALoads + kBLoads + 1;    // DMA loads per wave and segment
+static_assert(kBN * kSeg <= 64 * kWaves && 4 * kSeg <= 16 && 64 * kWaves * 4 == kDBytes,
+              "one d_x load per wave; B swizzle within 16 slots");
+constexpr int kALoads = kAInstr / kWaves;  // 3
+
+// Stage geometry of an item with NTF token fragments: the d_x offset, the
+// stage size, the number of stages and the DMA loads per wave and segment
+// (A x3, B x NTF/2 -- a wave with an odd NTF's extra load has one more -- and
+// d_x x1).
+template <int NTF>
+struct Geo {
+    static constexpr int kOffD = kOffB + NTF * kBFrag;
+    static constexpr int kBytes = kOffD + kDBytes;
+    static constexpr int kStages = kLdsDynamic / kBytes < kMaxStages ? kLdsDynamic / kBytes : kMaxStages;
+    static constexpr int kAhead = kStages - 1;  // segments in flight while one is multiplied
+    static constexpr int kLoadsMin = kALoads + NTF / 2 + 1;
+    static_assert(kStages >= 3 && kStages * kBytes <= kLdsDynamic, "stages");
+};
 
 
 // Integer-decode dot of one weight row with one entry's Q8_0 row (the
@@ -115,12 +131,42 @@ __device__ inline void stage_barrier() {
     asm volatile("" ::: "memory");
 }
 
-// Four bytes of the stage at byte offset o (any alignment): two aligned
-// dwords and a byte shift (an unaligned LDS dword read returns the same
-// bytes but is far slower).
-__device__ __attribute__((always_inline)) inline uint32_t nibble_word(const uint8_t *st, uint32_t o) {
-    const uint32_t *pw = reinterpret_cast<const uint32_t *>(st + (o & ~3u));
-    return __builtin_amdgcn_alignbyte(pw[1], pw[0], o & 3u);
+typedef __attribute__((address_space(3))) const uint8_t lds_cu8;
+typedef __attribute__((address_space(3))) const uint32_t lds_cu32;
+
+// A segment's operands in one stage, as LDS pointers computed once per
+// segment (every block's read is then a constant offset from them):
+// a[rf] = this lane's row window of fragment rf (the E8M0 byte of block j at
+// a[rf][17j]); n[rf] = a[rf] + 1 + 4g (the nibble bytes of block j for lane
+// group g at n[rf] + 17j); b[j] = quarter g of block j of this lane's entry
+// in token fragment 0 (fragment tf at + tf * 16 * kSeg * 64); d = d_x of this
+// lane's entry, block 0 (fragment tf, block j at + tf * 16 * kSeg + j).
+struct SegView {
+    lds_cu8 *a[2];
+    lds_cu8 *n[2];
+    lds_cu8 *b[kSeg];
+    __attribute__((address_space(3))) const float *d;
+};
+
+// Four bytes at LDS address p (any alignment): two aligned dwords and a byte
+// shift (an unaligned LDS dword read returns the same bytes but is far
+// slower; the shift operand's low two bits are the address's).
+__device__ __attribute__((always_inline)) inline uint32_t nibble_word(lds_cu8 *p) {
+    const uint32_t o = (uint32_t)reinterpret_cast<uintptr_t>(p);
+    lds_cu32 *pw = reinterpret_cast<lds_cu32 *>((uintptr_t)(o & ~3u));
+    return __builtin_amdgcn_alignbyte(pw[1], pw[0], o);
+}
+
+// A fragment of 16 weight rows x 32 K of block j as bf16 (the E2M1 nibbles
+// scaled by 2^(e-127)), and the block's E8M0.
+__device__ __attribute__((always_inline)) inline bf16x8 decode_a(uint32_t w4, uint32_t eb) {
+    const float sc = __uint_as_float(eb << 23);
+    u32x4 av;
+    av.x = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w4, sc, 0));
+    av.y = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w4, sc, 1));
+    av.z = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w4, sc, 2));
+    av.w = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w4, sc, 3));
+    return __builtin_bit_cast(bf16x8, av);
 }
 
 // Blocks [J0, J1) of a full segment with NTF token fragments, straight-line:
@@ -130,10 +176,8 @@ __device__ __attribute__((always_inline)) inline uint32_t nibble_word(const uint
 // segment is two such halves, so the rest of the next segment's loads can
 // go out between them without stretching the live ranges of either.
 template <int NTF, int J0, int J1>
-__device__ __attribute__((always_inline)) inline void seg_blocks(const uint8_t *st, const uint32_t (&a_img)[2],
-                                                                 const uint32_t (&b_lane)[kSeg], int g, int i16,
-                                                                 float (&acc)[2][4][4], uint32_t (&emin)[2],
-                                                                 uint32_t (&emax)[2]) {
+__device__ __attribute__((always_inline)) inline void seg_blocks(const SegView &v, float (&acc)[2][4][4],
+                                                                 uint32_t (&emin)[2], uint32_t (&emax)[2]) {
     constexpr int NJ = J1 - J0;
     uint32_t eb[NJ][2], w4[NJ][2];
 #pragma unroll
@@ -141,8 +185,8 @@ __device__ __attribute__((always_inline)) inline void seg_blocks(const uint8_t *
 #pragma unroll
         for (int rf = 0; rf < 2; rf++) {
             const int j = J0 + jj;
-            eb[jj][rf] = st[a_img[rf] + 17 * j];
-            w4[jj][rf] = nibble_word(st, a_img[rf] + 17u * (uint32_t)j + 1u + 4u * (uint32_t)g);
+            eb[jj][rf] = v.a[rf][17 * j];
+            w4[jj][rf] = nibble_word(v.n[rf] + 17 * j);
         }
     bf16x8 Bv[2][NTF];
     float dx[2][NTF];
@@ -150,8 +194,9 @@ __device__ __attribute__((always_inline)) inline void seg_blocks(const uint8_t *
         const int j = J0 + jj;
 #pragma unroll
         for (int tf = 0; tf < NTF; tf++) {
-            Bv[jj & 1][tf] = *reinterpret_cast<const bf16x8 *>(st + kOffB + tf * (16 * kSeg * 64) + b_lane[j]);
-            dx[jj & 1][tf] = *reinterpret_cast<const float *>(st + kOffD + ((16 * tf + i16) * kSeg + j) * 4);
+            Bv[jj & 1][tf] = *reinterpret_cast<__attribute__((address_space(3))) const bf16x8 *>(
+                v.b[j] + tf * (16 * kSeg * 64));
+            dx[jj & 1][tf] = v.d[tf * 16 * kSeg + j];
         }
     };
     load_b(0);
@@ -161,13 +206,7 @@ __device__ __attribute__((always_inline)) inline void seg_blocks(const uint8_t *
         v4f D[2][NTF];
 #pragma unroll
         for (int rf = 0; rf < 2; rf++) {
-            const float sc = __uint_as_float(eb[jj][rf] << 23);
-            u32x4 av;
-            av.x = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w4[jj][rf], sc, 0));
-            av.y = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w4[jj][rf], sc, 1));
-            av.z = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w4[jj][rf], sc, 2));
-            av.w = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w4[jj][rf], sc, 3));
-            const bf16x8 A = __builtin_bit_cast(bf16x8, av);
+            const bf16x8 A = decode_a(w4[jj][rf], eb[jj][rf]);
 #pragma unroll
             for (int tf = 0; tf < NTF; tf++)
                 D[rf][tf] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, Bv[jj & 1][tf], v4f{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
@@ -191,31 +230,23 @@ static_assert(kSeg % 4 == 0, "seg_blocks' halves and exponent reduction");
 
 // The last segment when it holds jn < kSeg blocks.
 template <int NTF>
-__device__ __attribute__((always_inline)) inline void seg_part(const uint8_t *st, const uint32_t (&a_img)[2],
-                                                               const uint32_t (&b_lane)[kSeg], int g, int i16, int jn,
-                                                               float (&acc)[2][4][4], uint32_t (&emin)[2],
-                                                               uint32_t (&emax)[2]) {
+__device__ __attribute__((always_inline)) inline void seg_part(const SegView &v, int jn, float (&acc)[2][4][4],
+                                                               uint32_t (&emin)[2], uint32_t (&emax)[2]) {
     for (int j = 0; j < jn; j++) {
         bf16x8 A[2];
 #pragma unroll
         for (int rf = 0; rf < 2; rf++) {
-            const uint32_t eb = st[a_img[rf] + 17 * j];
-            const uint32_t w4 = nibble_word(st, a_img[rf] + 17u * (uint32_t)j + 1u + 4u * (uint32_t)g);
+            const uint32_t eb = v.a[rf][17 * j];
+            const uint32_t w4 = nibble_word(v.n[rf] + 17 * j);
             emin[rf] = min(emin[rf], eb);
             emax[rf] = max(emax[rf], eb);
-            const float sc = __uint_as_float(eb << 23);
-            u32x4 av;
-            av.x = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w4, sc, 0));
-            av.y = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w4, sc, 1));
-            av.z = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w4, sc, 2));
-            av.w = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w4, sc, 3));
-            A[rf] = __builtin_bit_cast(bf16x8, av);
+            A[rf] = decode_a(w4, eb);
         }
 #pragma unroll
         for (int tf = 0; tf < NTF; tf++) {
-            const uint32_t bl = (uint32_t)i16 * (kSeg * 64) + 16u * (uint32_t)((4 * j + g) ^ i16);
-            const bf16x8 B = *reinterpret_cast<const bf16x8 *>(st + kOffB + tf * (16 * kSeg * 64) + bl);
-            const float dx = *reinterpret_cast<const float *>(st + kOffD + ((16 * tf + i16) * kSeg + j) * 4);
+            const bf16x8 B =
+                *reinterpret_cast<__attribute__((address_space(3))) const bf16x8 *>(v.b[j] + tf * (16 * kSeg * 64));
+            const float dx = v.d[tf * 16 * kSeg + j];
 #pragma unroll
             for (int rf = 0; rf < 2; rf++) {
                 const v4f D = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[rf], B, v4f{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
@@ -242,13 +273,13 @@ __device__ __attribute__((always_inline)) inline void seg_part(const uint8_t *st
 // wave w rows 32w .. 32w+31.  Every wave takes all 64 entries: 2 x 4 MFMA
 // tiles per block.
 //
-// The K loop runs over segments of kSeg blocks through kStages LDS stages
-// filled by LDS DMA loads (global/buffer -> LDS, no registers): segments s+1
-// and s+2 are in flight while segment s is multiplied.  Segments are
-// numbered across the workgroup's items, so the first segments of the next
-// item go to the stages the current item's last segment does not use, and
-// their loads can be issued without waiting for the slower waves to finish
-// that last segment.
+// The K loop runs over segments of kSeg blocks through LDS stages filled by
+// LDS DMA loads (global/buffer -> LDS, no registers): kAhead segments are
+// in flight while one is multiplied.  A stage holds the B codes of the
+// item's token fragments only, so an item with one fragment has five stages
+// (four segments in flight), with two or three fragments four, with four
+// three: the bytes in flight per CU, which set the rate at which its loads
+// arrive, stay near the LDS size.
 template <int MODE>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void k_mx_gemm(MxGemmArgs a) {
     extern __shared__ __align__(16) uint8_t lds[];
@@ -257,6 +288,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
     // gate rows then up rows) and the item's list entries (-1 past its end)
     __shared__ __align__(16) float s_bias[2][kBM];
     __shared__ int s_ent[2][kBN];
+    __shared__ int s_next[2];  // per item parity: the workgroup's next item
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -279,16 +311,18 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
     // a scalar offset)
     const u32x4v rs_b = rsrc_words(a.btab, (uint32_t)(a.tab_rows * (uint64_t)nb * 64u));
     const u32x4v rs_d = rsrc_words(a.scales, (uint32_t)(a.tab_rows * (uint64_t)nb * 4u));
-    // per lane: B slot offsets of quarter g of block j for this lane's entry
+    // per lane: stage offsets of the B slot of quarter g of block j for this lane's entry
     uint32_t b_lane[kSeg];
 #pragma unroll
-    for (int j = 0; j < kSeg; j++) b_lane[j] = (uint32_t)i16 * (kSeg * 64) + 16u * (uint32_t)((4 * j + g) ^ i16);
+    for (int j = 0; j < kSeg; j++) b_lane[j] = kOffB + (uint32_t)i16 * (kSeg * 64) + 16u * (uint32_t)((4 * j + g) ^ i16);
     typedef __attribute__((address_space(3))) uint8_t lds_u8;
     const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>((lds_u8 *)lds);
 
-    int seg0 = 0;   // stage of the item's first segment
-    int parity = 0; // item parity (s_bias / s_ent buffer)
-    for (int it = vb; it < total; it += G, seg0 = (seg0 + nseg) % kStages, parity ^= 1) {
+    // The first item of workgroup b is vb; later ones are claimed from the
+    // launch's counter (items G, G+1, ... in order, largest experts first),
+    // so the workgroups finish together.
+    int parity = 0;  // item parity (s_bias / s_ent / s_next buffer)
+    for (int it = vb; it < total; parity ^= 1) {
         // item -> slot: the number of slots i >= 1 whose first item is at or
         // below it (gm_tile_off is increasing), 64 slots per ballot
         int slot = 0;
@@ -334,9 +368,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
             a_pos[k] = ((MODE == kGateUp && r >= kBM / 2) ? le1 : le0) + (uint32_t)(a_ok[k] ? row : 0) * row_bytes +
                        16u * (uint32_t)pc;
         }
-        uint32_t b_off[kBLoads];
+        uint32_t b_off[2];
 #pragma unroll
-        for (int k = 0; k < kBLoads; k++) {
+        for (int k = 0; k < 2; k++) {
             const int q = tid + kThreads * k, t = q / (4 * kSeg), piece = (q % (4 * kSeg)) ^ (t & 15);
             b_off[k] = kOOR;
             if (t < nt) {
@@ -354,10 +388,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
                 d_off = ((uint32_t)ar * (uint32_t)nb + (uint32_t)j) * 4u;
             }
         }
-        // this thread's share of the item's bias and entries (staged in LDS
-        // once segment 0's loads have landed)
+        // this thread's share of the item's bias and entries, and the next
+        // item (staged in LDS once segment 0's loads have landed)
         float bias_v = 0.0f;
-        int ent_v = -1;
+        int ent_v = -1, next_v = 0;
+        if (tid == 0) next_v = G + atomicAdd(a.claim, 1);
         if (tid < kBM) {
             const int m = MODE == kGateUp ? tid / (kBM / 2) : 0;
             const int row = MODE == kGateUp ? u * (kBM / 2) + (tid & (kBM / 2 - 1)) : u * kBM + tid;
@@ -365,17 +400,15 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
         } else if (tid < kBM + kBN) {
             if (tid - kBM < nt) ent_v = a.list[begin + tid - kBM];
         }
-        // kSegLoads DMA loads per wave and stage (A x3, B x2, d_x x1), in
+        // The DMA loads of segment s into the stage at LDS byte address st, in
         // two parts: the weights and d_x, then the B codes (a wave stalls at
         // a load's issue while its CU's memory queue is full; the second part
         // goes out half a segment later, when the first has drained).  The
         // A window of segment s starts at the 16-byte boundary at or below
         // the row's byte pos + 68s (a_pos holds pos + 16 * piece).  Lanes
         // whose entries are past nt read nothing (zeros); the d_x loads of
-        // waves 4-7 hold no entries and fill the stage's spare d_x slots.
-        auto stage_of = [&](int s) { return lds0 + (uint32_t)((seg0 + s) % kStages) * kStageBytes; };
-        auto issue_a = [&](int s) {
-            const uint32_t st = stage_of(s);
+        // the waves past the item's entries fill the stage's spare d_x slots.
+        auto issue_a = [&](int s, uint32_t st, uint32_t off_d) {
 #pragma unroll
             for (int k = 0; k < kALoads; k++) {
                 const int i = wave + kWaves * k;
@@ -384,14 +417,22 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
                 dma16((MODE == kGateUp && i >= kAInstr / 2) ? rs1 : rs0, st + 16u * 64u * (uint32_t)i,
                       a_ok[k] ? (pos & ~15u) : kOOR, 0u);
             }
-            dma4(rs_d, st + kOffD + 256u * wave, d_off, (uint32_t)(kSeg * 4) * (uint32_t)s);
+            dma4(rs_d, st + off_d + 256u * wave, d_off, (uint32_t)(kSeg * 4) * (uint32_t)s);
         };
-        auto issue_b = [&](int s) {
-            const uint32_t st = stage_of(s);
+        // B load k of wave w covers entries 32k + 4w .. 32k + 4w + 3: the item's
+        // NTF fragments take loads k < NTF / 2 of every wave, and with an odd
+        // NTF load NTF / 2 of waves 0-3
+        auto issue_b = [&](auto ntf_c, int s, uint32_t st) {
+            constexpr int NTF = decltype(ntf_c)::value;
 #pragma unroll
-            for (int k = 0; k < kBLoads; k++)
+            for (int k = 0; k < NTF / 2; k++)
                 dma16_other_stage(rs_b, st + kOffB + 16u * (64 * wave + kThreads * k), b_off[k],
                                   (uint32_t)(kSeg * 64) * (uint32_t)s);
+            if constexpr (NTF % 2 == 1) {
+                if (wave < 4)
+                    dma16_other_stage(rs_b, st + kOffB + 16u * (64 * wave + kThreads * (NTF / 2)), b_off[NTF / 2],
+                                      (uint32_t)(kSeg * 64) * (uint32_t)s);
+            }
         };
 
         // this lane's A rows: LDS row and matrix byte position (the window of
@@ -416,76 +457,87 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
                 for (int r = 0; r < 4; r++) acc[rf][tf][r] = 0.0f;
         uint32_t emin[2] = {255u, 255u}, emax[2] = {0u, 0u};
 
-        // segment 0's loads, the bias and entries into LDS (waiting for
-        // their loads waits for segment 0's too, which the K loop would),
-        // then the loads of the other segments issued ahead
-        issue_a(0);
-        issue_b(0);
-        asm volatile("" ::: "memory");
-        if (tid < kBM)
-            s_bias[parity][tid] = bias_v;
-        else if (tid < kBM + kBN)
-            s_ent[parity][tid - kBM] = ent_v;
-        asm volatile("" ::: "memory");
-        for (int s = 1; s < kAhead && s < nseg; s++) {
-            issue_a(s);
-            issue_b(s);
-        }
-
         // The K loop, instantiated per number of token fragments (so the
-        // accumulators stay in place through it): the segments whose loads
-        // issue a later segment's in a loop of its own (one straight-line
-        // body, so the accumulators keep their registers across iterations),
-        // then the last kAhead segments.
+        // accumulators stay in place through it, and the stages have that
+        // many fragments' B slots): segment s in stage s % kStages of the
+        // item's geometry; the loads of segments 0 .. kAhead-1 first, then
+        // the segments whose loads issue a later segment's in a loop of
+        // their own (one straight-line body, so the accumulators keep their
+        // registers across iterations), then the last kAhead segments.
         auto kloop = [&](auto ntf_c) {
             constexpr int NTF = decltype(ntf_c)::value;
-            static_assert(kAhead == 2, "the waits below keep one segment in flight");
-            auto a_img_of = [&](int s, uint32_t(&a_img)[2]) {
+            typedef Geo<NTF> G;
+            auto st_of = [&](int stage) { return lds0 + (uint32_t)stage * (uint32_t)G::kBytes; };
+            // segment 0's loads, the bias and entries into LDS (waiting for
+            // their loads waits for segment 0's too, which the K loop would),
+            // then the loads of the other segments issued ahead
+            issue_a(0, st_of(0), G::kOffD);
+            issue_b(ntf_c, 0, st_of(0));
+            asm volatile("" ::: "memory");
+            if (tid < kBM)
+                s_bias[parity][tid] = bias_v;
+            else if (tid < kBM + kBN)
+                s_ent[parity][tid - kBM] = ent_v;
+            if (tid == 0) s_next[parity] = next_v;
+            asm volatile("" ::: "memory");
+            for (int q = 1; q < G::kAhead && q < nseg; q++) {
+                issue_a(q, st_of(q), G::kOffD);
+                issue_b(ntf_c, q, st_of(q));
+            }
+            auto view_of = [&](int s, int stage) {
+                SegView v;
+                lds_cu8 *st = reinterpret_cast<lds_cu8 *>((uintptr_t)st_of(stage));
 #pragma unroll
-                for (int rf = 0; rf < 2; rf++)
-                    a_img[rf] = l_row[rf] + ((l_pos[rf] + (uint32_t)(kSeg * kMxBlock) * (uint32_t)s) & 15u);
+                for (int rf = 0; rf < 2; rf++) {
+                    v.a[rf] = st + l_row[rf] + ((l_pos[rf] + (uint32_t)(kSeg * kMxBlock) * (uint32_t)s) & 15u);
+                    v.n[rf] = v.a[rf] + 1 + 4 * g;
+                }
+#pragma unroll
+                for (int j = 0; j < kSeg; j++) v.b[j] = st + b_lane[j];
+                v.d = reinterpret_cast<__attribute__((address_space(3))) const float *>(st + G::kOffD) + i16 * kSeg;
+                return v;
             };
-            const uint8_t *const st_base = lds;
-            int s = 0;
-            for (; s + kAhead < nseg; s++) {
-                // this wave's loads of segment s have landed (those of s+1,
-                // issued after them, may not have); after the barrier every
-                // wave's have, and every wave is done with segment s-1, whose
-                // stage segment s+2 reuses
-                asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(kSegLoads) : "memory");
+            int s = 0, cur = 0;  // segment, its stage
+            for (; s + G::kAhead < nseg; s++) {
+                // this wave's loads of segment s have landed (those of the
+                // kAhead-1 segments issued after them may not have: every
+                // wave issues at least kLoadsMin loads per segment); after
+                // the barrier every wave's have, and every wave is done with
+                // segment s-1, whose stage segment s + kAhead reuses
+                asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"((G::kAhead - 1) * G::kLoadsMin) : "memory");
                 stage_barrier();
-                issue_a(s + kAhead);
-                const uint8_t *st = st_base + (size_t)((seg0 + s) % kStages) * kStageBytes;
-                uint32_t a_img[2];
-                a_img_of(s, a_img);
-                seg_blocks<NTF, 0, kSeg / 2>(st, a_img, b_lane, g, i16, acc, emin, emax);
-                issue_b(s + kAhead);
-                seg_blocks<NTF, kSeg / 2, kSeg>(st, a_img, b_lane, g, i16, acc, emin, emax);
+                const int nxt = cur == 0 ? G::kStages - 1 : cur - 1;
+                issue_a(s + G::kAhead, st_of(nxt), G::kOffD);
+                const SegView v = view_of(s, cur);
+                seg_blocks<NTF, 0, kSeg / 2>(v, acc, emin, emax);
+                issue_b(ntf_c, s + G::kAhead, st_of(nxt));
+                seg_blocks<NTF, kSeg / 2, kSeg>(v, acc, emin, emax);
+                cur = cur + 1 == G::kStages ? 0 : cur + 1;
             }
-            // the segment before the last (full: only the last can be partial)
-            if (s + 1 < nseg) {
-                asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(kSegLoads) : "memory");
+            // the last kAhead segments (or fewer): every load is issued, and
+            // only the last segment can be partial
+            for (; s < nseg; s++) {
+                const int later = nseg - 1 - s;  // segments in flight after s
+                if (later >= 3)
+                    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(3 * G::kLoadsMin) : "memory");
+                else if (later == 2)
+                    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(2 * G::kLoadsMin) : "memory");
+                else if (later == 1)
+                    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(G::kLoadsMin) : "memory");
+                else
+                    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
                 stage_barrier();
-                const uint8_t *st = st_base + (size_t)((seg0 + s) % kStages) * kStageBytes;
-                uint32_t a_img[2];
-                a_img_of(s, a_img);
-                seg_blocks<NTF, 0, kSeg / 2>(st, a_img, b_lane, g, i16, acc, emin, emax);
-                seg_blocks<NTF, kSeg / 2, kSeg>(st, a_img, b_lane, g, i16, acc, emin, emax);
-                s++;
+                const SegView v = view_of(s, cur);
+                const int jn = nb - kSeg * s;
+                if (jn >= kSeg) {
+                    seg_blocks<NTF, 0, kSeg / 2>(v, acc, emin, emax);
+                    seg_blocks<NTF, kSeg / 2, kSeg>(v, acc, emin, emax);
+                } else {
+                    seg_part<NTF>(v, jn, acc, emin, emax);
+                }
+                cur = cur + 1 == G::kStages ? 0 : cur + 1;
             }
-            // the last segment
-            asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
-            stage_barrier();
-            const uint8_t *st = st_base + (size_t)((seg0 + s) % kStages) * kStageBytes;
-            uint32_t a_img[2];
-            a_img_of(s, a_img);
-            const int jn = nb - kSeg * s;
-            if (jn == kSeg) {
-                seg_blocks<NTF, 0, kSeg / 2>(st, a_img, b_lane, g, i16, acc, emin, emax);
-                seg_blocks<NTF, kSeg / 2, kSeg>(st, a_img, b_lane, g, i16, acc, emin, emax);
-            } else {
-                seg_part<NTF>(st, a_img, b_lane, g, i16, jn, acc, emin, emax);
-            }
+            static_assert(G::kAhead <= 4, "the tail's waits cover three later segments");
         };
         if (ntf == 4)
             kloop(std::integral_constant<int, 4>{});
@@ -495,6 +547,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
             kloop(std::integral_constant<int, 2>{});
         else
             kloop(std::integral_constant<int, 1>{});
+        // down: every wave is done with the stages before the next item's
+        // loads (gate/up waits at its epilogue's barrier)
+        if constexpr (MODE == kDown) stage_barrier();
 
         // entries of this lane's token columns
         int ent[4];
@@ -646,12 +701,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
                 }
             }
         }
+        it = s_next[parity];
     }
 }
 
 hipError_t launch_mx_gemm(hipStream_t s, GemvMode mode, const MxGemmArgs &a, int max_items) {
     if (max_items <= 0 || a.rows <= 0 || a.nb <= 0) return hipSuccess;
-    constexpr size_t lds = (size_t)kStages * kStageBytes;
+    constexpr size_t lds = (size_t)kLdsDynamic;
     static const hipError_t attr = [] {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_mx_gemm<kGateUp>),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
