@@ -4,10 +4,10 @@
 // forward.MulQ40BatchInto (forward/q40.go:40-103) for batches large enough
 // that the projection is a contraction: y[t][row] = sum_b float(isum) *
 // (d_w * d_x), with isum = sum (n - 8) * q the exact int32 block sum.  One
-// MFMA per 16 rows x 16 tokens x one block of 32: A = the weight nibbles n
-// (0..15, exact as int8), B = the Q8_0 codes, D = sum n * q exactly, so
-// isum = D - 8 * sum(q) with the per-block code sums of the quantizer; then
-// acc = fma(float(isum), d_w * d_x, acc), the GEMV's arithmetic per block.
+// MFMA per 16 rows x 16 tokens x one block of 32: A = the weight values
+// n - 8 (-8..7 as int8: (n | 0x80) - 8, then ^ 0x80, per byte), B = the Q8_0
+// codes, D = isum exactly; then acc = fma(float(isum), d_w * d_x, acc), the
+// GEMV's arithmetic per block.
 // K order inside a block: lane group g of the MFMA (k = 8g .. 8g+7) takes
 // nibble bytes 2+4g .. 5+4g of the block: low nibbles are elements 4g..4g+3,
 // high nibbles 16+4g..16+4g+3, matched by code dwords g and 4+g.
@@ -37,13 +37,12 @@ constexpr int kARow = 176;        // LDS bytes per staged row (44 dwords: rows o
 constexpr int kBTok = kSeg * 32 + 16;  // LDS bytes per staged token (68 dwords)
 constexpr int kOffB = kTR * kARow;
 constexpr int kOffD = kOffB + kTN * kBTok;  // d_x [token][kSeg]
-constexpr int kOffS = kOffD + kTN * kSeg * 4;  // code sums [token][kSeg]
-constexpr int kStageBytes = kOffS + kTN * kSeg * 4;
+constexpr int kStageBytes = kOffD + kTN * kSeg * 4;
 static_assert(kSeg * kQ40Block + 15 <= 16 * kAPieces && 16 * kAPieces <= kARow, "A window");
 constexpr int kALoads = (kTR * kAPieces + kThreads - 1) / kThreads;  // 3
 constexpr int kBLoads = kTN * kSeg * 2 / kThreads;                    // 4 (16 pieces of 16 B per token)
-constexpr int kSLoads = 2 * kTN * kSeg / kThreads;                    // 4 (d_x and sums, one dword each)
-static_assert(kTN * kSeg * 2 % kThreads == 0 && 2 * kTN * kSeg % kThreads == 0, "stage loads");
+constexpr int kSLoads = kTN * kSeg / kThreads;                        // 2 (d_x, one dword each)
+static_assert(kTN * kSeg * 2 % kThreads == 0 && kTN * kSeg % kThreads == 0, "stage loads");
 
 // Four bytes of the stage at byte offset o (o even: Q4_0 rows are 2-byte
 // aligned): two aligned dwords and a byte shift.
@@ -69,7 +68,6 @@ __device__ __attribute__((always_inline)) inline void q40_blocks(const uint8_t *
         uint32_t dwb[4];
         uint32_t bq[NTF][2];
         float dx[NTF];
-        int s8[NTF];
     };
     auto fetch = [&](int j, Blk &b) {
         b.w4 = word_at(st, L.alead + (uint32_t)j * kQ40Block);
@@ -82,11 +80,13 @@ __device__ __attribute__((always_inline)) inline void q40_blocks(const uint8_t *
             b.bq[tf][0] = bq[L.g];
             b.bq[tf][1] = bq[4 + L.g];
             b.dx[tf] = *reinterpret_cast<const float *>(st + kOffD + 4 * (t * kSeg + j));
-            b.s8[tf] = 8 * *reinterpret_cast<const int32_t *>(st + kOffS + 4 * (t * kSeg + j));
         }
     };
     auto run = [&](const Blk &b) {
-        const long A = (long)(b.w4 & 0x0F0F0F0Fu) | ((long)((b.w4 >> 4) & 0x0F0F0F0Fu) << 32);
+        // per byte: nibble n -> n - 8 as int8
+        const uint32_t lo = (((b.w4 & 0x0F0F0F0Fu) | 0x80808080u) - 0x08080808u) ^ 0x80808080u;
+        const uint32_t hi = ((((b.w4 >> 4) & 0x0F0F0F0Fu) | 0x80808080u) - 0x08080808u) ^ 0x80808080u;
+        const long A = (long)lo | ((long)hi << 32);
         float dw[4];
 #pragma unroll
         for (int r = 0; r < 4; r++) dw[r] = f16_bits_to_f32(b.dwb[r]);
@@ -97,7 +97,7 @@ __device__ __attribute__((always_inline)) inline void q40_blocks(const uint8_t *
 #pragma unroll
         for (int tf = 0; tf < NTF; tf++)
 #pragma unroll
-            for (int r = 0; r < 4; r++) acc[tf][r] = __builtin_fmaf((float)(D[tf][r] - b.s8[tf]), dw[r] * b.dx[tf], acc[tf][r]);
+            for (int r = 0; r < 4; r++) acc[tf][r] = __builtin_fmaf((float)D[tf][r], dw[r] * b.dx[tf], acc[tf][r]);
     };
     if constexpr (JN > 0) {
         Blk cur, nxt;
@@ -107,6 +107,9 @@ __device__ __attribute__((always_inline)) inline void q40_blocks(const uint8_t *
             if (j + 1 < JN) fetch(j + 1, nxt);
             run(cur);
             cur = nxt;
+            // keep the schedule one block deep (hoisting later blocks' reads
+            // runs out of registers)
+            __builtin_amdgcn_sched_barrier(0);
         }
     } else {
         for (int j = 0; j < jn; j++) {
@@ -180,13 +183,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
         }
 #pragma unroll
         for (int k = 0; k < kSLoads; k++) {
-            const int q = tid + kThreads * k, which = q / (kTN * kSeg), e = q % (kTN * kSeg);
+            const int e = tid + kThreads * k;
             const int t = e / kSeg, b = b0 + e % kSeg;
             uint32_t v = 0u;
-            if (t < nt && b < kb1) {
-                const size_t o = (size_t)(t0 + t) * nb + b;
-                v = which == 0 ? __float_as_uint(a.scales[o]) : (uint32_t)a.sumq[o];
-            }
+            if (t < nt && b < kb1) v = __float_as_uint(a.scales[(size_t)(t0 + t) * nb + b]);
             rsx[k] = v;
         }
     };
@@ -201,10 +201,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
             *reinterpret_cast<u32x4 *>(st + kOffB + t * kBTok + 16 * pc) = rb[k];
         }
 #pragma unroll
-        for (int k = 0; k < kSLoads; k++) {
-            const int q = tid + kThreads * k, which = q / (kTN * kSeg), e = q % (kTN * kSeg);
-            *reinterpret_cast<uint32_t *>(st + (which == 0 ? kOffD : kOffS) + 4 * e) = rsx[k];
-        }
+        for (int k = 0; k < kSLoads; k++) *reinterpret_cast<uint32_t *>(st + kOffD + 4 * (tid + kThreads * k)) = rsx[k];
     };
 
     // this lane's A row (MFMA layout: row i16) and D rows (4g .. 4g+3)
@@ -222,18 +219,15 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
 #pragma unroll
         for (int r = 0; r < 4; r++) acc[tf][r] = 0.0f;
 
-    // The K loop, instantiated per number of token fragments.
+    // The K loop, instantiated per number of token fragments: the full
+    // segments in a loop of their own (one straight-line body, so the
+    // accumulators keep their registers), then a last partial segment.
     auto kloop = [&](auto ntf_c) {
         constexpr int NTF = decltype(ntf_c)::value;
-        stage_load(0);
-        stage_store(0);
-        __syncthreads();
-        for (int s = 0; s < nseg; s++) {
-            if (s + 1 < nseg) stage_load(s + 1);
-            const uint8_t *st = lds + (size_t)(s & 1) * kStageBytes;
-            const int b0 = kb0 + s * kSeg, jn = min(kSeg, kb1 - b0);
-            // window offsets of this segment: A row (nibble bytes 2+4g..5+4g
-            // of block j at lead + 18j + 2 + 4g), and the D rows' scales
+        auto lane_of = [&](int s) {
+            // window offsets of segment s: A row (nibble bytes 2+4g..5+4g of
+            // block j at lead + 18j + 2 + 4g), and the D rows' scales
+            const int b0 = kb0 + s * kSeg;
             Q40Lane L;
             L.alead = (uint32_t)arow * kARow + ((apos + (uint32_t)b0 * kQ40Block) & 15u) + 2u + 4u * (uint32_t)g;
 #pragma unroll
@@ -241,10 +235,19 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
                 L.dlead[r] = (uint32_t)(16 * wave + 4 * g + r) * kARow + ((dpos[r] + (uint32_t)b0 * kQ40Block) & 15u);
             L.i16 = i16;
             L.g = g;
+            return L;
+        };
+        stage_load(0);
+        stage_store(0);
+        __syncthreads();
+        for (int s = 0; s < nseg; s++) {
+            if (s + 1 < nseg) stage_load(s + 1);
+            const uint8_t *st = lds + (size_t)(s & 1) * kStageBytes;
+            const int jn = min(kSeg, kb1 - kb0 - s * kSeg);
             if (jn == kSeg)
-                q40_blocks<NTF, kSeg>(st, L, jn, acc);
+                q40_blocks<NTF, kSeg>(st, lane_of(s), jn, acc);
             else
-                q40_blocks<NTF, 0>(st, L, jn, acc);
+                q40_blocks<NTF, 0>(st, lane_of(s), jn, acc);
             if (s + 1 < nseg) stage_store(s + 1);
             __syncthreads();
         }
