@@ -124,6 +124,7 @@ __device__ __attribute__((always_inline)) inline int lane63(int x) { return __bu
 // descending idx order: a per-expert bit row marks the chunk's members, so an
 // entry's rank is its expert's running count plus the bits below it.
 constexpr int kSelWG = 1024;
+static_assert(kSelWG >= 4 * kMaxExperts, "four threads per expert rank the GEMM experts");
 constexpr int kSelChunk = 512;
 constexpr int kSelWords = kSelChunk / 32;
 
@@ -197,19 +198,25 @@ __device__ void pack_lists(int n, int E, const SelectOut &o, const int32_t *s_id
     // the GEMM's work items, claimed in order by workgroups as they free up,
     // end with the smallest: an expert's rank and tile prefix count the GEMM
     // experts ordered before it.
+    // Four threads per expert, each counting over a quarter of the experts
+    // (kSelWG >= 4 * kMaxExperts), summed across the four lanes.
     __syncthreads();
-    if (s_gemm_on) {
-        for (int e = tid; e < E; e += blockDim.x) {
-            const int c = s_cnt[e];
-            if (!(c > 0 && c >= o.gemm_min)) continue;
-            int rank = 0, pre = 0;
-            for (int f = 0; f < E; f++) {
-                const int cf = s_cnt[f];
-                if (cf > 0 && cf >= o.gemm_min && (cf > c || (cf == c && f < e))) {
-                    rank++;
-                    pre += (cf + kGemmTokens - 1) / kGemmTokens;
-                }
+    if (s_gemm_on && tid < 4 * E) {
+        const int e = tid >> 2, part = tid & 3, q = (E + 3) / 4;
+        const int c = s_cnt[e];
+        int rank = 0, pre = 0;
+        for (int f = part * q; f < min(E, part * q + q); f++) {
+            const int cf = s_cnt[f];
+            if (cf > 0 && cf >= o.gemm_min && (cf > c || (cf == c && f < e))) {
+                rank++;
+                pre += (cf + kGemmTokens - 1) / kGemmTokens;
             }
+        }
+        rank += __shfl_xor(rank, 1);
+        pre += __shfl_xor(pre, 1);
+        rank += __shfl_xor(rank, 2);
+        pre += __shfl_xor(pre, 2);
+        if (part == 0 && c > 0 && c >= o.gemm_min) {
             o.gm_active[rank] = e;
             o.gm_tile_off[rank] = pre;
         }
