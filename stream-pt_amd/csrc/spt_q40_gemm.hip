@@ -36,7 +36,7 @@ constexpr int kAPieces = 10;      // 16-byte loads per row window (144 + 15 <= 1
 constexpr int kARow = 176;        // LDS bytes per staged row (44 dwords: rows over distinct banks)
 constexpr int kBTok = kSeg * 32 + 16;  // LDS bytes per staged token (68 dwords)
 constexpr int kOffB = kTR * kARow;
-constexpr int kOffD = kOffB + kTN * kBTok;  // d_x [token][kSeg]
+constexpr int kOffD = kOffB + kTN * kBTok;  // d_x [kSeg][token] (a fragment's 16 tokens in consecutive banks)
 constexpr int kStageBytes = kOffD + kTN * kSeg * 4;
 static_assert(kSeg * kQ40Block + 15 <= 16 * kAPieces && 16 * kAPieces <= kARow, "A window");
 constexpr int kALoads = (kTR * kAPieces + kThreads - 1) / kThreads;  // 3
@@ -79,7 +79,7 @@ __device__ __attribute__((always_inline)) inline void q40_blocks(const uint8_t *
             const uint32_t *bq = reinterpret_cast<const uint32_t *>(st + kOffB + t * kBTok + 32 * j);
             b.bq[tf][0] = bq[L.g];
             b.bq[tf][1] = bq[4 + L.g];
-            b.dx[tf] = *reinterpret_cast<const float *>(st + kOffD + 4 * (t * kSeg + j));
+            b.dx[tf] = *reinterpret_cast<const float *>(st + kOffD + 4 * (j * kTN + t));
         }
     };
     auto run = [&](const Blk &b) {
@@ -201,7 +201,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
             *reinterpret_cast<u32x4 *>(st + kOffB + t * kBTok + 16 * pc) = rb[k];
         }
 #pragma unroll
-        for (int k = 0; k < kSLoads; k++) *reinterpret_cast<uint32_t *>(st + kOffD + 4 * (tid + kThreads * k)) = rsx[k];
+        for (int k = 0; k < kSLoads; k++) {
+            const int e = tid + kThreads * k;  // token e / kSeg, block e % kSeg
+            *reinterpret_cast<uint32_t *>(st + kOffD + 4 * ((e % kSeg) * kTN + e / kSeg)) = rsx[k];
+        }
     };
 
     // this lane's A row (MFMA layout: row i16) and D rows (4g .. 4g+3)
