@@ -33,16 +33,22 @@ constexpr int kTR = 16 * kWaves;  // rows per workgroup (16 per wave)
 constexpr int kTN = 64;           // tokens per workgroup (4 fragments)
 constexpr int kSeg = 8;           // blocks per K segment (144 bytes of a row)
 constexpr int kAPieces = 10;      // 16-byte loads per row window (144 + 15 <= 160)
-constexpr int kARow = 176;        // LDS bytes per staged row (44 dwords: rows over distinct banks)
-constexpr int kBTok = kSeg * 32 + 16;  // LDS bytes per staged token (68 dwords)
+constexpr int kASlots = 11;       // LDS slots of 16 B per staged row (44 dwords: rows over distinct banks)
+constexpr int kARow = 16 * kASlots;
+constexpr int kAInstr = kTR * kASlots / 64;  // LDS DMA loads of a stage's A (64 slots each): 11
+constexpr int kBSlots = 2 * kSeg + 1;        // LDS slots of 16 B per staged token (the last is padding)
+constexpr int kBTok = 16 * kBSlots;          // 68 dwords: a fragment's tokens over distinct banks
+constexpr int kBInstr = kTN * kBSlots / 64;  // LDS DMA loads of a stage's B: 17
 constexpr int kOffB = kTR * kARow;
 constexpr int kOffD = kOffB + kTN * kBTok;  // d_x [kSeg][token] (a fragment's 16 tokens in consecutive banks)
 constexpr int kStageBytes = kOffD + kTN * kSeg * 4;
-static_assert(kSeg * kQ40Block + 15 <= 16 * kAPieces && 16 * kAPieces <= kARow, "A window");
-constexpr int kALoads = (kTR * kAPieces + kThreads - 1) / kThreads;  // 3
-constexpr int kBLoads = kTN * kSeg * 2 / kThreads;                    // 4 (16 pieces of 16 B per token)
-constexpr int kSLoads = kTN * kSeg / kThreads;                        // 2 (d_x, one dword each)
-static_assert(kTN * kSeg * 2 % kThreads == 0 && kTN * kSeg % kThreads == 0, "stage loads");
+constexpr uint32_t kOOR = 0x80000000u;      // buffer offset past every range: reads zero
+static_assert(kSeg * kQ40Block + 15 <= 16 * kAPieces && kAPieces < kASlots, "A window");
+static_assert(kTR * kASlots % 64 == 0, "whole A loads");
+constexpr int kALoadsMax = (kAInstr + kWaves - 1) / kWaves;  // 3 (wave w: loads w, w + 4, w + 8 below 11)
+constexpr int kBLoadsMax = (kBInstr + kWaves - 1) / kWaves;  // 5 (wave w: loads w, w + 4, ... below 17)
+constexpr int kDLoads = kSeg / kWaves;                       // 2 (one block of the 64 tokens' d_x each)
+static_assert(kTN * kBSlots % 64 == 0 && kSeg % kWaves == 0 && kTN == 64, "stage loads");
 
 // Four bytes of the stage at byte offset o (o even: Q4_0 rows are 2-byte
 // aligned): two aligned dwords and a byte shift.
@@ -124,8 +130,9 @@ __device__ __attribute__((always_inline)) inline void q40_blocks(const uint8_t *
 
 // Workgroup (x, y): rows 64x .. 64x+63, tokens 64y .. 64y+63.  Wave w takes
 // rows 16w .. 16w+15 with all 64 tokens (four MFMA fragments per block).
-// The K loop runs over segments of kSeg blocks with two LDS stages: while a
-// segment is multiplied, the next one's loads are in flight in registers.
+// The K loop runs over segments of kSeg blocks with two LDS stages filled by
+// LDS DMA loads (global/buffer -> LDS, no registers): while a segment is
+// multiplied, the next one's loads are in flight.
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void k_q40_gemm(Q40Args a) {
     extern __shared__ __align__(16) uint8_t lds[];
     const int tid = threadIdx.x, lane = tid & 63;
@@ -145,65 +152,57 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
     // the matrix from the 16-byte boundary at or below its first byte
     const uintptr_t wb = reinterpret_cast<uintptr_t>(a.w);
     const uint32_t le = (uint32_t)(wb & 15u);
-    const rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void *>(wb - le), (short)0,
-                                                        (int)(uint32_t)((a.nbytes + le + 15u) & ~15ull), kRsrcWord3);
 
-    // this thread's stage loads: A pieces (row p/10, piece p%10), B pieces
-    // (token q/16, piece q%16), d_x and code sums (one dword each)
-    uint32_t a_pos[kALoads];
-    int a_r[kALoads], a_pc[kALoads];
-    bool a_ok[kALoads];
+    // this thread's LDS DMA loads of a stage: A load i = wave + 4k fills slots
+    // 64i..64i+63 (slot q: row q / 11, piece q % 11; piece 10 is padding),
+    // B load i = wave + 4k likewise (slot q: token q / 17, piece q % 17;
+    // piece 16 is padding), d_x load k: block wave + 4k of token lane; past
+    // the rows, tokens or K range the loads read zeros
+    const u32x4v rsa = rsrc_words(reinterpret_cast<const void *>(wb - le), (uint32_t)((a.nbytes + le + 15u) & ~15ull));
+    const u32x4v rsb = rsrc_words(a.codes, (uint32_t)((size_t)a.ntok * nb * 32));
+    const u32x4v rsd = rsrc_words(a.scales, (uint32_t)((size_t)a.ntok * nb * 4));
+    uint32_t a_pos[kALoadsMax];
+    bool a_ok[kALoadsMax];
 #pragma unroll
-    for (int k = 0; k < kALoads; k++) {
-        const int p = tid + kThreads * k;
-        a_r[k] = p / kAPieces;
-        a_pc[k] = p - a_r[k] * kAPieces;
-        const int row = r0 + a_r[k];
-        a_ok[k] = p < kTR * kAPieces && row < a.rows;
-        a_pos[k] = le + (uint32_t)(a_ok[k] ? row : 0) * row_bytes;
+    for (int k = 0; k < kALoadsMax; k++) {
+        const int q = 64 * (wave + kWaves * k) + lane, r = q / kASlots, pc = q - r * kASlots;
+        const int row = r0 + r;
+        a_ok[k] = wave + kWaves * k < kAInstr && pc < kAPieces && row < a.rows;
+        a_pos[k] = le + (uint32_t)(a_ok[k] ? row : 0) * row_bytes + 16u * (uint32_t)pc;
     }
-    u32x4 ra[kALoads], rb[kBLoads];
-    uint32_t rsx[kSLoads];
-    auto stage_load = [&](int s) {
+    uint32_t b_tok[kBLoadsMax], b_pc[kBLoadsMax];
+    bool b_ok[kBLoadsMax];
+#pragma unroll
+    for (int k = 0; k < kBLoadsMax; k++) {
+        const int q = 64 * (wave + kWaves * k) + lane, t = q / kBSlots, p = q - t * kBSlots;
+        b_ok[k] = wave + kWaves * k < kBInstr && t < nt && p < 2 * kSeg;
+        b_tok[k] = (uint32_t)(t0 + (t < nt ? t : 0));
+        b_pc[k] = (uint32_t)p;
+    }
+    typedef __attribute__((address_space(3))) uint8_t lds_u8;
+    const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>((lds_u8 *)lds);
+    auto issue = [&](int s) {
+        const uint32_t st = lds0 + (uint32_t)(s & 1) * kStageBytes;
         const int b0 = kb0 + s * kSeg;
 #pragma unroll
-        for (int k = 0; k < kALoads; k++) {
-            const uint32_t off = ((a_pos[k] + (uint32_t)b0 * kQ40Block) & ~15u) + 16u * (uint32_t)a_pc[k];
-            ra[k] = a_ok[k] ? __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0))
-                            : u32x4{0u, 0u, 0u, 0u};
+        for (int k = 0; k < kALoadsMax; k++) {
+            if (wave + kWaves * k >= kAInstr) continue;  // wave-uniform
+            // (pos - 16*piece) rounded down to 16, plus 16*piece
+            const uint32_t pos = a_pos[k] + (uint32_t)b0 * kQ40Block;
+            dma16(rsa, st + 1024u * (uint32_t)(wave + kWaves * k), a_ok[k] ? (pos & ~15u) : kOOR, 0u);
         }
 #pragma unroll
-        for (int k = 0; k < kBLoads; k++) {
-            const int q = tid + kThreads * k, t = q >> 4, pc = q & 15;
-            const int b = b0 + (pc >> 1);
-            u32x4 v = {0u, 0u, 0u, 0u};
-            if (t < nt && b < kb1)
-                v = *reinterpret_cast<const u32x4 *>(a.codes + ((size_t)(t0 + t) * nb + b) * 32 + 16 * (pc & 1));
-            rb[k] = v;
+        for (int k = 0; k < kBLoadsMax; k++) {
+            if (wave + kWaves * k >= kBInstr) continue;  // wave-uniform
+            const int b = b0 + (int)(b_pc[k] >> 1);
+            const uint32_t off = (b_ok[k] && b < kb1) ? (b_tok[k] * (uint32_t)nb + (uint32_t)b) * 32u + 16u * (b_pc[k] & 1u) : kOOR;
+            dma16(rsb, st + kOffB + 1024u * (uint32_t)(wave + kWaves * k), off, 0u);
         }
 #pragma unroll
-        for (int k = 0; k < kSLoads; k++) {
-            const int e = tid + kThreads * k;
-            const int t = e / kSeg, b = b0 + e % kSeg;
-            uint32_t v = 0u;
-            if (t < nt && b < kb1) v = __float_as_uint(a.scales[(size_t)(t0 + t) * nb + b]);
-            rsx[k] = v;
-        }
-    };
-    auto stage_store = [&](int s) {
-        uint8_t *st = lds + (size_t)(s & 1) * kStageBytes;
-#pragma unroll
-        for (int k = 0; k < kALoads; k++)
-            if (tid + kThreads * k < kTR * kAPieces) *reinterpret_cast<u32x4 *>(st + a_r[k] * kARow + 16 * a_pc[k]) = ra[k];
-#pragma unroll
-        for (int k = 0; k < kBLoads; k++) {
-            const int q = tid + kThreads * k, t = q >> 4, pc = q & 15;
-            *reinterpret_cast<u32x4 *>(st + kOffB + t * kBTok + 16 * pc) = rb[k];
-        }
-#pragma unroll
-        for (int k = 0; k < kSLoads; k++) {
-            const int e = tid + kThreads * k;  // token e / kSeg, block e % kSeg
-            *reinterpret_cast<uint32_t *>(st + kOffD + 4 * ((e % kSeg) * kTN + e / kSeg)) = rsx[k];
+        for (int k = 0; k < kDLoads; k++) {
+            const int b = b0 + wave + kWaves * k;
+            const uint32_t off = (lane < nt && b < kb1) ? ((uint32_t)(t0 + lane) * (uint32_t)nb + (uint32_t)b) * 4u : kOOR;
+            dma4(rsd, st + kOffD + 256u * (uint32_t)(wave + kWaves * k), off, 0u);
         }
     };
 
@@ -240,19 +239,25 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
             L.g = g;
             return L;
         };
-        stage_load(0);
-        stage_store(0);
-        __syncthreads();
-        for (int s = 0; s < nseg; s++) {
-            if (s + 1 < nseg) stage_load(s + 1);
-            const uint8_t *st = lds + (size_t)(s & 1) * kStageBytes;
-            const int jn = min(kSeg, kb1 - kb0 - s * kSeg);
-            if (jn == kSeg)
-                q40_blocks<NTF, kSeg>(st, lane_of(s), jn, acc);
-            else
-                q40_blocks<NTF, 0>(st, lane_of(s), jn, acc);
-            if (s + 1 < nseg) stage_store(s + 1);
-            __syncthreads();
+        // this wave's loads of segment s have landed; after the barrier
+        // every wave's have, and every wave is done with segment s-1, whose
+        // stage segment s+1 reuses
+        auto wait_stage = [] {
+            asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+        };
+        const int nfull = (kb1 - kb0) / kSeg;
+        issue(0);
+        int s = 0;
+        for (; s < nfull; s++) {
+            wait_stage();
+            if (s + 1 < nseg) issue(s + 1);
+            q40_blocks<NTF, kSeg>(lds + (size_t)(s & 1) * kStageBytes, lane_of(s), kSeg, acc);
+        }
+        if (s < nseg) {
+            wait_stage();
+            q40_blocks<NTF, 0>(lds + (size_t)(s & 1) * kStageBytes, lane_of(s), kb1 - kb0 - kSeg * s, acc);
         }
     };
     if (ntf == 4)
