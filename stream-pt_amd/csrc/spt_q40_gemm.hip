@@ -113,8 +113,8 @@ __device__ __attribute__((always_inline)) inline void q40_blocks(const uint8_t *
             if (j + 1 < JN) fetch(j + 1, nxt);
             run(cur);
             cur = nxt;
-            // keep the schedule one block deep (hoisting later blocks' reads
-            // runs out of registers)
+            // keep the schedule one block deep (measured: Q at 512 tokens
+            // 45.6 us, 46.7 us when later blocks' reads may be hoisted)
             __builtin_amdgcn_sched_barrier(0);
         }
     } else {
