@@ -876,8 +876,7 @@ Q40Plan q40_plan(const Q40Proj *p, int np, int64_t nb, int64_t batch, bool q8_in
         if (p[i].w->nbytes >= spt::kQ40DecMaxBytes) L.dec = false;
         if (!q40_gemm_form(p[i].out, batch)) continue;
         gemm = true;
-        if (p[i].out < spt::kQ40GemmMinRows)
-            part = std::max(part, (size_t)spt::kQ40SplitK * batch * p[i].out * 4);
+        if (p[i].out < spt::kQ40GemmMinRows) part += (size_t)spt::kQ40SplitK * batch * p[i].out * 4;
     }
     L.views = !L.dec && (!q8_in || gemm);
     L.nb = nb;
@@ -893,8 +892,10 @@ Q40Plan q40_plan(const Q40Proj *p, int np, int64_t nb, int64_t batch, bool q8_in
 }
 
 // Quantize (x) or unpack (xq34) the input into the plan's views when it has
-// them, then one GEMV launch over every projection not on a GEMM form and
-// one GEMM launch per projection that is.
+// them, then one GEMV launch over every projection not on a GEMM form, one
+// GEMM launch over those on the wide GEMM form and one over those on the
+// split form (launches over several matrices of the same input fill the GPU
+// where one narrow matrix alone would not).
 int run_q40_at(spt_ctx *ctx, const Q40Proj *p, int np, const Q40Plan &L, char *S, const float *x,
                const uint8_t *xq34) {
     const int64_t nb = L.nb, batch = L.batch;
@@ -908,36 +909,35 @@ int run_q40_at(spt_ctx *ctx, const Q40Proj *p, int np, const Q40Plan &L, char *S
         }));
     }
     int rc;
-    spt::Q40Args g{};
-    int ng = 0;
+    // the three launches' arguments: 0 GEMV, 1 wide GEMM, 2 split GEMM
+    spt::Q40Args g[3]{};
+    int ng[3] = {0, 0, 0};
     for (int i = 0; i < np; i++) {
-        if ((rc = check_cancel(ctx))) return rc;
         const spt_tensor *w = p[i].w;
-        if (q40_gemm_form(p[i].out, batch)) {
-            spt::Q40Args a{(const uint8_t *)w->data, w->nbytes, (int)p[i].out, (int)nb, codes, scales, sumq,
-                           (int)batch, p[i].y, p[i].bias, p[i].btype, p[i].resid,
-                           p[i].out < spt::kQ40GemmMinRows ? (float *)(S + L.o_part) : nullptr};
-            SPT_HIP(timed(ctx, SPT_KERNEL_Q40, [&] { return spt::launch_q40_gemv(ctx->stream, a); }));
-            continue;
-        }
-        if (ng == 0) {
-            g = spt::Q40Args{(const uint8_t *)w->data, w->nbytes, (int)p[i].out, (int)nb, codes, scales, sumq,
-                             (int)batch, p[i].y, p[i].bias, p[i].btype, p[i].resid, nullptr};
+        const int k = !q40_gemm_form(p[i].out, batch) ? 0 : p[i].out >= spt::kQ40GemmMinRows ? 1 : 2;
+        if (ng[k] == 0) {
+            g[k] = spt::Q40Args{(const uint8_t *)w->data, w->nbytes, (int)p[i].out, (int)nb, codes, scales, sumq,
+                                (int)batch, p[i].y, p[i].bias, p[i].btype, p[i].resid,
+                                k == 2 ? (float *)(S + L.o_part) : nullptr};
         } else {
-            g.more[ng - 1] = spt::Q40Mat{(const uint8_t *)w->data, w->nbytes, (int)p[i].out, p[i].y, p[i].bias,
-                                         p[i].btype, p[i].resid};
+            g[k].more[ng[k] - 1] = spt::Q40Mat{(const uint8_t *)w->data, w->nbytes, (int)p[i].out, p[i].y, p[i].bias,
+                                               p[i].btype, p[i].resid};
         }
-        ng++;
+        g[k].nmore = ng[k]++;
     }
-    if (ng) {
-        g.nmore = ng - 1;
-        g.xq34 = L.views ? nullptr : xq34;
+    for (int k = 1; k < 3; k++) {
+        if (!ng[k]) continue;
+        if ((rc = check_cancel(ctx))) return rc;
+        SPT_HIP(timed(ctx, SPT_KERNEL_Q40, [&] { return spt::launch_q40_gemm(ctx->stream, g[k]); }));
+    }
+    if (ng[0]) {
+        g[0].xq34 = L.views ? nullptr : xq34;
         if ((rc = check_cancel(ctx))) return rc;
         if (L.dec) {
-            g.xf = x;
-            SPT_HIP(timed(ctx, SPT_KERNEL_Q40, [&] { return spt::launch_q40_dec(ctx->stream, g); }));
+            g[0].xf = x;
+            SPT_HIP(timed(ctx, SPT_KERNEL_Q40, [&] { return spt::launch_q40_dec(ctx->stream, g[0]); }));
         } else {
-            SPT_HIP(timed(ctx, SPT_KERNEL_Q40, [&] { return spt::launch_q40_gemv(ctx->stream, g); }));
+            SPT_HIP(timed(ctx, SPT_KERNEL_Q40, [&] { return spt::launch_q40_gemv(ctx->stream, g[0]); }));
         }
     }
     return SPT_OK;

@@ -175,14 +175,16 @@ struct Q40Args {
     const void *bias;
     int bias_type;
     float *resid;
-    // optional scratch of kQ40SplitK * ntok * rows floats: narrow projections
-    // of large batches then run on the GEMM with K split kQ40SplitK ways
+    // optional scratch of kQ40SplitK * ntok * rows floats (rows summed over
+    // the matrices of the launch): narrow projections of large batches then
+    // run on the GEMM with K split kQ40SplitK ways
     float *part;
     // GEMV only: the activations as GGML Q8_0 blocks ([ntok][nb] x 34 bytes,
     // 2-byte aligned) in place of codes / scales / sumq
     const uint8_t *xq34;
-    // GEMV only: up to two more matrices with the same input; their row
-    // tiles follow this matrix's in the grid
+    // up to two more matrices with the same input; their row tiles follow
+    // this matrix's in the grid (the GEMV, and the GEMM, whose partial sums
+    // of matrix i then start after the previous matrices' in part)
     int nmore;
     Q40Mat more[2];
     // few-token form only (q40_dec_form): the fp32 activations, quantized to
@@ -192,13 +194,16 @@ struct Q40Args {
 
 // The matrix of row tile `tile` (of `per_tile` rows) of a launch over
 // several matrices with the same input (Q40Args::more): its fields in place
-// of the first's, and the tile rebased to it.
-__device__ inline Q40Args q40_matrix(const Q40Args &args, int *tile, int per_tile) {
+// of the first's, and the tile rebased to it; *rows_before (when given) is
+// the number of rows of the matrices before it.
+__device__ inline Q40Args q40_matrix(const Q40Args &args, int *tile, int per_tile, int *rows_before = nullptr) {
     Q40Args a = args;
+    int before = 0;
     for (int i = 0; i < args.nmore; i++) {
         const int tiles = (a.rows + per_tile - 1) / per_tile;
         if (*tile < tiles) break;
         *tile -= tiles;
+        before += a.rows;
         const Q40Mat &m = args.more[i];
         a.w = m.w;
         a.nbytes = m.nbytes;
@@ -208,6 +213,7 @@ __device__ inline Q40Args q40_matrix(const Q40Args &args, int *tile, int per_til
         a.bias_type = m.bias_type;
         a.resid = m.resid;
     }
+    if (rows_before) *rows_before = before;
     return a;
 }
 

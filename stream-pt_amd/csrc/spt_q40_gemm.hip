@@ -133,14 +133,16 @@ __device__ __attribute__((always_inline)) inline void q40_blocks(const uint8_t *
 // The K loop runs over segments of kSeg blocks with two LDS stages filled by
 // LDS DMA loads (global/buffer -> LDS, no registers): while a segment is
 // multiplied, the next one's loads are in flight.
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void k_q40_gemm(Q40Args a) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void k_q40_gemm(Q40Args args) {
     extern __shared__ __align__(16) uint8_t lds[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int i16 = lane & 15, g = lane >> 4;
+    int tile = blockIdx.x, rows_before = 0;
+    const Q40Args a = q40_matrix(args, &tile, kTR, &rows_before);
     const int nb = a.nb;
     const uint32_t row_bytes = (uint32_t)nb * kQ40Block;
-    const int r0 = blockIdx.x * kTR, t0 = blockIdx.y * kTN;
+    const int r0 = tile * kTR, t0 = blockIdx.y * kTN;
     const int nt = min(kTN, a.ntok - t0);
     const int ntf = (nt + 15) >> 4;
     // K range of this workgroup: blocks [kb0, kb1) (split over grid z when
@@ -277,7 +279,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
         for (int tf = 0; tf < 4; tf++) {
             const int t = 16 * tf + i16;
             if (t >= nt) continue;
-            float *pp = a.part + ((size_t)kz * a.ntok + t0 + t) * a.rows + row;
+            float *pp = a.part + (size_t)ks * a.ntok * rows_before + ((size_t)kz * a.ntok + t0 + t) * a.rows + row;
 #pragma unroll
             for (int r = 0; r < 4; r++)
                 if (row + r < a.rows) pp[r] = acc[tf][r];
@@ -301,25 +303,45 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
 }
 
 // y[t][row] = the K ranges' partial sums added in range order, then the
-// projection epilogue.
-__global__ __launch_bounds__(256) void k_q40_reduce(Q40Args a, int ks) {
+// projection epilogue; element o of the launch's matrices in order (matrix i
+// holds ntok * rows_i of them; its ks partial sums start after the previous
+// matrices').
+__global__ __launch_bounds__(256) void k_q40_reduce(Q40Args args, int ks, size_t total) {
+    size_t o = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (o >= total) return;
+    int tile = 0, rows_before = 0;
+    Q40Args a = args;
+    for (int i = 0; i <= args.nmore; i++) {
+        int t = tile;
+        a = q40_matrix(args, &t, 1, &rows_before);
+        const size_t n = (size_t)a.ntok * a.rows;
+        if (o < n) break;
+        o -= n;
+        tile += a.rows;
+    }
     const size_t n = (size_t)a.ntok * a.rows;
-    const size_t o = (size_t)blockIdx.x * 256 + threadIdx.x;
-    if (o >= n) return;
-    float v = a.part[o];
-    for (int z = 1; z < ks; z++) v = v + a.part[(size_t)z * n + o];
+    const float *pp = a.part + (size_t)ks * a.ntok * rows_before + o;
+    float v = pp[0];
+    for (int z = 1; z < ks; z++) v = v + pp[(size_t)z * n];
     q40_store(a, o, (int)(o % (size_t)a.rows), v);
 }
 
 hipError_t launch_q40_gemm(hipStream_t s, const Q40Args &a) {
     if (a.rows <= 0 || a.ntok <= 0 || a.nb <= 0) return hipSuccess;
+    if (a.nmore < 0 || a.nmore > 2) return hipErrorInvalidValue;
+    int tiles = (a.rows + kTR - 1) / kTR, rows = a.rows;
+    for (int i = 0; i < a.nmore; i++) {
+        if (a.more[i].rows <= 0) return hipErrorInvalidValue;
+        tiles += (a.more[i].rows + kTR - 1) / kTR;
+        rows += a.more[i].rows;
+    }
     const int ks = a.part ? (a.nb < kQ40SplitK ? a.nb : kQ40SplitK) : 1;
-    dim3 grid((a.rows + kTR - 1) / kTR, (a.ntok + kTN - 1) / kTN, ks);
+    dim3 grid(tiles, (a.ntok + kTN - 1) / kTN, ks);
     hipLaunchKernelGGL(k_q40_gemm, grid, dim3(kThreads), 2 * (size_t)kStageBytes, s, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || !a.part) return e;
-    const size_t n = (size_t)a.ntok * a.rows;
-    hipLaunchKernelGGL(k_q40_reduce, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a, ks);
+    const size_t n = (size_t)a.ntok * rows;
+    hipLaunchKernelGGL(k_q40_reduce, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a, ks, n);
     return hipGetLastError();
 }
 

@@ -156,6 +156,40 @@ def test_q40_qkv_fused(gpu_ctx, O, batch, form):
     assert_close(ys[0].cpu().numpy(), wq.reshape(-1), what="fused Q")
 
 
+@pytest.mark.parametrize("douts", [(1088, 320, 200), (576, 128, 72), (200, 1100, 90)])
+def test_q40_qkv_fused_split_group(gpu_ctx, O, douts):
+    """The fused call at 300 tokens with narrow projections of ragged widths:
+    those under 1024 rows share one split-K GEMM launch (their partial sums
+    side by side in the arena, then one reduce over all of them), each
+    output bit-equal to its own call, the last also against the oracle.
+    65 blocks per row: the four K ranges end in partial segments."""
+    import torch
+
+    from spt import synth
+
+    din, batch = 2080, 300
+    names = ("attn_q", "attn_k", "attn_v")
+    mats = [_q40(n, din, d, 50 + i) for i, (n, d) in enumerate(zip(names, douts))]
+    biases = [_f32_bias(n + ".bias", d, 60 + i) for i, (n, d) in enumerate(zip(names, douts))]
+    biases[0] = None
+    x = synth.normal(synth.stream_key(26, batch), batch * din)
+    xd = _dev(x)
+    want = []
+    for (w, wd, t), bb in zip(mats, biases):
+        y = _zeros(batch * int(t.shape[1]))
+        gpu_ctx.mul_q40_batch_bias_into(t, bb[2] if bb else None, xd, y, batch)
+        want.append(y)
+    ys = [_zeros(batch * d) for d in douts]
+    gpu_ctx.mul_q40_qkv_batch_into([t for _, _, t in mats], [bb[2] if bb else None for bb in biases], xd, ys,
+                                   batch)
+    torch.cuda.synchronize()
+    for i in range(3):
+        assert np.array_equal(bits(ys[i].cpu().numpy()), bits(want[i].cpu().numpy())), f"projection {i}"
+    w, _, _ = mats[2]
+    wv = O.mul_q40_q8(w, x, din, douts[2], batch).reshape(batch, douts[2]) + biases[2][0][None, :]
+    assert_close(ys[2].cpu().numpy(), wv.reshape(-1), what="fused V")
+
+
 def test_rmsnorm_q8_feeds_qkv_and_moe(gpu_ctx, O):
     """The fused RMSNorm's Q8_0 output consumed as is: normBatch of 8 rows
     with its GGML blocks, then the fused Q/K/V call and the MoE layer on those
