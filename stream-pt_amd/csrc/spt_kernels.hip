@@ -251,59 +251,94 @@ static size_t select_lds(int n, int E) {
     return sizeof(int32_t) * (2 * (size_t)n + 3 * (size_t)E + 1) + sizeof(uint32_t) * kSelWords * (size_t)E;
 }
 
-// Router logits for batches of more than kRouteLdsMaxBatch tokens: one
-// workgroup per (4 experts, 1 token); wave w computes the logit of expert
-// 4 blockIdx.x + w for token blockIdx.y straight from memory (16 chunk
-// loads in flight per lane), so a batch's 128 x B wavefronts keep many
-// loads in flight per CU.  With q set, the workgroups of token t also
-// quantize its row of x to Q8_0, eight blocks each (a half-wave per block).
-// The FMA chains and the reduction are those of k_route below: the logits
-// are the same bits.
-__global__ __launch_bounds__(kWG) void k_route_rows(const float *__restrict__ router, const void *bias,
-                                                    int bias_type, const float *__restrict__ x, int H, int E,
+// Router logits for batches of more than kRouteLdsMaxBatch tokens: a
+// workgroup per (4 experts, EW * TT tokens), its four wavefronts in a
+// (4 / EW) x EW arrangement of (EW experts, TT tokens) each.  Lane L keeps one
+// accumulator per (expert, token) of its wavefront, each the FMA chain of
+// k_route below (element 64c + L over chunks c in order, the same bits), and
+// loads a chunk's element of each of its router rows and token rows once for
+// all of those chains, every load of a row in flight at once.  With q set,
+// the workgroups of a token group also quantize its rows of x to Q8_0 (a
+// half-wave per block).
+template <int EW, int TT>
+__global__ __launch_bounds__(kWG) void k_route_tile(const float *__restrict__ router, const void *bias,
+                                                    int bias_type, const float *__restrict__ x, int B, int H, int E,
                                                     float *__restrict__ logits, QuantOut q) {
+    static_assert(EW == 1 || EW == 2, "wavefronts of one or two experts");
+    constexpr int TW = EW * TT;  // tokens per workgroup
+    constexpr int U = 45;        // chunks per pass of loads
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int e = blockIdx.x * 4 + wave;
-    const int t = blockIdx.y;
-    const float *xt = x + (size_t)t * H;
+    const int tg0 = blockIdx.y * TW;
     if (q.codes || q.blocks34) {
-        const int nbh = H / 32;
-        for (int b0 = blockIdx.x * (kWG / 32); b0 < nbh; b0 += gridDim.x * (kWG / 32)) {
-            const int b = b0 + (tid >> 5), i = tid & 31;
+        const int nbh = H / 32, nq = min(TW, B - tg0) * nbh;
+        for (int f0 = blockIdx.x * (kWG / 32); f0 < nq; f0 += gridDim.x * (kWG / 32)) {
+            const int f = f0 + (tid >> 5), i = tid & 31;
+            const int fi = f < nq ? f : 0;
+            const int t = tg0 + fi / nbh, b = fi % nbh;
             uint16_t dh;
             int qv;
             if (q.src34) {
-                const uint8_t *blk = q.src34 + ((size_t)t * nbh + (b < nbh ? b : 0)) * kQ80Block;
+                const uint8_t *blk = q.src34 + ((size_t)t * nbh + b) * kQ80Block;
                 qv = (int)(int8_t)blk[2 + i];
                 dh = (uint16_t)(blk[0] | (blk[1] << 8));
             } else {
-                const float v = b < nbh ? xt[b * 32 + i] : 0.0f;
+                const float v = f < nq ? x[(size_t)t * H + b * 32 + i] : 0.0f;
                 qv = q8_quantize_half(v, lane, &dh);  // every lane takes part
             }
-            if (b < nbh) write_q8_lane(qv, dh, i, (size_t)t * nbh + b, q.codes, q.scales, q.mxtab, q.blocks34, q.btab);
+            if (f < nq) write_q8_lane(qv, dh, i, (size_t)t * nbh + b, q.codes, q.scales, q.mxtab, q.blocks34, q.btab);
         }
     }
-    if (e >= E) return;
-    const float *w = router + (size_t)e * H;
-    const int nfull = H / 64;
-    float acc = 0.0f;
-    for (int c0 = 0; c0 < nfull; c0 += 16) {
-        float wv[16], xv[16];
+    const int e0 = blockIdx.x * 4 + EW * (wave % (4 / EW)), t0 = tg0 + TT * (wave / (4 / EW));
+    if (e0 >= E || t0 >= B) return;  // whole wavefronts
+    const float *wr[EW], *xr[TT];
 #pragma unroll
-        for (int u = 0; u < 16; u++) {
-            const int cc = c0 + u;
-            if (cc < nfull) {
-                wv[u] = w[cc * 64 + lane];
-                xv[u] = xt[cc * 64 + lane];
+    for (int i = 0; i < EW; i++) wr[i] = router + (size_t)min(e0 + i, E - 1) * H + lane;
+#pragma unroll
+    for (int j = 0; j < TT; j++) xr[j] = x + (size_t)min(t0 + j, B - 1) * H + lane;
+    float acc[EW][TT];
+#pragma unroll
+    for (int i = 0; i < EW; i++)
+#pragma unroll
+        for (int j = 0; j < TT; j++) acc[i][j] = 0.0f;
+    // passes of U chunks with every load of a pass in flight at once (one
+    // pass over a 2880-wide row); chunks past the row load its last chunk
+    // and are not multiplied
+    const int nfull = H / 64;
+    for (int c0 = 0; c0 < nfull; c0 += U) {
+        float wv[U][EW], xv[U][TT];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int c = min(c0 + u, nfull - 1) * 64;
+#pragma unroll
+            for (int i = 0; i < EW; i++) wv[u][i] = wr[i][c];
+#pragma unroll
+            for (int j = 0; j < TT; j++) xv[u][j] = xr[j][c];
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            if (c0 + u < nfull) {
+#pragma unroll
+                for (int i = 0; i < EW; i++)
+#pragma unroll
+                    for (int j = 0; j < TT; j++) acc[i][j] = __builtin_fmaf(wv[u][i], xv[u][j], acc[i][j]);
             }
         }
-#pragma unroll
-        for (int u = 0; u < 16; u++)
-            if (c0 + u < nfull) acc = __builtin_fmaf(wv[u], xv[u], acc);
     }
-    if (nfull * 64 < H && lane < 32) acc = __builtin_fmaf(w[nfull * 64 + lane], xt[nfull * 64 + lane], acc);
-    const float r = router_reduce(acc, lane);
-    if (lane == 0) logits[(size_t)t * E + e] = r + bias_at(bias, bias_type, e);
+    if (nfull * 64 < H && lane < 32) {
+#pragma unroll
+        for (int i = 0; i < EW; i++)
+#pragma unroll
+            for (int j = 0; j < TT; j++)
+                acc[i][j] = __builtin_fmaf(wr[i][nfull * 64], xr[j][nfull * 64], acc[i][j]);
+    }
+#pragma unroll
+    for (int i = 0; i < EW; i++)
+#pragma unroll
+        for (int j = 0; j < TT; j++) {
+            const float r = router_reduce(acc[i][j], lane);
+            if (lane == 0 && e0 + i < E && t0 + j < B)
+                logits[(size_t)(t0 + j) * E + e0 + i] = r + bias_at(bias, bias_type, e0 + i);
+        }
 }
 
 // Router logits: one wavefront per (expert, token), a workgroup each, so a
@@ -314,7 +349,7 @@ __global__ __launch_bounds__(kWG) void k_route_rows(const float *__restrict__ ro
 // wavefronts e < H/64 quantize two blocks of x each (a half-wave per block).
 constexpr int kRouteSeg = 4096;
 // Up to this many tokens the router spreads over one workgroup per (expert,
-// token) with LDS staging (latency); beyond, k_route_rows (throughput).
+// token) with LDS staging (latency); beyond, k_route_tile (throughput).
 constexpr int kRouteLdsMaxBatch = 4;
 template <bool MULTI>  // MULTI: H > kRouteSeg, segments in a loop; else one segment, straight-line
 __global__ __launch_bounds__(64) void k_route(const float *__restrict__ router, const void *bias, int bias_type,
@@ -439,9 +474,18 @@ hipError_t launch_route(hipStream_t s, const float *router, const void *bias, in
                         const float *x, int batch, int hidden, int experts, float *logits,
                         const QuantOut &q) {
     if (batch > kRouteLdsMaxBatch) {
-        dim3 grid((experts + 3) / 4, batch);
-        hipLaunchKernelGGL(k_route_rows, grid, dim3(kWG), 0, s, router, bias, bias_type, x, hidden, experts, logits,
-                           q);
+        // from 32 tokens, wavefronts of (2 experts, 2 tokens): 512 workgroups
+        // at 64 tokens and 128 experts, two waves per SIMD, one round;
+        // below, of (1 expert, 1 token), so few tokens still fill the CUs
+        if (batch >= 32) {
+            dim3 grid((experts + 3) / 4, (batch + 3) / 4);
+            hipLaunchKernelGGL((k_route_tile<2, 2>), grid, dim3(kWG), 0, s, router, bias, bias_type, x, batch, hidden,
+                               experts, logits, q);
+        } else {
+            dim3 grid((experts + 3) / 4, batch);
+            hipLaunchKernelGGL((k_route_tile<1, 1>), grid, dim3(kWG), 0, s, router, bias, bias_type, x, batch, hidden,
+                               experts, logits, q);
+        }
         return hipGetLastError();
     }
     // a wavefront per (expert, token); the Q8_0 of x needs H/64 of them per token

@@ -312,3 +312,31 @@ def test_moe_decode_continuous_batching(gpu_ctx, O, batch, path):
         e2e = assert_close(g["out"], want, tol=1e-2, what=f"layer {l} end-to-end")
         print(f"layer {l}: gemv max rel err {err:.2e}, end-to-end {e2e:.2e}")
         del lay
+
+
+@pytest.mark.parametrize("batch", [5, 33, 256, 257])
+def test_route_select_gpt_oss_router(gpu_ctx, O, batch):
+    """Router, top-k and per-expert lists at GPT-OSS-120B router shape (128
+    experts, top-4) through the batched router's token groups of two (5
+    tokens) and four (33 and more, ragged at 257), on two calls in a row
+    with different tokens: logits, ids, weights, lists and the combine
+    bit-exact against the oracle."""
+    import torch
+
+    import spt
+    from spt import workloads as W
+
+    shp = W.MoEShape()
+    seed = 5
+    dl = W.device_layer(gpu_ctx, seed=seed, layer=0, shp=shp)
+    lay = W.host_layer(seed, 0, shp, experts=[])
+    H, D, E, k = shp.hidden, shp.expert_dim, shp.experts, shp.topk
+    for rep in range(2):
+        x = W.x_tokens(seed, rep, batch, H)
+        t = _taps(batch, H, D, E, k)
+        out = torch.full((batch * H,), 999.0, dtype=torch.float32, device="cuda")
+        gpu_ctx.forward_moe_batch(dl.config, dl.layer, torch.from_numpy(x).cuda(), out, batch, spt.make_taps(**t))
+        torch.cuda.synchronize()
+        g = _host(t)
+        g["out"] = out.cpu().numpy()
+        check_stagewise(O, lay, x, batch, g, sample=[])
