@@ -409,7 +409,7 @@ struct MoELayout {
     int gemm_min;
     bool forced;
     size_t o_xc, o_xs, o_xm, o_xb, o_logits, o_ids, o_w, o_cnt, o_off, o_list, o_act_list, o_na;
-    size_t o_gv, o_gvn, o_gvp, o_gm, o_gmn, o_gmt, o_act, o_ac, o_as, o_am, o_ab, o_res;
+    size_t o_gv, o_gvn, o_gvp, o_gvs, o_gm, o_gmn, o_gmt, o_act, o_ac, o_as, o_am, o_ab, o_res;
     size_t total;
 };
 
@@ -435,6 +435,7 @@ MoELayout moe_layout(const spt_ctx *ctx, const MoEDims &m, bool act_tap, size_t 
     L.o_ids = c.take(n * 4), L.o_w = c.take(n * 4), L.o_cnt = c.take(E * 4), L.o_off = c.take((E + 1) * 4);
     L.o_list = c.take(n * 4), L.o_act_list = c.take(E * 4), L.o_na = c.take(4);
     L.o_gv = c.take(E * 4), L.o_gvn = c.take(4), L.o_gvp = c.take((E + 1) * 4);
+    L.o_gvs = c.take(L.decode ? 0 : sizeof(int32_t) * 2 * spt::kGvStartMax * spt::kGvStartWords);
     L.o_gm = c.take(E * 4), L.o_gmn = c.take(12), L.o_gmt = c.take((E + 1) * 4);  // gm_n, then the two claim counters
     L.o_act = c.take(act_tap ? n * d * 4 : 0), L.o_ac = c.take(n * d), L.o_as = c.take(n * nbd * 4);
     L.o_am = c.take(n * nbd * 64);
@@ -477,6 +478,19 @@ int run_moe_at(spt_ctx *ctx, const spt_moe_layer *lw, const float *x, float *out
     so.gm_n = (int32_t *)(S + L.o_gmn);
     so.gm_claim = (int32_t *)(S + L.o_gmn) + 1;
     so.gm_tile_off = (int32_t *)(S + L.o_gmt);
+    // the two grouped GEMV launches' start table, for their grids
+    const int slots = (int)(n < E ? n : E);
+    if (!L.decode) {
+        spt::MxMfmaArgs g{};
+        g.rows = (int)d;
+        so.gv_grid[0] = spt::mx_mfma_grid(spt::kGateUp, g, slots);
+        g.rows = (int)h;
+        so.gv_grid[1] = spt::mx_mfma_grid(spt::kDown, g, slots);
+        so.gv_tiles[0] = (int32_t)((d + 31) / 32);
+        so.gv_tiles[1] = (int32_t)((h + 63) / 64);
+        if (so.gv_grid[0] <= spt::kGvStartMax && so.gv_grid[1] <= spt::kGvStartMax)
+            so.gv_start = (int32_t *)(S + L.o_gvs);
+    }
     hipStream_t s = ctx->stream;
 
     // the Q8_0 of x: quantized by the router's launch, or unpacked there from
@@ -569,7 +583,6 @@ int run_moe_at(spt_ctx *ctx, const spt_moe_layer *lw, const float *x, float *out
         }
         return SPT_OK;
     }
-    const int slots = (int)(n < E ? n : E);
     spt::MxMfmaArgs ga{};
     ga.w[0] = (const uint8_t *)lw->ffn_gate_exps.data;
     ga.w[1] = (const uint8_t *)lw->ffn_up_exps.data;
@@ -598,6 +611,7 @@ int run_moe_at(spt_ctx *ctx, const spt_moe_layer *lw, const float *x, float *out
     ga.act_scales = as;
     ga.act_mxtab = am;
     ga.act_blocks34 = taps ? (uint8_t *)taps->actq : nullptr;
+    ga.start = so.gv_start;
     if ((rc = check_cancel(ctx))) return rc;
     SPT_HIP(timed(ctx, SPT_KERNEL_GATE_UP, [&] { return spt::launch_mx_mfma(s, spt::kGateUp, ga, slots); }));
     // Upper bound of the GEMM work items (token tiles x row units): every
@@ -658,6 +672,7 @@ int run_moe_at(spt_ctx *ctx, const spt_moe_layer *lw, const float *x, float *out
     da.list = so.list;
     da.topk = (int)k;
     da.out = res;
+    da.start = so.gv_start ? so.gv_start + spt::kGvStartMax * spt::kGvStartWords : nullptr;
     if ((rc = check_cancel(ctx))) return rc;
     SPT_HIP(timed(ctx, SPT_KERNEL_DOWN, [&] { return spt::launch_mx_mfma(s, spt::kDown, da, slots); }));
     if (use_gemm) {

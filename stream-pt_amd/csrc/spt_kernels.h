@@ -42,7 +42,17 @@ struct SelectOut {
     int32_t *gm_n;
     int32_t *gm_tile_off;  // [E+1] prefix over GEMM experts of ceil(count / kGemmTokens)
     int32_t *gm_claim;     // [2] work-item counters of the two GEMM launches (zeroed)
+    // Optional start table of the two grouped GEMV launches (gate/up, down):
+    // for workgroup b of launch l, kGvStartWords ints at
+    // gv_start[(l * kGvStartMax + b) * kGvStartWords]: its item range
+    // [w0, w1), the slot, expert and pass of w0 (gv_grid[l] workgroups,
+    // gv_tiles[l] row units per pass).
+    int32_t *gv_start;
+    int32_t gv_grid[2];
+    int32_t gv_tiles[2];
 };
+constexpr int kGvStartMax = 1024;
+constexpr int kGvStartWords = 8;
 
 // Optional Q8_0 outputs of a quantized activation (see write_q8_block);
 // with src34 set, the router's launch unpacks these GGML Q8_0 blocks of the
@@ -90,6 +100,9 @@ struct MxMfmaArgs {
     float *act_scales;
     uint8_t *act_mxtab;
     uint8_t *act_blocks34;
+    // grouped modes, optional: this launch's rows of SelectOut::gv_start
+    // (the launch's grid must be the one they were computed for)
+    const int32_t *start;
 };
 
 // The decode path (spt_mx_decode.hip) for batches of a few tokens with
@@ -258,6 +271,8 @@ hipError_t launch_select(hipStream_t s, const float *logits, int batch, int expe
                          const SelectOut &o);
 // slots: upper bound of the active experts (1 for kRows).
 hipError_t launch_mx_mfma(hipStream_t s, GemvMode mode, const MxMfmaArgs &a, int slots);
+// The grid launch_mx_mfma uses for these arguments (0: nothing to launch).
+int mx_mfma_grid(GemvMode mode, const MxMfmaArgs &a, int slots);
 // max_items: upper bound of the GEMM work items (0: nothing to launch).
 hipError_t launch_mx_gemm(hipStream_t s, GemvMode mode, const MxGemmArgs &a, int max_items);
 // Q4_0 x Q8_0 for a batch: the int8-MFMA GEMM (spt_q40_gemm.hip) from

@@ -130,7 +130,10 @@ constexpr int kSelWords = kSelChunk / 32;
 
 __device__ void pack_lists(int n, int E, const SelectOut &o, const int32_t *s_ids, const float *s_w,
                            int32_t *s_cnt, int32_t *s_off, int32_t *s_run, uint32_t *s_bits) {
-    __shared__ int s_gemm_on;
+    __shared__ int s_gemm_on, s_nv;
+    // the GEMV experts and their pass prefix, for the start table
+    int32_t *s_poff = reinterpret_cast<int32_t *>(s_bits + kSelWords * E);
+    int32_t *s_gva = s_poff + E + 1;
     const int tid = threadIdx.x;
     for (int i = tid; i < E; i += blockDim.x) {
         s_cnt[i] = 0;
@@ -170,6 +173,8 @@ __device__ void pack_lists(int n, int E, const SelectOut &o, const int32_t *s_id
                     const int r = nv + __builtin_popcountll(actv & below);
                     o.gv_active[r] = e;
                     o.gv_pass_off[r] = npass + pincl - np;
+                    s_gva[r] = e;
+                    s_poff[r] = npass + pincl - np;
                 }
             }
             pos += lane63(incl);
@@ -185,6 +190,8 @@ __device__ void pack_lists(int n, int E, const SelectOut &o, const int32_t *s_id
             *o.n_active = na;
             *o.gv_n = nv;
             o.gv_pass_off[nv] = npass;
+            s_poff[nv] = npass;
+            s_nv = nv;
             *o.gm_n = nm;
             o.gm_tile_off[nm] = ntile;
             if (o.gm_claim) {
@@ -221,6 +228,31 @@ __device__ void pack_lists(int n, int E, const SelectOut &o, const int32_t *s_id
             o.gm_tile_off[rank] = pre;
         }
     }
+    // Start table of the two GEMV launches (threads [0, G0) the first,
+    // [G0, G0 + G1) the second): workgroup b of G takes items
+    // [b W / G, (b + 1) W / G) of the W = passes x row units, from the slot
+    // holding the pass of its first item (the last slot whose pass prefix is
+    // at most that pass).  Written before the lists, so the stores' latency
+    // overlaps them.
+    if (o.gv_start) {
+        const int nv = s_nv, P = s_poff[nv];
+        for (int i = tid; i < o.gv_grid[0] + o.gv_grid[1]; i += blockDim.x) {
+            const int l = i < o.gv_grid[0] ? 0 : 1, b = i - (l ? o.gv_grid[0] : 0);
+            const int G = o.gv_grid[l], tiles = o.gv_tiles[l];
+            const int W = P * tiles;
+            const int w0 = (int)((int64_t)b * W / G), w1 = (int)((int64_t)(b + 1) * W / G);
+            const int q0 = tiles > 0 ? w0 / tiles : 0;
+            int lo = 0, hi = nv - 1;
+            while (lo < hi) {
+                const int mid = (lo + hi + 1) >> 1;
+                if (s_poff[mid] <= q0) lo = mid;
+                else hi = mid - 1;
+            }
+            int32_t *d = o.gv_start + ((size_t)l * kGvStartMax + b) * kGvStartWords;
+            *reinterpret_cast<int4 *>(d) = make_int4(w0, w1, lo, nv > 0 ? s_gva[lo] : 0);
+            d[4] = nv > 0 ? q0 - s_poff[lo] : 0;
+        }
+    }
     for (int p0 = 0; p0 < n; p0 += kSelChunk) {
         for (int i = tid; i < E * kSelWords; i += blockDim.x) s_bits[i] = 0u;
         __syncthreads();
@@ -248,7 +280,8 @@ __device__ void pack_lists(int n, int E, const SelectOut &o, const int32_t *s_id
 }
 
 static size_t select_lds(int n, int E) {
-    return sizeof(int32_t) * (2 * (size_t)n + 3 * (size_t)E + 1) + sizeof(uint32_t) * kSelWords * (size_t)E;
+    return sizeof(int32_t) * (2 * (size_t)n + 3 * (size_t)E + 1) + sizeof(uint32_t) * kSelWords * (size_t)E +
+           sizeof(int32_t) * (2 * (size_t)E + 1);
 }
 
 // Router logits for batches of more than kRouteLdsMaxBatch tokens: a

@@ -235,23 +235,40 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(2))) void k
     const int tile_rows = kUnitRows;
     const int tiles = (a.rows + tile_rows - 1) / tile_rows;
     const Route rt{r_active, r_offsets, r_pass_off, r_list};
-    const int n_slots = MODE == kRows ? 1 : *r_n_active;
-    const int P = MODE == kRows ? (a.ntok + kTokPerPass - 1) / kTokPerPass : rt.pass_off[n_slots];
-    const int W = P * tiles;
-    const int w0 = (int)((int64_t)blockIdx.x * W / gridDim.x);
-    const int w1 = (int)((int64_t)(blockIdx.x + 1) * W / gridDim.x);
-    if (w0 >= w1) return;
-    // slot of the first item: the number of pass_off[s] <= w0 / tiles, minus 1
-    const int q0 = w0 / tiles;
-    int slot0 = 0;
-    if (MODE != kRows) {
-        int ones = 0;
-        for (int s0 = 0; s0 <= n_slots; s0 += kWG) {
-            const int sidx = s0 + tid;
-            ones += __syncthreads_count(sidx <= n_slots && rt.pass_off[sidx] <= q0);
+    // The workgroup's item range and its first item's slot, expert and
+    // pass: one load from the start table the packing wrote when there is
+    // one, else found here (the expert count, the pass total and the slot
+    // scan: three dependent round trips before the first weight load).
+    const bool table = MODE != kRows && a.start != nullptr;
+    int w0, w1, slot0 = 0, e0 = a.expert, p0 = 0;
+    if (table) {
+        const int32_t *st = a.start + (size_t)blockIdx.x * kGvStartWords;
+        w0 = st[0];
+        w1 = st[1];
+        slot0 = st[2];
+        e0 = st[3];
+        p0 = st[4];
+        if (w0 >= w1) return;
+    } else {
+        const int n_slots = MODE == kRows ? 1 : *r_n_active;
+        const int P = MODE == kRows ? (a.ntok + kTokPerPass - 1) / kTokPerPass : rt.pass_off[n_slots];
+        const int W = P * tiles;
+        w0 = (int)((int64_t)blockIdx.x * W / gridDim.x);
+        w1 = (int)((int64_t)(blockIdx.x + 1) * W / gridDim.x);
+        if (w0 >= w1) return;
+        // slot of the first item: the number of pass_off[s] <= w0 / tiles, minus 1
+        if (MODE != kRows) {
+            const int q = w0 / tiles;
+            int ones = 0;
+            for (int s0 = 0; s0 <= n_slots; s0 += kWG) {
+                const int sidx = s0 + tid;
+                ones += __syncthreads_count(sidx <= n_slots && rt.pass_off[sidx] <= q);
+            }
+            slot0 = ones - 1;
+            e0 = rt.active[slot0];
         }
-        slot0 = ones - 1;
     }
+    const int q0 = w0 / tiles;
 
     // matrix and first row (within the unit) of each row tile
     auto tile_m = [](int r) { return MODE == kGateUp ? (r >> 1) : 0; };
@@ -286,7 +303,7 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(2))) void k
     // The first unit's expert is all its tile loads need: they are issued
     // before its pass and token list are read (two dependent round trips
     // fewer before the first weights are in flight).
-    cur.e = MODE == kRows ? a.expert : rt.active[slot0];
+    cur.e = e0;
 
     // Registers of the next unit: this wave's groups of its tile image, and
     // the bias words of this thread's row.
@@ -436,7 +453,7 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(2))) void k
     issue(std::integral_constant<int, 0>{});
     issue(std::integral_constant<int, 1>{});
     issue(std::integral_constant<int, 2>{});
-    cur.p = MODE == kRows ? q0 : q0 - rt.pass_off[slot0];
+    cur.p = MODE == kRows ? q0 : table ? p0 : q0 - rt.pass_off[slot0];
     slot_info<MODE>(a, rt, cur);
     PassTokens npt = pass_tokens<MODE>(a, rt, cur);  // tokens of the unit in the registers
 
@@ -575,6 +592,23 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(2))) void k
     if (n_staged > 0) flush(kStage * cur_set, n_staged);
 }
 
+int mx_mfma_grid(GemvMode mode, const MxMfmaArgs &a, int slots) {
+    if (slots <= 0 || a.rows <= 0) return 0;
+    static int n_cu = 0;
+    if (n_cu == 0) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n_cu <= 0)
+            n_cu = 256;
+    }
+    // Upper bound of the work items: every selection its own pass.
+    const int tile_rows = mode == kGateUp ? 32 : 64;
+    const int max_passes = mode == kRows ? (a.ntok + kTokPerPass - 1) / kTokPerPass : slots;
+    const int64_t items = (int64_t)max_passes * ((a.rows + tile_rows - 1) / tile_rows);
+    // one workgroup of eight waves per CU (its LDS holds four tile images)
+    return items < n_cu ? (int)items : n_cu;
+}
+
 hipError_t launch_mx_mfma(hipStream_t s, GemvMode mode, const MxMfmaArgs &a, int slots) {
     if (slots <= 0 || a.rows <= 0) return hipSuccess;
     if (a.nb <= 0 || a.nb > kMaxNb) return hipErrorInvalidConfiguration;
@@ -593,19 +627,8 @@ hipError_t launch_mx_mfma(hipStream_t s, GemvMode mode, const MxMfmaArgs &a, int
         return e;
     }();
     if (attr != hipSuccess) return attr;
-    static int n_cu = 0;
-    if (n_cu == 0) {
-        int dev = 0;
-        if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n_cu <= 0)
-            n_cu = 256;
-    }
-    // Upper bound of the work items: every selection its own pass.
-    const int tile_rows = mode == kGateUp ? 32 : 64;
-    const int max_passes = mode == kRows ? (a.ntok + kTokPerPass - 1) / kTokPerPass : slots;
-    const int64_t items = (int64_t)max_passes * ((a.rows + tile_rows - 1) / tile_rows);
-    // one workgroup of eight waves per CU (its LDS holds four tile images)
-    const int grid = items < n_cu ? (int)items : n_cu;
+    const int grid = mx_mfma_grid(mode, a, slots);
+    if (a.start && grid > kGvStartMax) return hipErrorInvalidConfiguration;
     if (mode == kGateUp) {
         hipLaunchKernelGGL(k_mx_mfma<kGateUp>, dim3(grid), dim3(kWG), lds, s, a, a.active, a.offsets, a.pass_off,
                            a.list, a.n_active);
