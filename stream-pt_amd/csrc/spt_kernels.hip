@@ -729,24 +729,54 @@ hipError_t launch_q40_gemv(hipStream_t s, const Q40Args &a) {
 // Weighted combine (forward/moe_batch.go:163-192): out = 0, then for ranks
 // 0..k-1 with weight > 0, out = fma(result, weight, out).
 // ---------------------------------------------------------------------------
+// Four outputs per thread; each group of four ranks' weights and results is
+// loaded at once (a skipped rank's results are read and not used), then
+// applied in rank order.  OUT16: the output is 16-byte aligned (else four
+// dword stores).
+template <bool OUT16>
 __global__ __launch_bounds__(kWG) void k_combine(const float *__restrict__ results,
                                                  const float *__restrict__ weights, int topk,
                                                  int H, float *__restrict__ out) {
-    const int i = blockIdx.x * kWG + threadIdx.x, t = blockIdx.y;
+    const int i = 4 * (blockIdx.x * kWG + threadIdx.x), t = blockIdx.y;
     if (i >= H) return;
-    float o = 0.0f;
-    for (int r = 0; r < topk; r++) {
-        float w = weights[t * topk + r];
-        if (w <= 0.0f) continue;
-        o = __builtin_fmaf(results[(size_t)(t * topk + r) * H + i], w, o);
+    float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int r0 = 0; r0 < topk; r0 += 4) {
+        float w[4];
+        float4 v[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int r = min(r0 + j, topk - 1);
+            w[j] = weights[t * topk + r];
+            v[j] = *reinterpret_cast<const float4 *>(results + (size_t)(t * topk + r) * H + i);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            if (r0 + j >= topk || w[j] <= 0.0f) continue;
+            o.x = __builtin_fmaf(v[j].x, w[j], o.x);
+            o.y = __builtin_fmaf(v[j].y, w[j], o.y);
+            o.z = __builtin_fmaf(v[j].z, w[j], o.z);
+            o.w = __builtin_fmaf(v[j].w, w[j], o.w);
+        }
     }
-    out[(size_t)t * H + i] = o;
+    float *d = out + (size_t)t * H + i;
+    if constexpr (OUT16) {
+        *reinterpret_cast<float4 *>(d) = o;
+    } else {
+        d[0] = o.x;
+        d[1] = o.y;
+        d[2] = o.z;
+        d[3] = o.w;
+    }
 }
 
 hipError_t launch_combine(hipStream_t s, const float *results, const float *weights, int batch,
                           int topk, int hidden, float *out) {
-    dim3 grid((hidden + kWG - 1) / kWG, batch);
-    hipLaunchKernelGGL(k_combine, grid, dim3(kWG), 0, s, results, weights, topk, hidden, out);
+    if (hidden % 4 != 0) return hipErrorInvalidValue;  // hidden is a multiple of the 32-element block
+    dim3 grid((hidden / 4 + kWG - 1) / kWG, batch);
+    if ((reinterpret_cast<uintptr_t>(out) & 15u) == 0)
+        hipLaunchKernelGGL(k_combine<true>, grid, dim3(kWG), 0, s, results, weights, topk, hidden, out);
+    else
+        hipLaunchKernelGGL(k_combine<false>, grid, dim3(kWG), 0, s, results, weights, topk, hidden, out);
     return hipGetLastError();
 }
 

@@ -340,3 +340,29 @@ def test_route_select_gpt_oss_router(gpu_ctx, O, batch):
         g = _host(t)
         g["out"] = out.cpu().numpy()
         check_stagewise(O, lay, x, batch, g, sample=[])
+
+
+@pytest.mark.parametrize("batch", [5, 37])
+def test_moe_output_any_alignment(gpu_ctx, O, batch):
+    """The combine writes four outputs per thread with one 16-byte store
+    when the caller's output is 16-byte aligned and with four dword stores
+    otherwise: an output 4 bytes past a 16-byte boundary gets the same bits,
+    and the words around it are untouched."""
+    import torch
+
+    lay = moe_batch_fixture(96, 64, 8, 2, 0, "normal")
+    keep, cfg, lw = device_moe_layer(lay)
+    H = lay["hidden"]
+    x = moe_batch_x(batch, H, "normal")
+    xd = torch.from_numpy(x).cuda()
+    a = torch.full((batch * H,), 999.0, dtype=torch.float32, device="cuda")
+    buf = torch.full((batch * H + 8,), 777.0, dtype=torch.float32, device="cuda")
+    b = buf[1:1 + batch * H]
+    assert b.data_ptr() % 16 == 4
+    gpu_ctx.forward_moe_batch(cfg, lw, xd, a, batch)
+    gpu_ctx.forward_moe_batch(cfg, lw, xd, b, batch)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(a.cpu().numpy()), bits(b.cpu().numpy()))
+    h = buf.cpu().numpy()
+    assert h[0] == 777.0 and np.all(h[1 + batch * H:] == 777.0)
+    assert_close(a.cpu().numpy(), O.forward_moe_batch(lay, x, batch, q8=True), what="aligned output")
