@@ -863,12 +863,15 @@ struct Q40Proj {
     float *resid;
 };
 
-// The int8-MFMA GEMM forms (launch_q40_gemv's choice): 64 tokens and more
-// on 1024 rows and more, or 256 tokens and more on narrower projections (K
-// split kQ40SplitK ways through partial sums in the arena).
-bool q40_gemm_form(int64_t out, int64_t batch) {
-    return (batch >= spt::kQ40GemmMinTokens && out >= spt::kQ40GemmMinRows) ||
-           (batch >= spt::kQ40SplitMinTokens && out < spt::kQ40GemmMinRows);
+// The int8-MFMA GEMM forms and their split-K subset: spt::q40_gemm_form
+// and spt::q40_gemm_split (launch_q40_gemv's choice).
+bool q40_gemm_form(int64_t out, int64_t batch) { return spt::q40_gemm_form(out, batch); }
+bool q40_split(int64_t out, int64_t batch) { return spt::q40_gemm_split(out, batch); }
+
+// The launch of each of the np <= 3 projections of a call over one input:
+// 0 the GEMV, 1 the GEMM, 2 the split-K GEMM.
+void q40_launches(const Q40Proj *p, int np, int64_t batch, int *k) {
+    for (int i = 0; i < np; i++) k[i] = !q40_gemm_form(p[i].out, batch) ? 0 : !q40_split(p[i].out, batch) ? 1 : 2;
 }
 
 // Arena layout of a Q4_0 call over np projections sharing one input.  The
@@ -887,11 +890,13 @@ Q40Plan q40_plan(const Q40Proj *p, int np, int64_t nb, int64_t batch, bool q8_in
     bool gemm = false;
     size_t part = 0;
     L.dec = spt::q40_dec_form(batch, nb);
+    int k[3];
+    q40_launches(p, np, batch, k);
     for (int i = 0; i < np; i++) {
         if (p[i].w->nbytes >= spt::kQ40DecMaxBytes) L.dec = false;
-        if (!q40_gemm_form(p[i].out, batch)) continue;
+        if (k[i] == 0) continue;
         gemm = true;
-        if (p[i].out < spt::kQ40GemmMinRows) part += (size_t)spt::kQ40SplitK * batch * p[i].out * 4;
+        if (k[i] == 2) part += (size_t)spt::kQ40SplitK * batch * p[i].out * 4;
     }
     L.views = !L.dec && (!q8_in || gemm);
     L.nb = nb;
@@ -926,10 +931,11 @@ int run_q40_at(spt_ctx *ctx, const Q40Proj *p, int np, const Q40Plan &L, char *S
     int rc;
     // the three launches' arguments: 0 GEMV, 1 wide GEMM, 2 split GEMM
     spt::Q40Args g[3]{};
-    int ng[3] = {0, 0, 0};
+    int ng[3] = {0, 0, 0}, kl[3];
+    q40_launches(p, np, batch, kl);
     for (int i = 0; i < np; i++) {
         const spt_tensor *w = p[i].w;
-        const int k = !q40_gemm_form(p[i].out, batch) ? 0 : p[i].out >= spt::kQ40GemmMinRows ? 1 : 2;
+        const int k = kl[i];
         if (ng[k] == 0) {
             g[k] = spt::Q40Args{(const uint8_t *)w->data, w->nbytes, (int)p[i].out, (int)nb, codes, scales, sumq,
                                 (int)batch, p[i].y, p[i].bias, p[i].btype, p[i].resid,

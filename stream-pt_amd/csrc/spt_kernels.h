@@ -275,17 +275,31 @@ hipError_t launch_mx_mfma(hipStream_t s, GemvMode mode, const MxMfmaArgs &a, int
 int mx_mfma_grid(GemvMode mode, const MxMfmaArgs &a, int slots);
 // max_items: upper bound of the GEMM work items (0: nothing to launch).
 hipError_t launch_mx_gemm(hipStream_t s, GemvMode mode, const MxGemmArgs &a, int max_items);
-// Q4_0 x Q8_0 for a batch: the int8-MFMA GEMM (spt_q40_gemm.hip) from
-// kQ40GemmMinTokens tokens and kQ40GemmMinRows output rows (narrower
-// projections give it too few 64-row tiles to fill the device), else the
-// GEMV.
-constexpr int kQ40GemmMinTokens = 64;
+// Q4_0 x Q8_0 for a batch: the int8-MFMA GEMM (spt_q40_gemm.hip, tiles of
+// kQ40TileRows rows x kQ40TileTokens tokens) from kQ40GemmMinTokens tokens
+// on kQ40GemmMinRows output rows and more, and from kQ40SplitMinTokens
+// tokens on narrower projections; else the GEMV.  The GEMM splits K
+// kQ40SplitK ways (partial sums in Q40Args::part, then summed in order,
+// when the caller provides the scratch) for narrow projections and for wide
+// ones of fewer than kQ40SplitMaxTiles tiles (too few to fill the device).
+// Unsplit, its sums are the GEMV's bit for bit; split, the partial sums of
+// the K ranges are added in range order (within rounding of the GEMV).
+constexpr int kQ40TileRows = 64;
+constexpr int kQ40TileTokens = 64;
+constexpr int kQ40GemmMinTokens = 32;
 constexpr int kQ40GemmMinRows = 1024;
-// Narrower projections of kQ40SplitMinTokens tokens and more: the GEMM with
-// K split kQ40SplitK ways (partial sums in Q40Args::part, then summed in
-// order), when the caller provides the scratch.
 constexpr int kQ40SplitK = 4;
-constexpr int kQ40SplitMinTokens = 256;
+constexpr int kQ40SplitMinTokens = 32;
+constexpr int kQ40SplitMaxTiles = 256;
+inline bool q40_gemm_form(int64_t rows, int64_t ntok) {
+    return (ntok >= kQ40GemmMinTokens && rows >= kQ40GemmMinRows) ||
+           (ntok >= kQ40SplitMinTokens && rows < kQ40GemmMinRows);
+}
+inline bool q40_gemm_split(int64_t rows, int64_t ntok) {
+    return rows < kQ40GemmMinRows ||
+           ((rows + kQ40TileRows - 1) / kQ40TileRows) * ((ntok + kQ40TileTokens - 1) / kQ40TileTokens) <
+               kQ40SplitMaxTiles;
+}
 // The GEMV stages its tokens' activations (40 bytes per block) in at most
 // kQ40GemvLds bytes of LDS, at least one token per pass: inputs up to
 // kQ40MaxInput elements.

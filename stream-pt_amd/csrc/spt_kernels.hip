@@ -711,12 +711,14 @@ hipError_t launch_q40_gemv(hipStream_t s, const Q40Args &a) {
         if (per_lane <= 6) return launch_q40_maxp<6>(s, a);
         return launch_q40_maxp<8>(s, a);
     }
-    if (a.ntok >= kQ40GemmMinTokens && a.rows >= kQ40GemmMinRows) {
+    if (q40_gemm_form(a.rows, a.ntok)) {
+        // split K with the caller's scratch where the form asks for it;
+        // without scratch, wide projections take the GEMM unsplit and
+        // narrow ones the GEMV
         Q40Args g = a;
-        g.part = nullptr;
-        return launch_q40_gemm(s, g);
+        if (!q40_gemm_split(a.rows, a.ntok)) g.part = nullptr;
+        if (g.part || a.rows >= kQ40GemmMinRows) return launch_q40_gemm(s, g);
     }
-    if (a.part && a.ntok >= kQ40SplitMinTokens) return launch_q40_gemm(s, a);
     const int per_lane = (a.nb + 15) / 16;
     if (per_lane <= 1) return launch_q40_maxp<1>(s, a);
     if (per_lane <= 2) return launch_q40_maxp<2>(s, a);

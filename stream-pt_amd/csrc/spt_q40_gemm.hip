@@ -31,6 +31,7 @@ constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kTR = 16 * kWaves;  // rows per workgroup (16 per wave)
 constexpr int kTN = 64;           // tokens per workgroup (4 fragments)
+static_assert(kTR == kQ40TileRows && kTN == kQ40TileTokens, "the tiles the split rule counts");
 constexpr int kSeg = 8;           // blocks per K segment (144 bytes of a row)
 constexpr int kAPieces = 10;      // 16-byte loads per row window (144 + 15 <= 160)
 constexpr int kASlots = 11;       // LDS slots of 16 B per staged row (44 dwords: rows over distinct banks)
