@@ -1,5 +1,5 @@
-// spt_q40_gemm.hip -- Q4_0 x Q8_0 GEMM for large batches on the gfx950 int8
-// MFMA (v_mfma_i32_16x16x32_i8).
+// spt_q40_gemm.hip -- Q4_0 x Q8_0 GEMM for batches of 32 tokens and more on
+// the gfx950 int8 MFMA (v_mfma_i32_16x16x32_i8).
 //
 // forward.MulQ40BatchInto (forward/q40.go:40-103) for batches large enough
 // that the projection is a contraction: y[t][row] = sum_b float(isum) *
