@@ -269,6 +269,9 @@ hipError_t launch_pack(hipStream_t s, int batch, int experts, int topk, const Se
 // Top-k + softmax per token, then the per-expert lists (one workgroup).
 hipError_t launch_select(hipStream_t s, const float *logits, int batch, int experts, int topk,
                          const SelectOut &o);
+// Compute units of the current device (queried once per device; 256 if the
+// query fails): the persistent launches size their grids by it.
+int device_cus();
 // slots: upper bound of the active experts (1 for kRows).
 hipError_t launch_mx_mfma(hipStream_t s, GemvMode mode, const MxMfmaArgs &a, int slots);
 // The grid launch_mx_mfma uses for these arguments (0: nothing to launch).

@@ -6,6 +6,8 @@
 // blocks (288 contiguous bytes) per load.  Activations (Q8_0 codes + scales
 // of the workgroup's tokens) are staged in LDS once and shared by the rows.
 // The MXFP4 GEMV lives in spt_mx_mfma.hip.
+#include <atomic>
+
 #include "spt_device.h"
 #include "spt_kernels.h"
 #include "spt_select.h"
@@ -501,6 +503,19 @@ __global__ __launch_bounds__(kSelWG) void k_pack(int batch, int E, int topk, Sel
     }
     __syncthreads();
     pack_lists(n, E, o, s_ids, s_w, s_cnt, s_off, s_run, s_bits);
+}
+
+int device_cus() {
+    constexpr int kMaxCuDevices = 64;
+    static std::atomic<int> cus[kMaxCuDevices];  // 0: not queried yet
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxCuDevices) return 256;
+    int n = cus[dev].load(std::memory_order_relaxed);
+    if (n == 0) {
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cus[dev].store(n, std::memory_order_relaxed);
+    }
+    return n;
 }
 
 hipError_t launch_route(hipStream_t s, const float *router, const void *bias, int bias_type,

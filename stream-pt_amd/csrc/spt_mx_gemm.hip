@@ -717,13 +717,7 @@ hipError_t launch_mx_gemm(hipStream_t s, GemvMode mode, const MxGemmArgs &a, int
         return e;
     }();
     if (attr != hipSuccess) return attr;
-    static int n_cu = 0;
-    if (n_cu == 0) {
-        int dev = 0;
-        if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n_cu <= 0)
-            n_cu = 256;
-    }
+    const int n_cu = device_cus();
     const int grid = max_items < n_cu ? max_items : n_cu;
     if (mode == kGateUp)
         hipLaunchKernelGGL(k_mx_gemm<kGateUp>, dim3(grid), dim3(kThreads), lds, s, a);

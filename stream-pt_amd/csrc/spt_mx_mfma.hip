@@ -594,13 +594,7 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(2))) void k
 
 int mx_mfma_grid(GemvMode mode, const MxMfmaArgs &a, int slots) {
     if (slots <= 0 || a.rows <= 0) return 0;
-    static int n_cu = 0;
-    if (n_cu == 0) {
-        int dev = 0;
-        if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n_cu <= 0)
-            n_cu = 256;
-    }
+    const int n_cu = device_cus();
     // Upper bound of the work items: every selection its own pass.
     const int tile_rows = mode == kGateUp ? 32 : 64;
     const int max_passes = mode == kRows ? (a.ntok + kTokPerPass - 1) / kTokPerPass : slots;
