@@ -39,6 +39,11 @@ struct spt_ctx {
     int32_t gemm_min_group = 0;  // 0: the default policy (kGemmMinGroup)
     int32_t decode_max_selections = 0;  // 0: kDecodeMaxSelections; < 0: decode path off
     int n_cu = 0;                // compute units of the device
+    // A second stream of the device and two events: a layer's grouped GEMM
+    // launches run there beside its GEMV launches (fork after the
+    // selection, join before the combine).  Null: everything on `stream`.
+    hipStream_t side = nullptr;
+    hipEvent_t ev_fork = nullptr, ev_join = nullptr;
 };
 
 // Scratch of spt_forward_moe_batch_noalloc: a fixed device array, one copy
@@ -613,6 +618,26 @@ int run_moe_at(spt_ctx *ctx, const spt_moe_layer *lw, const float *x, float *out
     ga.act_blocks34 = taps ? (uint8_t *)taps->actq : nullptr;
     ga.start = so.gv_start;
     if ((rc = check_cancel(ctx))) return rc;
+    // The grouped GEMM (its own experts, act rows and results) on the side
+    // stream from here to the combine, so its launches fill the CUs the
+    // GEMV launches leave idle and the reverse; with timing on, in line.
+    // The join is recorded however the call ends.
+    struct Join {
+        spt_ctx *ctx;
+        hipStream_t s;
+        bool on = false;
+        ~Join() {
+            if (on && hipEventRecord(ctx->ev_join, ctx->side) == hipSuccess)
+                (void)hipStreamWaitEvent(s, ctx->ev_join, 0);
+        }
+    } join{ctx, s};
+    hipStream_t sg = s;
+    if (use_gemm && ctx->side && !ctx->timing) {
+        SPT_HIP(hipEventRecord(ctx->ev_fork, s));
+        SPT_HIP(hipStreamWaitEvent(ctx->side, ctx->ev_fork, 0));
+        sg = ctx->side;
+        join.on = true;
+    }
     SPT_HIP(timed(ctx, SPT_KERNEL_GATE_UP, [&] { return spt::launch_mx_mfma(s, spt::kGateUp, ga, slots); }));
     // Upper bound of the GEMM work items (token tiles x row units): every
     // GEMM expert holds at least gemm_min selections.
@@ -651,7 +676,7 @@ int run_moe_at(spt_ctx *ctx, const spt_moe_layer *lw, const float *x, float *out
         const int64_t items = gm_tiles * ((d + 127) / 128);
         if ((rc = check_cancel(ctx))) return rc;
         SPT_HIP(timed(ctx, SPT_KERNEL_GATE_UP_GEMM, [&] {
-            return spt::launch_mx_gemm(s, spt::kGateUp, gg, (int)std::min<int64_t>(items, INT_MAX));
+            return spt::launch_mx_gemm(sg, spt::kGateUp, gg, (int)std::min<int64_t>(items, INT_MAX));
         }));
     }
     spt::MxMfmaArgs da{};
@@ -698,8 +723,13 @@ int run_moe_at(spt_ctx *ctx, const spt_moe_layer *lw, const float *x, float *out
         const int64_t items = gm_tiles * ((h + 255) / 256);
         if ((rc = check_cancel(ctx))) return rc;
         SPT_HIP(timed(ctx, SPT_KERNEL_DOWN_GEMM, [&] {
-            return spt::launch_mx_gemm(s, spt::kDown, gd, (int)std::min<int64_t>(items, INT_MAX));
+            return spt::launch_mx_gemm(sg, spt::kDown, gd, (int)std::min<int64_t>(items, INT_MAX));
         }));
+    }
+    if (join.on) {
+        join.on = false;
+        SPT_HIP(hipEventRecord(ctx->ev_join, sg));
+        SPT_HIP(hipStreamWaitEvent(s, ctx->ev_join, 0));
     }
     if ((rc = check_cancel(ctx))) return rc;
     SPT_HIP(timed(ctx, SPT_KERNEL_COMBINE, [&] { return spt::launch_combine(s, res, so.weights, (int)B, (int)k, (int)h, out); }));
@@ -1131,6 +1161,17 @@ int spt_ctx_create(int device, void *hip_stream, spt_ctx **out) {
             ctx->n_cu = 256;
         // with the device current: its copy of the no-allocation scratch
         noalloc_scratch_of(device, &ctx->noalloc, &ctx->noalloc_err);
+        // the side stream (default priority) and its fork / join events; if
+        // any of them cannot be made, layers run on the one stream
+        if (hipStreamCreateWithFlags(&ctx->side, hipStreamNonBlocking) != hipSuccess ||
+            hipEventCreateWithFlags(&ctx->ev_fork, hipEventDisableTiming) != hipSuccess ||
+            hipEventCreateWithFlags(&ctx->ev_join, hipEventDisableTiming) != hipSuccess) {
+            if (ctx->side) (void)hipStreamDestroy(ctx->side);
+            if (ctx->ev_fork) (void)hipEventDestroy(ctx->ev_fork);
+            if (ctx->ev_join) (void)hipEventDestroy(ctx->ev_join);
+            ctx->side = nullptr;
+            ctx->ev_fork = ctx->ev_join = nullptr;
+        }
     }
     *out = ctx;
     return SPT_OK;
@@ -1148,6 +1189,12 @@ int spt_ctx_destroy(spt_ctx *ctx) {
             (void)hipEventDestroy(p.second.second);
         }
         for (hipEvent_t e : ctx->free_events) (void)hipEventDestroy(e);
+        if (ctx->side) {
+            (void)hipStreamSynchronize(ctx->side);
+            (void)hipStreamDestroy(ctx->side);
+            (void)hipEventDestroy(ctx->ev_fork);
+            (void)hipEventDestroy(ctx->ev_join);
+        }
         if (ctx->own_stream) (void)hipStreamDestroy(ctx->stream);
     }
     delete ctx;

@@ -366,3 +366,49 @@ def test_moe_output_any_alignment(gpu_ctx, O, batch):
     h = buf.cpu().numpy()
     assert h[0] == 777.0 and np.all(h[1 + batch * H:] == 777.0)
     assert_close(a.cpu().numpy(), O.forward_moe_batch(lay, x, batch, q8=True), what="aligned output")
+
+
+def test_moe_gemm_side_stream_in_graph(O):
+    """With the grouped GEMM on (every group), a layer forks its GEMM
+    launches onto the context's second stream and joins them before the
+    combine.  Captured into a HIP graph on the context's stream and replayed
+    three times, with eager calls of another batch between the replays,
+    every replay's output equals the eager call's bit for bit (the fork and
+    the join are part of the graph), and the eager output matches the
+    oracle."""
+    import torch
+
+    import spt
+
+    stream = torch.cuda.Stream()
+    ctx = spt.Context(0, stream.cuda_stream)
+    try:
+        with gemm_path(ctx, "gemm"):
+            lay = moe_batch_fixture(96, 64, 8, 2, 0, "normal")
+            keep, cfg, lw = device_moe_layer(lay)
+            H = lay["hidden"]
+            batch = 37
+            x = moe_batch_x(batch, H, "normal")
+            other = moe_batch_x(11, H, "normal")
+            with torch.cuda.stream(stream):
+                xd = torch.from_numpy(x).cuda()
+                od = torch.from_numpy(other).cuda()
+                ref = torch.empty(batch * H, dtype=torch.float32, device="cuda")
+                out = torch.empty(batch * H, dtype=torch.float32, device="cuda")
+                oo = torch.empty(11 * H, dtype=torch.float32, device="cuda")
+                ctx.forward_moe_batch(cfg, lw, xd, ref, batch)
+                stream.synchronize()
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g, stream=stream):
+                    ctx.forward_moe_batch(cfg, lw, xd, out, batch)
+                for _ in range(3):
+                    out.fill_(999.0)
+                    g.replay()
+                    stream.synchronize()
+                    assert np.array_equal(bits(out.cpu().numpy()), bits(ref.cpu().numpy()))
+                    ctx.forward_moe_batch(cfg, lw, od, oo, 11)
+                    stream.synchronize()
+                del g
+        assert_close(ref.cpu().numpy(), O.forward_moe_batch(lay, x, batch, q8=True), what="gemm path, side stream")
+    finally:
+        ctx.close()
