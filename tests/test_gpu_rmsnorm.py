@@ -58,7 +58,7 @@ def test_rmsnorm_formats(gpu_ctx, O, typ, inplace):
     _same_bits(y, O.rmsnorm_batch_f32(x, w, 1, 1e-5))
 
 
-@pytest.mark.parametrize("n", [1, 7, 8, 31, 32, 33, 96, 2880, 4097])
+@pytest.mark.parametrize("n", [1, 7, 8, 31, 32, 33, 96, 256, 1056, 2048, 2880, 4097, 8192, 8224])
 def test_rmsnorm_ragged_lengths(gpu_ctx, O, n):
     from spt import synth
 
