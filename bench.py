@@ -421,6 +421,22 @@ def prefill(args, ctx, dl, shp, W, stream, reps=20):
     return out
 
 
+def warm(fn, seconds=0.03, min_calls=3, sync_every=16):
+    """Calls fn back to back for at least `seconds` of wall time (and at
+    least min_calls times), so that the timed calls after it run in steady
+    state rather than right after host-side set-up."""
+    import torch
+
+    t_end = time.perf_counter() + seconds
+    n = 0
+    while n < min_calls or time.perf_counter() < t_end:
+        fn()
+        n += 1
+        if n % sync_every == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+
+
 def q40_projections(ctx, B, W, stream, reps):
     """Q4_0 x Q8_0 attention projections of one layer (Q 2880->4096,
     K/V 2880->512, O 4096->2880; fp16 scales |N(0,0.01)|, uniform nibbles)
@@ -436,9 +452,7 @@ def q40_projections(ctx, B, W, stream, reps):
         t = spt.Tensor.make(name, spt.TYPE_Q4_0, [din, dout], wb.data_ptr(), wb.numel())
         xq = torch.from_numpy(synth.normal(synth.stream_key(50 + i, B), B * din)).cuda()
         yq = torch.empty(B * dout, dtype=torch.float32, device="cuda")
-        for _ in range(3):
-            ctx.mul_q40_batch_into(t, xq, yq, B)
-        torch.cuda.synchronize()
+        warm(lambda: ctx.mul_q40_batch_into(t, xq, yq, B))
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record(stream)
         for _ in range(reps):
@@ -482,9 +496,7 @@ def q40_fused(ctx, B, W, stream, reps):
         ctx.mul_q40_qkv_batch_into(ts[:3], None, None, ys, B, xq=xq, x_len=B * H)
         ctx.mul_q40_batch_into(ts[3], ctxv, yo, B)
 
-    for _ in range(3):
-        run()
-    torch.cuda.synchronize()
+    warm(run)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(stream)
     for _ in range(reps):
@@ -532,10 +544,11 @@ def lm_head(ctx, stream, reps=20, rows=201088, input_dim=2880):
     t = spt.Tensor.make("output.weight", spt.TYPE_Q8_0, [input_dim, rows], wb.data_ptr(), wb.numel())
     x = torch.from_numpy(synth.normal(synth.stream_key(61, 0), input_dim)).cuda()
     y = torch.empty(rows, dtype=torch.float32, device="cuda")
-    for _ in range(3):
+    def both():
         ctx.mul_q80_into(t, x, y)
         ctx.mul_q80_argmax(t, x)
-    torch.cuda.synchronize()
+
+    warm(both, sync_every=2)
     res = {"rows": rows, "input": input_dim, "matrix_bytes": wb.numel()}
     for name, call, extra in (("into", lambda: ctx.mul_q80_into(t, x, y), rows * 4),
                               ("argmax", lambda: ctx.mul_q80_argmax(t, x), 0)):
@@ -571,8 +584,7 @@ def rmsnorm_rows(ctx, stream, reps=50, dim=2880):
         x = torch.from_numpy(synth.normal(synth.stream_key(91, B), B * dim)).cuda()
         y = torch.empty_like(x)
         q = torch.empty(B * dim // 32 * 34, dtype=torch.uint8, device="cuda")
-        for _ in range(3):
-            ctx.rmsnorm_batch_into(t, x, y, B, 1e-5, q)
+        warm(lambda: ctx.rmsnorm_batch_into(t, x, y, B, 1e-5, q))
         ctx.enable_timing(True)
         ctx.read_timing()
         for _ in range(reps):
