@@ -14,9 +14,13 @@
 // carries digit `part` (h with B scale 2^4, l with 2^0) of token `slot`'s
 // block g, zero elsewhere.  So D[r][c] = 2^(e-127) * 2^(4 or 0) * sum(E2M1*digit)
 // exactly, and D[r][g] + D[r][g+4] = 2^(e-127) * sum(E2M1*q) exactly: the same
-// value as the integer form isum * 2^(e-128) (isum = sum of 2*E2M1*q).  The
-// activation scale d_x is applied per block with one FMA:
-//   acc = fma(D_h + D_l, d_x, acc)  ==  fma(float(isum), d_x * 2^(e-128), acc).
+// value as the integer form isum * 2^(e-128) (isum = sum of 2*E2M1*q).  Each
+// lane applies the activation scale to its own digit column,
+//   acc = fma(D_part, d_x, acc),
+// and the product is exact (D_part has at most 13 significant bits, the fp16
+// d_x at most 11), so what rounds is only the fp32 adding of the two digit
+// halves and of the blocks, in the lanes' and waves' order: with one block
+// the result is the single rounding of isum * d_x * 2^(e-128).
 // Rows of a 16-row tile that contain an E8M0 outside [4, 240] are computed
 // with the integer LUT decode instead, so the results keep the reference's
 // special-value semantics: 255 is the +Inf scale, and above 240 a D value

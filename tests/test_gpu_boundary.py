@@ -118,12 +118,13 @@ def test_q40_few_tokens_quantize_in_launch(gpu_ctx, O, batch):
         assert_close(ya.cpu().numpy()[:(batch - 1) * dout], want, what="few-token projection")
 
 
-@pytest.mark.parametrize("batch", [1, 3, 32, 300])
+@pytest.mark.parametrize("batch", [1, 3, 32, 300, 512])
 @pytest.mark.parametrize("form", ["fp32", "q8"])
 def test_q40_qkv_fused(gpu_ctx, O, batch, form):
     """The Q, K, V projections of one normed input in one call (one
     quantization or none, one GEMV launch for all three below the GEMM batch
-    sizes): each output bit-equal to its own MulQ40BatchInto + bias call."""
+    sizes): each output bit-equal to its own MulQ40BatchInto + bias call,
+    and each against the oracle (at 512 tokens: the long-prompt chunk)."""
     import torch
 
     from spt import synth
@@ -150,10 +151,13 @@ def test_q40_qkv_fused(gpu_ctx, O, batch, form):
     torch.cuda.synchronize()
     for i in range(3):
         assert np.array_equal(bits(ys[i].cpu().numpy()), bits(want[i].cpu().numpy())), f"projection {i}"
-    # Q against the oracle
-    w, _, t = mats[0]
-    wq = O.mul_q40_q8(w, x, din, 4096, batch).reshape(batch, 4096) + biases[0][0][None, :]
-    assert_close(ys[0].cpu().numpy(), wq.reshape(-1), what="fused Q")
+    for i, name in enumerate("QKV"):
+        w, _, t = mats[i]
+        dout = int(t.shape[1])
+        want_i = O.mul_q40_q8(w, x, din, dout, batch).reshape(batch, dout)
+        if biases[i] is not None:
+            want_i = want_i + biases[i][0][None, :]
+        assert_close(ys[i].cpu().numpy(), want_i.reshape(-1), what=f"fused {name}")
 
 
 @pytest.mark.parametrize("douts", [(1088, 320, 200), (576, 128, 72), (200, 1100, 90)])

@@ -191,7 +191,7 @@ def test_mxfp4_expert_gemv_odd_half_bias(gpu_ctx, O, bias_type):
     # row counts off the 64-row tile and the 4-row stores, inputs shorter
     # than one 8-block segment and off its multiple
     (2880, 4096, 100), (2880, 512, 64), (4096, 2880, 70), (32, 17, 64), (96, 70, 129),
-    (288, 4, 65), (2880, 512, 512),
+    (288, 4, 65), (2880, 512, 512), (4096, 2880, 512),
     # narrow projections of 256 tokens and up: the GEMM with K split four
     # ways (fewer ways when the input has fewer blocks)
     (96, 70, 300), (32, 17, 256), (4096, 512, 257),
@@ -351,3 +351,43 @@ def test_mxfp4_large_scales_stay_finite(gpu_ctx, O):
     assert_close(got, want, what="large scales vs Q8_0 oracle")
     ref = np.array([math.ldexp(1, s - 127) for s in range(239, 255)], np.float64)
     assert np.all(np.abs(got - ref) <= 1e-3 * ref), "closed form 2^(s-127)"
+
+
+def test_q40_split_batch_dependence(gpu_ctx, O):
+    """The split-K GEMM adds its four K ranges' partial sums in range order,
+    so a token's projection may differ in the last bits from the same token
+    in a batch large enough for the unsplit GEMM: the O projection
+    (4096 -> 2880) of 70 tokens alone (45 x 2 tiles: split) and as the first
+    70 of 512 (45 x 8 tiles: unsplit) agree within the oracle's tolerance,
+    each against the oracle too.  (With exactly representable sums the two
+    agree bit for bit: test_gpu_exact.py.)"""
+    import torch
+
+    import spt
+    from spt import synth
+
+    din, dout = 4096, 2880
+    w = synth.q40_bytes(synth.stream_key(8, dout), dout, din)
+    x = synth.normal(synth.stream_key(12, 512), 512 * din)
+    wd, xd = _dev(w), _dev(x)
+    t = spt.Tensor.make("attn_output", spt.TYPE_Q4_0, [din, dout], wd.data_ptr(), w.size)
+    assert spt_split(dout, 70) and not spt_split(dout, 512)
+    y70 = torch.zeros(70 * dout, dtype=torch.float32, device="cuda")
+    y512 = torch.zeros(512 * dout, dtype=torch.float32, device="cuda")
+    gpu_ctx.mul_q40_batch_into(t, xd[:70 * din], y70, 70)
+    gpu_ctx.mul_q40_batch_into(t, xd, y512, 512)
+    torch.cuda.synchronize()
+    a, b = y70.cpu().numpy(), y512.cpu().numpy()[:70 * dout]
+    want = O.mul_q40_q8(w, x[:70 * din], din, dout, 70)
+    assert_close(a, want, what="split")
+    assert_close(b, want, what="unsplit")
+    e = assert_close(a, b, what="split vs unsplit")
+    ulps = np.abs(a.view(np.int32).astype(np.int64) - b.view(np.int32).astype(np.int64))
+    print(f"split vs unsplit: {np.count_nonzero(ulps)} of {a.size} differ, max {ulps.max()} ulp, rel {e:.2e}")
+
+
+def spt_split(rows, ntok):
+    """The library's split rule (kQ40SplitMaxTiles = 256 tiles of 64 x 64,
+    narrow projections below 1024 rows always)."""
+    tiles = ((rows + 63) // 64) * ((ntok + 63) // 64)
+    return ntok >= 32 and (rows < 1024 or tiles < 256)

@@ -188,3 +188,42 @@ def test_q40_batch_path(O, batch):
     for t in range(batch):
         y1 = O.mul_q40_f32(w, x[t * input_dim:(t + 1) * input_dim], input_dim, output_dim, 1)
         assert np.all(np.abs(yb[t] - y1) <= 1e-4 * (1 + np.abs(y1)))
+
+
+def test_exact_tables_match_oracle(O):
+    """The decode tables tests/exact.py computes the bit-exact tests' expected values
+    from (2 * E2M1 per nibble, low nibble = element i and high = i + 16;
+    Q4_0 n - 8) against the oracle's integer block sums, over every nibble
+    byte at every position and code vectors of both signs, and the E2M1
+    table against the format's values (LEVELS64, the reference's table)."""
+    from exact import LUT2, all_pairs_bytes, exact_dots, mx_matrix, q40_matrix
+
+    assert np.array_equal(LUT2, (2 * LEVELS64).astype(np.int64))
+    rng = np.random.default_rng(11)
+    nib = all_pairs_bytes(256)
+    for q in (np.full(32, 1, np.int8), np.arange(-16, 16, dtype=np.int8) * 7,
+              rng.integers(-127, 128, size=32).astype(np.int8)):
+        lo = LUT2[nib & 15].astype(np.int64)
+        hi = LUT2[nib >> 4].astype(np.int64)
+        mine = lo @ q[:16].astype(np.int64) + hi @ q[16:].astype(np.int64)
+        w = mx_matrix(nib[:, None, :], np.full((256, 1), 127, np.uint8))
+        assert np.array_equal(mine, [O.isum_mxfp4_q8(w[r, 0], q) for r in range(256)])
+        wq = q40_matrix(nib[:, None, :], np.full((256, 1), 0x3C00, np.uint16))
+        qs = (((nib & 15).astype(np.int64) - 8) @ q[:16].astype(np.int64) +
+              ((nib >> 4).astype(np.int64) - 8) @ q[16:].astype(np.int64))
+        assert np.array_equal(qs, [O.isum_q40_q8(wq[r, 0], q) for r in range(256)])
+    # the one-block float64 form against the oracle's row dot (one block,
+    # so the same single rounding), for E8M0 {4, 118, 127, 240} and d_x of
+    # random fp16 values
+    x = (rng.standard_normal((3, 32)) * 40).astype(np.float32)
+    x[:, 0] = 127
+    xq = O.quantize_q8_0(x.reshape(-1)).reshape(3, 1, 34)
+    codes = xq[..., 2:].copy().view(np.int8)
+    d = xq[..., :2].copy().view(np.float16)[..., 0].astype(np.float64)
+    for e in (4, 118, 127, 240):
+        w = mx_matrix(nib[:, None, :], np.full((256, 1), e, np.uint8))
+        vals = np.concatenate([LUT2[w[..., 1:] & 15], LUT2[w[..., 1:] >> 4]], axis=-1)
+        want = exact_dots(vals, np.ldexp(1.0, w[..., 0].astype(np.int64) - 128), codes, d)
+        got = np.array([[O.dot_mxfp4_q8(w[r].reshape(-1), xq[t].reshape(-1)) for r in range(256)]
+                        for t in range(3)], np.float32)
+        assert np.array_equal(got, want), e
