@@ -42,8 +42,7 @@ enum {
     SPT_ERR_DEVICE = 2,   /* HIP runtime error, or a context without device */
     SPT_ERR_NOMEM = 3,    /* device allocation failed                       */
     SPT_ERR_CANCELED = 4, /* cancellation flag was set                      */
-    SPT_ERR_IO = 5,       /* a GGUF file could not be opened or read        */
-    SPT_ERR_NOT_FOUND = 6 /* no tensor / metadata key / span of that name   */
+    SPT_ERR_IO = 5        /* a model file could not be opened or read       */
 };
 
 /* GGML type ids used on this path (ggufindex/index.go:540-551). */
@@ -171,6 +170,12 @@ int spt_ctx_enable_timing(struct spt_ctx *ctx, int enable);
  * kind since the last read (arrays of SPT_KERNEL_KINDS) and reset them. */
 int spt_ctx_read_timing(struct spt_ctx *ctx, double *total_ms, int64_t *launches);
 
+/* Bytes the context holds in its grow-only device scratch arena and in its
+ * pinned host staging (both grow on demand and are kept until
+ * spt_ctx_destroy).  No reference counterpart: memory accounting for a
+ * serving loop, and how a caller checks that a call allocated nothing. */
+int spt_ctx_memory(struct spt_ctx *ctx, uint64_t *arena_bytes, uint64_t *staging_bytes);
+
 /* ---- device memory and weight residency -------------------------------- */
 
 int spt_alloc(struct spt_ctx *ctx, uint64_t nbytes, void **out_dev);
@@ -182,6 +187,21 @@ int spt_copy_d2h(struct spt_ctx *ctx, void *dst_host, const void *src_dev, uint6
  * ggufmap mmap windows (ggufmap/mmap_linux.go:210-291,391-555).  Free with
  * spt_free(ctx, (void *)t->data). */
 int spt_tensor_upload(struct spt_ctx *ctx, spt_tensor *t, const void *src_host);
+
+/* Residency from the model files: the bytes [start, end) of the file at
+ * `path` -- a ggufindex.Tensor's Range (ggufindex/index.go:15-26), as
+ * ggufindex.Open recorded it for the tensor -- copied to a new device
+ * allocation unchanged, read in 8 MiB chunks through the context's pinned
+ * staging (no mmap window is held).  Replaces the per-call streaming of
+ * ggufmap's WithTensorChunks / WithExpertRanges
+ * (ggufmap/mmap_linux.go:239-291,391-555) with residency.  The caller fills
+ * t->name, t->type, t->n_dims (1..4) and t->shape from the ggufindex.Tensor;
+ * for the path's types (F32, F16, BF16, Q4_0, Q8_0, MXFP4) the range must
+ * hold exactly the bytes that type and shape take.  Sets t->nbytes =
+ * end - start and t->data.  SPT_ERR_IO when the file cannot be opened or
+ * ends before `end`; nothing stays allocated on failure.  Free with
+ * spt_free(ctx, (void *)t->data). */
+int spt_upload_range(struct spt_ctx *ctx, const char *path, uint64_t start, uint64_t end, spt_tensor *t);
 
 /* ---- operators ----------------------------------------------------------- */
 
@@ -308,12 +328,19 @@ int spt_forward_moe(struct spt_ctx *ctx, const spt_moe_config *cfg, const spt_mo
 /* forward.forwardMoEBatch (forward/moe_batch.go:76-194): router, top-k
  * softmax, per-expert grouping, gate/up, clamped SwiGLU, down and the
  * weighted combine for batch tokens of x [batch][hidden] into out.
- * x and out must not overlap. */
+ * x and out must not overlap.  Any batch is accepted, as the reference
+ * accepts any (moe_batch.go:29-38,84-90): a batch of more than 4096
+ * selections (batch * experts used) runs as consecutive slices of
+ * 4096 / experts-used whole tokens (1,024 at top-4), each token's output
+ * computed from its own row of x as in one call of that slice.  Limits:
+ * experts used <= 16 and experts <= 256 (SPT_ERR_INVALID beyond). */
 int spt_forward_moe_batch(struct spt_ctx *ctx, const spt_moe_config *cfg,
                           const spt_moe_layer *lw, const float *x_dev, int64_t x_len,
                           float *out_dev, int64_t out_len, int64_t batch);
 
-/* forwardMoEBatch with parity taps / injected logits (taps may be NULL). */
+/* forwardMoEBatch with parity taps / injected logits (taps may be NULL).
+ * With taps the batch holds at most 4096 selections (the taps describe one
+ * launch sequence's lists); without, it is spt_forward_moe_batch. */
 int spt_forward_moe_batch_ex(struct spt_ctx *ctx, const spt_moe_config *cfg,
                              const spt_moe_layer *lw, const float *x_dev, int64_t x_len,
                              float *out_dev, int64_t out_len, int64_t batch,

@@ -10,8 +10,8 @@
 // the library cannot be loaded the program fails: there is no CPU fallback.
 //
 // NOT COMPILED HERE: the environment this library was built in has no Go
-// toolchain.  The C side it calls (include/spt_moe.h, include/spt_gguf.h)
-// is exercised through the same entry points by the Python tests.
+// toolchain.  The C side it calls (include/spt_moe.h) is exercised through
+// the same entry points by the Python tests.
 //
 //go:build spt_gpu
 
@@ -22,7 +22,6 @@ package forward
 #cgo LDFLAGS: -L${SRCDIR}/../third_party/spt/lib -lspt_moe -Wl,-rpath,${SRCDIR}/../third_party/spt/lib
 #include <stdlib.h>
 #include "spt_moe.h"
-#include "spt_gguf.h"
 */
 import "C"
 
@@ -47,7 +46,6 @@ type sptDevice struct {
 	ctx     *C.struct_spt_ctx
 	cancel  *C.int32_t               // C memory, polled before each launch
 	tensors map[string]C.spt_tensor // HBM-resident tensors by GGUF name
-	index   *C.spt_gguf              // the model's directory, when preloaded
 	xdev    unsafe.Pointer           // device staging of forwardMoE (one token)
 	ydev    unsafe.Pointer
 	xbytes  int
@@ -108,11 +106,12 @@ func (d *sptDevice) run(ctx context.Context, fn func() C.int) error {
 	return nil
 }
 
-// PreloadSPT makes every layer's MoE and Q4_0 projection tensors and the
-// output head resident in HBM at engine start: the directory is read by
-// spt_gguf_open over the model's files and each tensor's bytes are copied
-// from its file unchanged (spt_gguf_upload), in place of the per-call
-// streaming of WithTensorChunks / WithExpertRanges (mmap_linux.go:239,391).
+// PreloadSPT makes every layer's tensors and the output head resident in
+// HBM at engine start: each ggufindex.Tensor's Range, as ggufindex.Open
+// recorded it (ggufindex/index.go:15-26), is copied from its file unchanged
+// by spt_upload_range, in place of the per-call streaming of
+// WithTensorChunks / WithExpertRanges (mmap_linux.go:239,391).  The model
+// is the one the engine already opened; no file is parsed again.
 func PreloadSPT(model *ggufindex.Model) error {
 	d, err := activeSPT()
 	if err != nil {
@@ -120,46 +119,41 @@ func PreloadSPT(model *ggufindex.Model) error {
 	}
 	d.mu.Lock()
 	defer d.mu.Unlock()
-	paths := make([]*C.char, len(model.Paths))
-	for i, p := range model.Paths {
-		paths[i] = C.CString(p)
-		defer C.free(unsafe.Pointer(paths[i]))
-	}
-	if d.index == nil {
-		if rc := C.spt_gguf_open(&paths[0], C.int32_t(len(paths)), &d.index); rc != C.SPT_OK {
-			return sptErr(rc)
-		}
-	}
-	upload := func(name string) error {
-		if name == "" {
+	upload := func(t ggufindex.Tensor) error {
+		if t.Name == "" {
 			return nil
 		}
-		if _, ok := d.tensors[name]; ok {
+		if _, ok := d.tensors[t.Name]; ok {
 			return nil
 		}
-		cn := C.CString(name)
-		defer C.free(unsafe.Pointer(cn))
-		var t C.spt_tensor
-		if rc := C.spt_gguf_upload(d.ctx, d.index, cn, &t); rc != C.SPT_OK {
+		var ct C.spt_tensor
+		if len(t.Shape) > len(ct.shape) {
+			return fmt.Errorf("%q: %d dimensions (at most %d are supported)", t.Name, len(t.Shape), len(ct.shape))
+		}
+		ct.name = C.CString(t.Name) // lives as long as the device
+		ct._type = C.uint32_t(t.Type)
+		ct.n_dims = C.uint32_t(len(t.Shape))
+		for i, s := range t.Shape {
+			ct.shape[i] = C.uint64_t(s)
+		}
+		path := C.CString(t.Range.File)
+		defer C.free(unsafe.Pointer(path))
+		if rc := C.spt_upload_range(d.ctx, path, C.uint64_t(t.Range.Start), C.uint64_t(t.Range.End), &ct); rc != C.SPT_OK {
+			C.free(unsafe.Pointer(ct.name))
 			return sptErr(rc)
 		}
-		d.tensors[name] = t // t.name points into the index, which stays open
+		d.tensors[t.Name] = ct
 		return nil
 	}
 	for _, layer := range model.Layers {
-		lw := NewLayerWeights(layer)
-		for _, t := range []ggufindex.Tensor{
-			lw.AttnQ, lw.AttnK, lw.AttnV, lw.AttnOutput,
-			lw.FFNGateInp, lw.FFNGateInpBias, lw.FFNGateExps, lw.FFNGateExpsBias,
-			lw.FFNUpExps, lw.FFNUpExpsBias, lw.FFNDownExps, lw.FFNDownExpsBias,
-		} {
-			if err := upload(t.Name); err != nil {
+		for _, t := range layer.Tensors {
+			if err := upload(t); err != nil {
 				return err
 			}
 		}
 	}
 	if head, ok := model.TensorByName("output.weight"); ok {
-		return upload(head.Name)
+		return upload(head)
 	}
 	return nil
 }

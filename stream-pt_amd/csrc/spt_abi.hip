@@ -6,6 +6,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cerrno>
 #include <climits>
 #include <cstdarg>
 #include <cstdio>
@@ -15,8 +16,6 @@
 #include <utility>
 #include <vector>
 
-#include "spt_gguf.h"
-#include "spt_gguf_index.h"
 #include "spt_kernels.h"
 #include "spt_moe.h"
 
@@ -348,10 +347,12 @@ struct MoEDims {
     int64_t h, d, E, k, batch;
 };
 
-// forwardMoEBatch validation (forward/moe_batch.go:81-130).
+// forwardMoEBatch validation (forward/moe_batch.go:81-130).  With `sliced`
+// the batch may hold more selections than one launch sequence takes
+// (spt::kMaxSelections): the caller runs it as slices of whole tokens.
 int validate_moe(spt_ctx *ctx, const spt_moe_config *cfg, const spt_moe_layer *lw,
                  const float *x, int64_t x_len, const float *out, int64_t out_len, int64_t batch,
-                 MoEDims *dims) {
+                 MoEDims *dims, bool sliced = false) {
     if (!ctx || !cfg || !lw) return fail(SPT_ERR_INVALID, "nil MoE context, reader, configuration or weights");
     int64_t h = cfg->hidden_dim, d = cfg->expert_hidden_dim, E = cfg->num_experts, k = cfg->num_experts_used;
     int64_t n;
@@ -379,10 +380,10 @@ int validate_moe(spt_ctx *ctx, const spt_moe_config *cfg, const spt_moe_layer *l
     if (named(lw->ffn_gate_inp_bias) && lw->ffn_gate_inp_bias.n_dims != 1)
         return fail(SPT_ERR_INVALID, "\"%s\": invalid float vector shape or range", tname(&lw->ffn_gate_inp_bias));
     if (h % 32 != 0) return fail(SPT_ERR_INVALID, "hidden dimension %lld is not a multiple of 32", (long long)h);
-    if (k > spt::kMaxTopK || E > spt::kMaxExperts || batch * k > spt::kMaxSelections)
+    if (k > spt::kMaxTopK || E > spt::kMaxExperts || (!sliced && batch * k > spt::kMaxSelections))
         return fail(SPT_ERR_INVALID,
                     "MoE shape beyond this device path's limits (experts used <= %d, experts <= %d, "
-                    "batch*experts used <= %d)",
+                    "batch*experts used <= %d per call with taps or without allocation)",
                     spt::kMaxTopK, spt::kMaxExperts, spt::kMaxSelections);
     *dims = MoEDims{h, d, E, k, batch};
     return SPT_OK;
@@ -747,6 +748,14 @@ int run_moe_at(spt_ctx *ctx, const spt_moe_layer *lw, const float *x, float *out
     return SPT_OK;
 }
 
+// Tokens per launch sequence: a batch of more selections than
+// spt::kMaxSelections runs as consecutive slices of this many whole tokens.
+// The reference accepts any batch (forward/moe_batch.go:29-38,84-90), and a
+// token's output depends only on its own row of x, so slicing changes no
+// routing; the slices' own expert groups decide which of the grouped GEMV
+// and GEMM each group takes, as for separate calls of those tokens.
+int64_t moe_slice_tokens(const MoEDims &m) { return spt::kMaxSelections / m.k; }
+
 int run_moe(spt_ctx *ctx, const spt_moe_layer *lw, const float *x, float *out, const MoEDims &m,
             const spt_moe_taps *taps) {
     const MoELayout L = moe_layout(ctx, m, taps && taps->act, 0);
@@ -1047,27 +1056,33 @@ int q80_argmax_at(spt_ctx *ctx, const spt_tensor *w, int64_t in, int64_t out, co
 }  // namespace
 
 // ---------------------------------------------------------------------------
-// GGUF residency loader
+// Residency from the model files
 // ---------------------------------------------------------------------------
-// An opened model: the index and its tensors in the order of Layers then
-// Shared.
-struct spt_gguf {
-    spt::gguf::Model model;
-    std::vector<const spt::gguf::Tensor *> order;
-};
-
 namespace {
 
-void gguf_info(const spt::gguf::Tensor &t, spt_gguf_tensor *o) {
-    memset(o, 0, sizeof *o);
-    o->name = t.name.c_str();
-    o->type = t.type;
-    o->n_dims = (uint32_t)t.shape.size();
-    for (size_t i = 0; i < t.shape.size() && i < 8; i++) o->shape[i] = t.shape[i];
-    o->file = t.range.file;
-    o->layer = t.layer;
-    o->start = t.range.start;
-    o->end = t.range.end;
+// Byte size of a tensor of one of the path's GGML types from its shape (the
+// per-type sizes of ggufindex's tensorSize, ggufindex/index.go:535-574):
+// false for another type or a shape that is not a whole number of blocks.
+bool path_tensor_bytes(const spt_tensor &t, uint64_t *out) {
+    if (t.n_dims < 1 || t.n_dims > 4) return false;
+    uint64_t e = 1;
+    for (uint32_t i = 0; i < t.n_dims; i++) {
+        if (t.shape[i] != 0 && e > UINT64_MAX / t.shape[i]) return false;
+        e *= t.shape[i];
+    }
+    uint64_t block = 1, bytes;
+    switch (t.type) {
+    case SPT_TYPE_F32: bytes = 4; break;
+    case SPT_TYPE_F16:
+    case SPT_TYPE_BF16: bytes = 2; break;
+    case SPT_TYPE_Q4_0: block = 32, bytes = 18; break;
+    case SPT_TYPE_Q8_0: block = 32, bytes = 34; break;
+    case SPT_TYPE_MXFP4: block = 32, bytes = 17; break;
+    default: return false;
+    }
+    if (t.shape[0] % block != 0 || e / block > UINT64_MAX / bytes) return false;
+    *out = e / block * bytes;
+    return true;
 }
 
 // Bytes [start, start + n) of a file into device memory at dst: chunks read
@@ -1114,28 +1129,6 @@ int load_range(spt_ctx *ctx, const std::string &path, uint64_t start, uint64_t n
         if (ev[h]) (void)hipEventDestroy(ev[h]);
     fclose(f);
     return rc;
-}
-
-int gguf_upload(spt_ctx *ctx, const spt_gguf *g, const spt::gguf::Tensor &t, spt_tensor *out) {
-    if (t.shape.size() > 4)
-        return fail(SPT_ERR_INVALID, "\"%s\": %zu dimensions (at most 4 are supported)", t.name.c_str(),
-                    t.shape.size());
-    const uint64_t n = t.range.end - t.range.start;
-    void *d = nullptr;
-    int rc;
-    if ((rc = spt_alloc(ctx, n, &d))) return rc;
-    if ((rc = load_range(ctx, g->model.paths[t.range.file], t.range.start, n, (char *)d))) {
-        (void)hipFree(d);
-        return rc;
-    }
-    memset(out, 0, sizeof *out);
-    out->name = t.name.c_str();
-    out->type = t.type;
-    out->n_dims = (uint32_t)t.shape.size();
-    for (size_t i = 0; i < t.shape.size(); i++) out->shape[i] = t.shape[i];
-    out->nbytes = n;
-    out->data = d;
-    return SPT_OK;
 }
 
 }  // namespace
@@ -1680,10 +1673,17 @@ int spt_forward_moe_batch_ex(spt_ctx *ctx, const spt_moe_config *cfg, const spt_
                              const spt_moe_taps *taps) {
     MoEDims m;
     int rc;
-    if ((rc = validate_moe(ctx, cfg, lw, x_dev, x_len, out_dev, out_len, batch, &m))) return rc;
+    if ((rc = validate_moe(ctx, cfg, lw, x_dev, x_len, out_dev, out_len, batch, &m, !taps))) return rc;
     if ((rc = check_cancel(ctx))) return rc;
     if ((rc = check_device(ctx))) return rc;
-    return run_moe(ctx, lw, x_dev, out_dev, m, taps);
+    const int64_t st = moe_slice_tokens(m);
+    for (int64_t t0 = 0; t0 < batch; t0 += st) {
+        MoEDims ms = m;
+        ms.batch = std::min(st, batch - t0);
+        if ((rc = check_cancel(ctx))) return rc;
+        if ((rc = run_moe(ctx, lw, x_dev + t0 * m.h, out_dev + t0 * m.h, ms, taps))) return rc;
+    }
+    return SPT_OK;
 }
 
 int spt_forward_moe_batch(spt_ctx *ctx, const spt_moe_config *cfg, const spt_moe_layer *lw, const float *x_dev,
@@ -1709,24 +1709,31 @@ int spt_forward_moe_batch_host(spt_ctx *ctx, const spt_moe_config *cfg, const sp
                                int64_t batch) {
     MoEDims m;
     int rc;
-    if ((rc = validate_moe(ctx, cfg, lw, x_host, x_len, out_host, out_len, batch, &m))) return rc;
+    if ((rc = validate_moe(ctx, cfg, lw, x_host, x_len, out_host, out_len, batch, &m, true))) return rc;
     if ((rc = check_cancel(ctx)) || (rc = check_device(ctx))) return rc;
     // x and out travel through the context's pinned staging buffer and the
     // head of its device arena; nothing is allocated once both have grown
-    const size_t xb = align256((size_t)x_len * 4), ob = align256((size_t)out_len * 4);
-    const MoELayout L = moe_layout(ctx, m, false, xb + ob);
-    char *S, *P;
-    if ((rc = arena(ctx, L.total, &S)) || (rc = staging(ctx, xb + ob, &P))) return rc;
-    memcpy(P, x_host, (size_t)x_len * 4);
-    SPT_HIP(hipMemcpyAsync(S, P, (size_t)x_len * 4, hipMemcpyHostToDevice, ctx->stream));
-    rc = run_moe_at(ctx, lw, (const float *)S, (float *)(S + xb), m, nullptr, S, L);
-    if (!rc) {
-        SPT_HIP(hipMemcpyAsync(P + xb, S + xb, (size_t)out_len * 4, hipMemcpyDeviceToHost, ctx->stream));
+    const int64_t st = moe_slice_tokens(m);
+    for (int64_t t0 = 0; t0 < batch; t0 += st) {
+        MoEDims ms = m;
+        ms.batch = std::min(st, batch - t0);
+        const size_t n = (size_t)(ms.batch * m.h);
+        const size_t xb = align256(n * 4), ob = align256(n * 4);
+        const MoELayout L = moe_layout(ctx, ms, false, xb + ob);
+        char *S, *P;
+        if ((rc = check_cancel(ctx))) return rc;
+        if ((rc = arena(ctx, L.total, &S)) || (rc = staging(ctx, xb + ob, &P))) return rc;
+        memcpy(P, x_host + t0 * m.h, n * 4);
+        SPT_HIP(hipMemcpyAsync(S, P, n * 4, hipMemcpyHostToDevice, ctx->stream));
+        rc = run_moe_at(ctx, lw, (const float *)S, (float *)(S + xb), ms, nullptr, S, L);
+        if (!rc) {
+            SPT_HIP(hipMemcpyAsync(P + xb, S + xb, n * 4, hipMemcpyDeviceToHost, ctx->stream));
+        }
+        const hipError_t e = hipStreamSynchronize(ctx->stream);
+        if (rc) return rc;
+        if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+        memcpy(out_host + t0 * m.h, P + xb, n * 4);
     }
-    const hipError_t e = hipStreamSynchronize(ctx->stream);
-    if (rc) return rc;
-    if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
-    memcpy(out_host, P + xb, (size_t)out_len * 4);
     return SPT_OK;
 }
 
@@ -1734,16 +1741,25 @@ int spt_forward_moe_batch_q8(spt_ctx *ctx, const spt_moe_config *cfg, const spt_
                              const void *xq_dev, int64_t x_len, float *out_dev, int64_t out_len, int64_t batch) {
     MoEDims m;
     int rc;
-    if ((rc = validate_moe(ctx, cfg, lw, x_dev, x_len, out_dev, out_len, batch, &m))) return rc;
+    if ((rc = validate_moe(ctx, cfg, lw, x_dev, x_len, out_dev, out_len, batch, &m, true))) return rc;
     if (!xq_dev) return fail(SPT_ERR_INVALID, "nil Q8_0 input");
     if ((uintptr_t)xq_dev & 1) return fail(SPT_ERR_INVALID, "Q8_0 input must be 2-byte aligned");
     if (ranges_overlap(xq_dev, (uint64_t)x_len / 32 * 34, out_dev, (uint64_t)out_len * 4))
         return fail(SPT_ERR_INVALID, "MoE Q8_0 input and output overlap");
     if ((rc = check_cancel(ctx)) || (rc = check_device(ctx))) return rc;
-    const MoELayout L = moe_layout(ctx, m, false, 0);
-    char *S;
-    if ((rc = arena(ctx, L.total, &S))) return rc;
-    return run_moe_at(ctx, lw, x_dev, out_dev, m, nullptr, S, L, (const uint8_t *)xq_dev);
+    const int64_t st = moe_slice_tokens(m);
+    for (int64_t t0 = 0; t0 < batch; t0 += st) {
+        MoEDims ms = m;
+        ms.batch = std::min(st, batch - t0);
+        const MoELayout L = moe_layout(ctx, ms, false, 0);
+        char *S;
+        if ((rc = check_cancel(ctx))) return rc;
+        if ((rc = arena(ctx, L.total, &S))) return rc;
+        if ((rc = run_moe_at(ctx, lw, x_dev + t0 * m.h, out_dev + t0 * m.h, ms, nullptr, S, L,
+                             (const uint8_t *)xq_dev + t0 * (m.h / 32) * 34)))
+            return rc;
+    }
+    return SPT_OK;
 }
 
 int spt_forward_moe_batch_noalloc(spt_ctx *ctx, const spt_moe_config *cfg, const spt_moe_layer *lw,
@@ -1809,127 +1825,45 @@ int spt_synth_mxfp4(spt_ctx *ctx, void *dst_dev, uint64_t key, uint64_t first_bl
 }
 
 
-int spt_gguf_open(const char *const *paths, int32_t n_paths, spt_gguf **out) {
-    if (!out) return fail(SPT_ERR_INVALID, "nil output pointer");
-    *out = nullptr;
-    if (n_paths < 0 || (n_paths > 0 && !paths)) return fail(SPT_ERR_INVALID, "nil path list");
-    std::vector<std::string> ps;
-    for (int32_t i = 0; i < n_paths; i++) {
-        if (!paths[i]) return fail(SPT_ERR_INVALID, "nil path");
-        ps.emplace_back(paths[i]);
-    }
-    spt_gguf *g = new (std::nothrow) spt_gguf;
-    if (!g) return fail(SPT_ERR_NOMEM, "cannot allocate the index");
-    std::string err;
-    if (!spt::gguf::open(ps, &g->model, &err)) {
-        delete g;
-        const bool io = err.find(": open ") != std::string::npos || err.compare(0, 5, "open ") == 0;
-        return fail(io ? SPT_ERR_IO : SPT_ERR_INVALID, "%s", err.c_str());
-    }
-    for (const auto &layer : g->model.layers)
-        for (const auto &t : layer) g->order.push_back(&t);
-    for (const auto &t : g->model.shared) g->order.push_back(&t);
-    *out = g;
-    return SPT_OK;
-}
-
-int spt_gguf_close(spt_gguf *g) {
-    delete g;
-    return SPT_OK;
-}
-
-int spt_gguf_info(const spt_gguf *g, int64_t *layer_count, int64_t *n_tensors, uint64_t *alignment) {
-    if (!g) return fail(SPT_ERR_INVALID, "nil model");
-    if (layer_count) *layer_count = g->model.layer_count;
-    if (n_tensors) *n_tensors = (int64_t)g->order.size();
-    if (alignment) *alignment = g->model.alignment;
-    return SPT_OK;
-}
-
-int spt_gguf_tensor_at(const spt_gguf *g, int64_t i, spt_gguf_tensor *out) {
-    if (!g || !out) return fail(SPT_ERR_INVALID, "nil model or output");
-    if (i < 0 || i >= (int64_t)g->order.size()) return fail(SPT_ERR_NOT_FOUND, "tensor index %lld out of range", (long long)i);
-    gguf_info(*g->order[i], out);
-    return SPT_OK;
-}
-
-int spt_gguf_find(const spt_gguf *g, const char *name, spt_gguf_tensor *out) {
-    if (!g || !name || !out) return fail(SPT_ERR_INVALID, "nil model, name or output");
-    const spt::gguf::Tensor *t = spt::gguf::find(g->model, name);
-    if (!t) return fail(SPT_ERR_NOT_FOUND, "tensor \"%s\" not found", name);
-    gguf_info(*t, out);
-    return SPT_OK;
-}
-
-int spt_gguf_layer_span(const spt_gguf *g, int64_t layer, int32_t i, int32_t *file, uint64_t *start,
-                        uint64_t *end) {
-    if (!g || !file || !start || !end) return fail(SPT_ERR_INVALID, "nil model or output");
-    if (layer < 0 || layer >= (int64_t)g->model.spans.size()) return fail(SPT_ERR_NOT_FOUND, "no layer %lld", (long long)layer);
-    const auto &sp = g->model.spans[(size_t)layer];
-    if (i < 0 || i >= (int32_t)sp.size()) return fail(SPT_ERR_NOT_FOUND, "no span %d of layer %lld", i, (long long)layer);
-    *file = sp[(size_t)i].file;
-    *start = sp[(size_t)i].start;
-    *end = sp[(size_t)i].end;
-    return SPT_OK;
-}
-
-int spt_gguf_metadata(const spt_gguf *g, const char *key, uint32_t *type, int32_t *file, uint64_t *start,
-                      uint64_t *end) {
-    if (!g || !key || !type || !file || !start || !end) return fail(SPT_ERR_INVALID, "nil model, key or output");
-    auto it = g->model.metadata.find(key);
-    if (it == g->model.metadata.end()) return fail(SPT_ERR_NOT_FOUND, "metadata key \"%s\" not found", key);
-    *type = it->second.type;
-    *file = it->second.range.file;
-    *start = it->second.range.start;
-    *end = it->second.range.end;
-    return SPT_OK;
-}
-
-int spt_gguf_upload(spt_ctx *ctx, const spt_gguf *g, const char *name, spt_tensor *out) {
+// Residency from the model files: a ggufindex.Tensor's Range copied to HBM.
+int spt_upload_range(spt_ctx *ctx, const char *path, uint64_t start, uint64_t end, spt_tensor *t) {
     int rc;
     if ((rc = check_ctx(ctx))) return rc;
-    if (!g || !name || !out) return fail(SPT_ERR_INVALID, "nil model, name or output");
+    if (!path || !t) return fail(SPT_ERR_INVALID, "nil path or tensor");
+    if (end < start)
+        return fail(SPT_ERR_INVALID, "\"%s\": invalid byte range [%llu, %llu)", tname(t), (unsigned long long)start,
+                    (unsigned long long)end);
+    if (t->n_dims < 1 || t->n_dims > 4)
+        return fail(SPT_ERR_INVALID, "\"%s\": %u dimensions (1 to 4 are supported)", tname(t), t->n_dims);
+    const uint64_t n = end - start;
+    uint64_t want;
+    const bool known = path_tensor_bytes(*t, &want);
+    if (t->type == SPT_TYPE_F32 || t->type == SPT_TYPE_F16 || t->type == SPT_TYPE_BF16 || t->type == SPT_TYPE_Q4_0 ||
+        t->type == SPT_TYPE_Q8_0 || t->type == SPT_TYPE_MXFP4) {
+        if (!known || want != n)
+            return fail(SPT_ERR_INVALID, "\"%s\": byte range of %llu bytes does not match its type %u and shape",
+                        tname(t), (unsigned long long)n, t->type);
+    }
     if ((rc = check_device(ctx))) return rc;
-    const spt::gguf::Tensor *t = spt::gguf::find(g->model, name);
-    if (!t) return fail(SPT_ERR_NOT_FOUND, "tensor \"%s\" not found", name);
-    return gguf_upload(ctx, g, *t, out);
-}
-
-int spt_gguf_upload_moe_layer(spt_ctx *ctx, const spt_gguf *g, int64_t layer, spt_moe_layer *out) {
-    int rc;
-    if ((rc = check_ctx(ctx))) return rc;
-    if (!g || !out) return fail(SPT_ERR_INVALID, "nil model or output");
-    if ((rc = check_device(ctx))) return rc;
-    if (layer < 0 || layer >= (int64_t)g->model.layers.size()) return fail(SPT_ERR_NOT_FOUND, "no layer %lld", (long long)layer);
-    memset(out, 0, sizeof *out);
-    const std::pair<const char *, spt_tensor *> fields[] = {
-        {"ffn_gate_inp.weight", &out->ffn_gate_inp},       {"ffn_gate_inp.bias", &out->ffn_gate_inp_bias},
-        {"ffn_gate_exps.weight", &out->ffn_gate_exps},     {"ffn_gate_exps.bias", &out->ffn_gate_exps_bias},
-        {"ffn_up_exps.weight", &out->ffn_up_exps},         {"ffn_up_exps.bias", &out->ffn_up_exps_bias},
-        {"ffn_down_exps.weight", &out->ffn_down_exps},     {"ffn_down_exps.bias", &out->ffn_down_exps_bias},
-    };
-    // NewLayerWeights: the last tensor (in name order) with a field's suffix wins
-    const spt::gguf::Tensor *pick[8] = {};
-    for (const auto &t : g->model.layers[(size_t)layer])
-        for (int f = 0; f < 8; f++) {
-            const size_t ls = strlen(fields[f].first);
-            if (t.name.size() >= ls && t.name.compare(t.name.size() - ls, ls, fields[f].first) == 0) {
-                pick[f] = &t;
-                break;
-            }
-        }
-    for (int f = 0; f < 8; f++) {
-        if (!pick[f]) continue;
-        if ((rc = gguf_upload(ctx, g, *pick[f], fields[f].second))) {
-            char msg[sizeof g_error];
-            memcpy(msg, g_error, sizeof msg);
-            for (int k = 0; k < f; k++)
-                if (fields[k].second->data) (void)hipFree(const_cast<void *>(fields[k].second->data));
-            memset(out, 0, sizeof *out);
-            memcpy(g_error, msg, sizeof msg);
+    void *d = nullptr;
+    if (n) {
+        if ((rc = spt_alloc(ctx, n, &d))) return rc;
+        if ((rc = load_range(ctx, path, start, n, (char *)d))) {
+            (void)hipFree(d);
             return rc;
         }
     }
+    t->nbytes = n;
+    t->data = d;
+    return SPT_OK;
+}
+
+int spt_ctx_memory(spt_ctx *ctx, uint64_t *arena_bytes, uint64_t *staging_bytes) {
+    int rc;
+    if ((rc = check_ctx(ctx))) return rc;
+    if (!arena_bytes || !staging_bytes) return fail(SPT_ERR_INVALID, "nil output pointer");
+    *arena_bytes = ctx->scratch_bytes;
+    *staging_bytes = ctx->pinned_bytes;
     return SPT_OK;
 }
 

@@ -12,15 +12,14 @@ from __future__ import annotations
 import ctypes as C
 import os
 
-__all__ = ["SptError", "Tensor", "MoEConfig", "MoELayer", "MoETaps", "Context", "Gguf", "GgufTensor", "lib",
-           "LIB_PATH",
+__all__ = ["SptError", "Tensor", "MoEConfig", "MoELayer", "MoETaps", "Context", "lib", "LIB_PATH",
            "TYPE_F32", "TYPE_F16", "TYPE_Q4_0", "TYPE_Q8_0", "TYPE_BF16", "TYPE_MXFP4",
-           "OK", "ERR_INVALID", "ERR_DEVICE", "ERR_NOMEM", "ERR_CANCELED", "ERR_IO", "ERR_NOT_FOUND"]
+           "OK", "ERR_INVALID", "ERR_DEVICE", "ERR_NOMEM", "ERR_CANCELED", "ERR_IO"]
 
 _PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB_PATH = os.path.join(_PKG_DIR, "libspt_moe.so")
 
-OK, ERR_INVALID, ERR_DEVICE, ERR_NOMEM, ERR_CANCELED, ERR_IO, ERR_NOT_FOUND = 0, 1, 2, 3, 4, 5, 6
+OK, ERR_INVALID, ERR_DEVICE, ERR_NOMEM, ERR_CANCELED, ERR_IO = 0, 1, 2, 3, 4, 5
 TYPE_F32, TYPE_F16, TYPE_Q4_0, TYPE_Q8_0, TYPE_BF16, TYPE_MXFP4 = 0, 1, 2, 8, 30, 39
 
 EXPORTED = (
@@ -34,9 +33,7 @@ EXPORTED = (
     "spt_mul_q80_into", "spt_mul_q80_argmax", "spt_mul_q80_into_host", "spt_mul_q80_argmax_host",
     "spt_rmsnorm_into", "spt_rmsnorm_batch_into", "spt_mul_q40_batch_bias_into",
     "spt_mul_q40_batch_q8_into", "spt_mul_q40_qkv_batch_into", "spt_forward_moe_batch_q8",
-    "spt_forward_moe_batch_noalloc", "spt_ctx_set_decode_max_selections",
-    "spt_gguf_open", "spt_gguf_close", "spt_gguf_info", "spt_gguf_tensor_at", "spt_gguf_find",
-    "spt_gguf_layer_span", "spt_gguf_metadata", "spt_gguf_upload", "spt_gguf_upload_moe_layer",
+    "spt_forward_moe_batch_noalloc", "spt_ctx_set_decode_max_selections", "spt_upload_range", "spt_ctx_memory",
 )
 KERNEL_KINDS = ("quantize", "route", "gate_up", "down", "combine", "q40", "select", "gate_up_gemm", "down_gemm",
                 "q80", "rmsnorm")
@@ -80,17 +77,6 @@ class MoELayer(C.Structure):
     _fields_ = [(n, Tensor) for n in (
         "ffn_gate_inp", "ffn_gate_inp_bias", "ffn_gate_exps", "ffn_gate_exps_bias",
         "ffn_up_exps", "ffn_up_exps_bias", "ffn_down_exps", "ffn_down_exps_bias")]
-
-
-class GgufTensor(C.Structure):
-    """spt_gguf_tensor: a ggufindex.Tensor as read from the directory."""
-    _fields_ = [("name", C.c_char_p), ("type", C.c_uint32), ("n_dims", C.c_uint32),
-                ("shape", C.c_uint64 * 8), ("file", C.c_int32), ("layer", C.c_int64),
-                ("start", C.c_uint64), ("end", C.c_uint64)]
-
-    @property
-    def dims(self):
-        return [int(self.shape[i]) for i in range(self.n_dims)]
 
 
 class MoETaps(C.Structure):
@@ -155,16 +141,8 @@ def lib():
         "spt_synth_mxfp4": ([vp, vp, u64, u64, u64, i32, i32], C.c_int),
         "spt_ctx_enable_timing": ([vp, C.c_int], C.c_int),
         "spt_ctx_read_timing": ([vp, C.POINTER(C.c_double), C.POINTER(C.c_int64)], C.c_int),
-        "spt_gguf_open": ([C.POINTER(C.c_char_p), i32, C.POINTER(vp)], C.c_int),
-        "spt_gguf_close": ([vp], C.c_int),
-        "spt_gguf_info": ([vp, C.POINTER(i64), C.POINTER(i64), C.POINTER(u64)], C.c_int),
-        "spt_gguf_tensor_at": ([vp, i64, C.POINTER(GgufTensor)], C.c_int),
-        "spt_gguf_find": ([vp, C.c_char_p, C.POINTER(GgufTensor)], C.c_int),
-        "spt_gguf_layer_span": ([vp, i64, i32, C.POINTER(i32), C.POINTER(u64), C.POINTER(u64)], C.c_int),
-        "spt_gguf_metadata": ([vp, C.c_char_p, C.POINTER(C.c_uint32), C.POINTER(i32), C.POINTER(u64),
-                               C.POINTER(u64)], C.c_int),
-        "spt_gguf_upload": ([vp, vp, C.c_char_p, T], C.c_int),
-        "spt_gguf_upload_moe_layer": ([vp, vp, i64, C.POINTER(MoELayer)], C.c_int),
+        "spt_upload_range": ([vp, C.c_char_p, u64, u64, T], C.c_int),
+        "spt_ctx_memory": ([vp, C.POINTER(u64), C.POINTER(u64)], C.c_int),
     }
     for name, (args, res) in sig.items():
         f = getattr(L, name)
@@ -200,95 +178,6 @@ def _check(rc):
 
 def _ref(t):
     return C.byref(t) if t is not None else None
-
-
-class Gguf:
-    """ggufindex.Open over one or more GGUF files: the tensor directory,
-    metadata ranges and layer spans, and uploads of tensors to HBM."""
-
-    def __init__(self, paths):
-        if isinstance(paths, (str, os.PathLike)):
-            paths = [paths]
-        enc = [os.fspath(p).encode() for p in paths]
-        arr = (C.c_char_p * max(1, len(enc)))(*enc)
-        h = C.c_void_p()
-        _check(lib().spt_gguf_open(arr, len(enc), C.byref(h)))
-        self.handle = h
-        self.paths = [os.fspath(p) for p in paths]
-
-    def close(self):
-        if self.handle:
-            lib().spt_gguf_close(self.handle)
-            self.handle = None
-
-    def __enter__(self):
-        return self
-
-    def __exit__(self, *exc):
-        self.close()
-
-    def __del__(self):
-        try:
-            self.close()
-        except Exception:
-            pass
-
-    def info(self):
-        """(layer_count, n_tensors, alignment)."""
-        lc, nt, al = C.c_int64(), C.c_int64(), C.c_uint64()
-        _check(lib().spt_gguf_info(self.handle, C.byref(lc), C.byref(nt), C.byref(al)))
-        return lc.value, nt.value, al.value
-
-    def tensors(self):
-        """Every tensor: the layers' in order, then the shared ones."""
-        out = []
-        for i in range(self.info()[1]):
-            t = GgufTensor()
-            _check(lib().spt_gguf_tensor_at(self.handle, i, C.byref(t)))
-            out.append(t)
-        return out
-
-    def find(self, name):
-        """TensorByName; None when absent."""
-        t = GgufTensor()
-        rc = lib().spt_gguf_find(self.handle, name.encode(), C.byref(t))
-        if rc == ERR_NOT_FOUND:
-            return None
-        _check(rc)
-        return t
-
-    def layer_spans(self, layer):
-        """[(file, start, end)] of Layer.Spans."""
-        out = []
-        f, a, b = C.c_int32(), C.c_uint64(), C.c_uint64()
-        while True:
-            rc = lib().spt_gguf_layer_span(self.handle, layer, len(out), C.byref(f), C.byref(a), C.byref(b))
-            if rc == ERR_NOT_FOUND:
-                return out
-            _check(rc)
-            out.append((f.value, a.value, b.value))
-
-    def metadata(self, key):
-        """(type, file, start, end) of Model.Metadata[key]; None when absent."""
-        t, f, a, b = C.c_uint32(), C.c_int32(), C.c_uint64(), C.c_uint64()
-        rc = lib().spt_gguf_metadata(self.handle, key.encode(), C.byref(t), C.byref(f), C.byref(a), C.byref(b))
-        if rc == ERR_NOT_FOUND:
-            return None
-        _check(rc)
-        return t.value, f.value, a.value, b.value
-
-    def upload(self, ctx, name):
-        """The tensor's bytes copied into a new device allocation: a Tensor
-        (free with ctx.free(t.data))."""
-        t = Tensor()
-        _check(lib().spt_gguf_upload(ctx.handle, self.handle, name.encode(), C.byref(t)))
-        return t
-
-    def upload_moe_layer(self, ctx, layer):
-        """The layer's MoE tensors (NewLayerWeights suffixes) in HBM."""
-        lw = MoELayer()
-        _check(lib().spt_gguf_upload_moe_layer(ctx.handle, self.handle, layer, C.byref(lw)))
-        return lw
 
 
 class Context:
@@ -331,6 +220,24 @@ class Context:
         n = (C.c_int64 * len(KERNEL_KINDS))()
         _check(lib().spt_ctx_read_timing(self.handle, ms, n))
         return {k: (ms[i], n[i]) for i, k in enumerate(KERNEL_KINDS)}
+
+    def memory(self):
+        """(arena_bytes, staging_bytes) the context holds."""
+        a, b = C.c_uint64(), C.c_uint64()
+        _check(lib().spt_ctx_memory(self.handle, C.byref(a), C.byref(b)))
+        return a.value, b.value
+
+    def upload_range(self, path, start: int, end: int, name, typ: int, shape) -> Tensor:
+        """Bytes [start, end) of the file at path (a ggufindex.Tensor's
+        Range) copied to a new device allocation: the resident Tensor (free
+        with ctx.free(t.data)).  The name bytes are kept on the Tensor."""
+        t = Tensor.make(name, typ, shape, None, 0)
+        _check(lib().spt_upload_range(self.handle, os.fspath(path).encode(), int(start), int(end), C.byref(t)))
+        return t
+
+    def free(self, dev):
+        if dev:
+            _check(lib().spt_free(self.handle, dev))
 
     def set_gemm_min_group(self, min_group: int):
         """Expert groups of at least min_group selections use the grouped

@@ -333,3 +333,34 @@ def test_forward_moe_unnamed_router_bias_still_checked(vctx):
     lw.ffn_gate_inp_bias.name = None
     assert _call_moe_single(vctx, cfg, lw, X, 32, OUT, 32) == spt.ERR_INVALID
     assert b"unnamed MoE bias has nonempty range" in spt.lib().spt_last_error()
+
+
+def test_moe_large_batches_run_as_slices(vctx):
+    """More than 4096 selections: the plain, host and Q8_0-input forms accept
+    the batch (it runs as slices of whole tokens; the validation-only
+    context stops at the device), the tapped form refuses it, and the
+    experts-used and expert-count limits hold."""
+    H, k = 32, 2
+    cfg, lw = _moe_descriptors(H=H, k=k)
+    batch = 4096 // k + 1
+    n = batch * H
+    assert _call_moe(vctx, cfg, lw, X, n, OUT, n, batch) == spt.ERR_DEVICE
+    x = np.zeros(n, np.float32)
+    out = np.zeros(n, np.float32)
+    rc = spt.lib().spt_forward_moe_batch_host(vctx.handle, C.byref(cfg), C.byref(lw), x.ctypes.data, n,
+                                              out.ctypes.data, n, batch)
+    assert rc == spt.ERR_DEVICE
+    rc = spt.lib().spt_forward_moe_batch_q8(vctx.handle, C.byref(cfg), C.byref(lw), X, 0x40000000, n, OUT, n,
+                                            batch)
+    assert rc == spt.ERR_DEVICE
+    taps = spt.MoETaps()
+    rc = spt.lib().spt_forward_moe_batch_ex(vctx.handle, C.byref(cfg), C.byref(lw), X, n, OUT, n, batch,
+                                            C.byref(taps))
+    assert rc == spt.ERR_INVALID and b"4096" in spt.lib().spt_last_error()
+    rc = spt.lib().spt_forward_moe_batch_ex(vctx.handle, C.byref(cfg), C.byref(lw), X, n - H, OUT, n - H,
+                                            batch - 1, C.byref(taps))
+    assert rc == spt.ERR_DEVICE
+    for E, kk in ((257, 2), (32, 17)):
+        cfg, lw = _moe_descriptors(H=H, E=E, k=kk)
+        assert _call_moe(vctx, cfg, lw, X, 2 * H, OUT, 2 * H, 2) == spt.ERR_INVALID
+        assert b"experts used <= 16, experts <= 256" in spt.lib().spt_last_error()

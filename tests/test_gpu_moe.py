@@ -412,3 +412,49 @@ def test_moe_gemm_side_stream_in_graph(O):
         assert_close(ref.cpu().numpy(), O.forward_moe_batch(lay, x, batch, q8=True), what="gemm path, side stream")
     finally:
         ctx.close()
+
+
+def test_moe_batch_beyond_selection_limit(gpu_ctx, O):
+    """A batch of more than 4096 selections runs as slices of whole tokens.
+    The reference fixture at top-2 with 2,100 tokens (4,200 selections:
+    slices of 2,048 and 52 tokens) equals the same tokens sent as those two
+    calls bit for bit, through the device and the host-slice forms, and the
+    oracle within tolerance; at GPT-OSS-120B shape 1,500 tokens (slices of
+    1,024 and 476) equal the two calls bit for bit."""
+    import torch
+
+    from spt import workloads as W
+
+    lay = moe_batch_fixture(96, 64, 8, 2, 0, "normal")
+    keep, cfg, lw = device_moe_layer(lay)
+    H = lay["hidden"]
+    batch = 2100
+    x = moe_batch_x(batch, H, "normal")
+    xd = torch.from_numpy(x).cuda()
+    whole = torch.full((batch * H,), 999.0, dtype=torch.float32, device="cuda")
+    parts = torch.full((batch * H,), -999.0, dtype=torch.float32, device="cuda")
+    gpu_ctx.forward_moe_batch(cfg, lw, xd, whole, batch)
+    gpu_ctx.forward_moe_batch(cfg, lw, xd[:2048 * H], parts[:2048 * H], 2048)
+    gpu_ctx.forward_moe_batch(cfg, lw, xd[2048 * H:], parts[2048 * H:], batch - 2048)
+    host_out = np.zeros(batch * H, np.float32)
+    gpu_ctx.forward_moe_batch_host(cfg, lw, x, host_out, batch)
+    torch.cuda.synchronize()
+    got = whole.cpu().numpy()
+    assert np.array_equal(bits(got), bits(parts.cpu().numpy()))
+    assert np.array_equal(bits(got), bits(host_out))
+    assert_close(got, O.forward_moe_batch(lay, x, batch, q8=True, threads=8), what="2,100 tokens")
+
+    shp = W.MoEShape()
+    dl = W.device_layer(gpu_ctx, seed=6, layer=0, shp=shp)
+    batch = 1500
+    Hg = shp.hidden
+    xg = torch.from_numpy(W.x_tokens(6, 0, batch, Hg)).cuda()
+    whole = torch.full((batch * Hg,), 999.0, dtype=torch.float32, device="cuda")
+    parts = torch.full((batch * Hg,), -999.0, dtype=torch.float32, device="cuda")
+    gpu_ctx.forward_moe_batch(dl.config, dl.layer, xg, whole, batch)
+    gpu_ctx.forward_moe_batch(dl.config, dl.layer, xg[:1024 * Hg], parts[:1024 * Hg], 1024)
+    gpu_ctx.forward_moe_batch(dl.config, dl.layer, xg[1024 * Hg:], parts[1024 * Hg:], batch - 1024)
+    torch.cuda.synchronize()
+    got = whole.cpu().numpy()
+    assert np.all(np.isfinite(got))
+    assert np.array_equal(bits(got), bits(parts.cpu().numpy()))
