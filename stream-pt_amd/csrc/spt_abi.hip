@@ -918,10 +918,13 @@ void q40_launches(const Q40Proj *p, int np, int64_t batch, int *k) {
 // is GGML Q8_0 blocks that every projection's GEMV reads directly.
 // A call of a few tokens (spt::q40_dec_form) runs as one launch that
 // quantizes or unpacks its input itself: no views.
+// A call of 5 to 64 tokens on inputs up to 128 blocks (spt::q40_tile_form)
+// runs as one launch over every projection reading GGML Q8_0 blocks: the
+// caller's, or those the quantizer writes into the arena (o_q34) first.
 struct Q40Plan {
-    bool views, dec;
+    bool views, dec, tile;
     int64_t nb, batch;
-    size_t o_c, o_s, o_q, o_part, total;
+    size_t o_c, o_s, o_q, o_part, o_q34, total;
 };
 
 Q40Plan q40_plan(const Q40Proj *p, int np, int64_t nb, int64_t batch, bool q8_in, size_t base) {
@@ -929,15 +932,17 @@ Q40Plan q40_plan(const Q40Proj *p, int np, int64_t nb, int64_t batch, bool q8_in
     bool gemm = false;
     size_t part = 0;
     L.dec = spt::q40_dec_form(batch, nb);
+    for (int i = 0; i < np; i++)
+        if (p[i].w->nbytes >= spt::kQ40DecMaxBytes) L.dec = false;
+    L.tile = !L.dec && spt::q40_tile_form(batch, nb);
     int k[3];
     q40_launches(p, np, batch, k);
-    for (int i = 0; i < np; i++) {
-        if (p[i].w->nbytes >= spt::kQ40DecMaxBytes) L.dec = false;
+    for (int i = 0; i < np && !L.tile; i++) {
         if (k[i] == 0) continue;
         gemm = true;
         if (k[i] == 2) part += (size_t)spt::kQ40SplitK * batch * p[i].out * 4;
     }
-    L.views = !L.dec && (!q8_in || gemm);
+    L.views = !L.dec && !L.tile && (!q8_in || gemm);
     L.nb = nb;
     L.batch = batch;
     Carve c;
@@ -946,6 +951,7 @@ Q40Plan q40_plan(const Q40Proj *p, int np, int64_t nb, int64_t batch, bool q8_in
     L.o_s = c.take(L.views ? batch * nb * 4 : 0);
     L.o_q = c.take(L.views ? batch * nb * 4 : 0);
     L.o_part = c.take(part);
+    L.o_q34 = c.take(L.tile && !q8_in ? batch * nb * spt::kQ80Block : 0);
     L.total = c.off;
     return L;
 }
@@ -958,6 +964,32 @@ Q40Plan q40_plan(const Q40Proj *p, int np, int64_t nb, int64_t batch, bool q8_in
 int run_q40_at(spt_ctx *ctx, const Q40Proj *p, int np, const Q40Plan &L, char *S, const float *x,
                const uint8_t *xq34) {
     const int64_t nb = L.nb, batch = L.batch;
+    int rc;
+    if (L.tile) {
+        if (x) {
+            uint8_t *q = (uint8_t *)(S + L.o_q34);
+            SPT_HIP(timed(ctx, SPT_KERNEL_QUANTIZE, [&] {
+                return spt::launch_quantize(ctx->stream, x, batch * nb, nullptr, nullptr, nullptr, nullptr, q, nullptr);
+            }));
+            xq34 = q;
+        }
+        spt::Q40Args g{};
+        for (int i = 0; i < np; i++) {
+            const spt_tensor *w = p[i].w;
+            if (i == 0) {
+                g = spt::Q40Args{(const uint8_t *)w->data, w->nbytes, (int)p[i].out, (int)nb, nullptr, nullptr, nullptr,
+                                 (int)batch, p[i].y, p[i].bias, p[i].btype, p[i].resid, nullptr};
+            } else {
+                g.more[i - 1] = spt::Q40Mat{(const uint8_t *)w->data, w->nbytes, (int)p[i].out, p[i].y, p[i].bias,
+                                            p[i].btype, p[i].resid};
+            }
+        }
+        g.nmore = np - 1;
+        g.xq34 = xq34;
+        if ((rc = check_cancel(ctx))) return rc;
+        SPT_HIP(timed(ctx, SPT_KERNEL_Q40, [&] { return spt::launch_q40_tile(ctx->stream, g); }));
+        return SPT_OK;
+    }
     int8_t *codes = L.views ? (int8_t *)(S + L.o_c) : nullptr;
     float *scales = L.views ? (float *)(S + L.o_s) : nullptr;
     int32_t *sumq = L.views ? (int32_t *)(S + L.o_q) : nullptr;
@@ -967,7 +999,6 @@ int run_q40_at(spt_ctx *ctx, const Q40Proj *p, int np, const Q40Plan &L, char *S
                      : spt::launch_q8_unpack(ctx->stream, xq34, batch * nb, codes, scales, sumq, nullptr);
         }));
     }
-    int rc;
     // the three launches' arguments: 0 GEMV, 1 wide GEMM, 2 split GEMM
     spt::Q40Args g[3]{};
     int ng[3] = {0, 0, 0}, kl[3];

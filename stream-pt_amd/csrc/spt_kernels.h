@@ -323,6 +323,18 @@ hipError_t launch_q40_dec(hipStream_t s, const Q40Args &a);
 hipError_t launch_q8_unpack(hipStream_t s, const uint8_t *blocks34, int64_t nblocks, int8_t *codes,
                             float *scales, int32_t *sumq, uint8_t *mxtab);
 hipError_t launch_q40_gemm(hipStream_t s, const Q40Args &a);
+// 5 to 64 tokens of inputs up to 128 blocks (spt_q40_tile.hip): a
+// workgroup per 32 output rows and 32 tokens (16 when the input is too long
+// for 32 tokens' blocks in LDS), the K blocks split over its waves and their
+// sums added in wave order; the activations as GGML Q8_0 blocks
+// (Q40Args::xq34), all the matrices of the call in one launch.  Used while a
+// tile needs at most two token groups (beyond, the GEMM reads each weight
+// byte fewer times).
+constexpr int kQ40TileMinTokens = kQ40DecTokens + 1;
+constexpr int kQ40TileMaxTokens = 64;
+constexpr int kQ40TileMaxNb = 128;
+bool q40_tile_form(int64_t batch, int64_t nb);
+hipError_t launch_q40_tile(hipStream_t s, const Q40Args &a);
 int q80_grid_waves(int rows, int nb, int n_cu);
 // RMSNorm of `batch` rows of n (spt_rmsnorm.hip): y = x * w * factor in the
 // lane order of RMSNormInto, or of normBatch with batch_order; with q8 set,
