@@ -228,11 +228,15 @@ __device__ __attribute__((always_inline)) inline void seg_blocks(const SegView &
 }
 static_assert(kSeg % 4 == 0, "seg_blocks' halves and exponent reduction");
 
-// The last segment when it holds jn < kSeg blocks.
+// The last segment when it holds jn < kSeg blocks (unrolled with a guard:
+// a loop bound by jn would index the view's pointer array at run time,
+// which puts it in scratch memory).
 template <int NTF>
 __device__ __attribute__((always_inline)) inline void seg_part(const SegView &v, int jn, float (&acc)[2][4][4],
                                                                uint32_t (&emin)[2], uint32_t (&emax)[2]) {
-    for (int j = 0; j < jn; j++) {
+#pragma unroll
+    for (int j = 0; j < kSeg - 1; j++) {
+        if (j >= jn) break;
         bf16x8 A[2];
 #pragma unroll
         for (int rf = 0; rf < 2; rf++) {

@@ -243,10 +243,17 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(2))) void k
     // pass: one load from the start table the packing wrote when there is
     // one, else found here (the expert count, the pass total and the slot
     // scan: three dependent round trips before the first weight load).
+    // Workgroup b runs on XCD b % 8 (round-robin dispatch), each XCD with its
+    // own L2: the item ranges are dealt XCD-major, so neighbouring ranges
+    // (the passes of one expert, which read the same tiles at about the same
+    // time) run on one XCD (measured: the 36-layer step at 64 tokens 9.99 ->
+    // 9.91 ms, the 32-token Zipf layer 168.7 -> 166.3 us).
+    const int G = gridDim.x;
+    const int vb = (G % 8 == 0) ? ((int)blockIdx.x % 8) * (G / 8) + (int)blockIdx.x / 8 : (int)blockIdx.x;
     const bool table = MODE != kRows && a.start != nullptr;
     int w0, w1, slot0 = 0, e0 = a.expert, p0 = 0;
     if (table) {
-        const int32_t *st = a.start + (size_t)blockIdx.x * kGvStartWords;
+        const int32_t *st = a.start + (size_t)vb * kGvStartWords;
         w0 = st[0];
         w1 = st[1];
         slot0 = st[2];
@@ -257,8 +264,8 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(2))) void k
         const int n_slots = MODE == kRows ? 1 : *r_n_active;
         const int P = MODE == kRows ? (a.ntok + kTokPerPass - 1) / kTokPerPass : rt.pass_off[n_slots];
         const int W = P * tiles;
-        w0 = (int)((int64_t)blockIdx.x * W / gridDim.x);
-        w1 = (int)((int64_t)(blockIdx.x + 1) * W / gridDim.x);
+        w0 = (int)((int64_t)vb * W / G);
+        w1 = (int)((int64_t)(vb + 1) * W / G);
         if (w0 >= w1) return;
         // slot of the first item: the number of pass_off[s] <= w0 / tiles, minus 1
         if (MODE != kRows) {
