@@ -309,16 +309,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
     const int vb = (G % kXcds == 0) ? ((int)blockIdx.x % kXcds) * (G / kXcds) + (int)blockIdx.x / kXcds : (int)blockIdx.x;
     if (vb >= total) return;
 
-    const int i16 = lane & 15, g = lane >> 4;
     const int nseg = (nb + kSeg - 1) / kSeg;
     // activation tables through buffer descriptors (the per-stage advance is
     // a scalar offset)
     const u32x4v rs_b = rsrc_words(a.btab, (uint32_t)(a.tab_rows * (uint64_t)nb * 64u));
     const u32x4v rs_d = rsrc_words(a.scales, (uint32_t)(a.tab_rows * (uint64_t)nb * 4u));
-    // per lane: stage offsets of the B slot of quarter g of block j for this lane's entry
-    uint32_t b_lane[kSeg];
-#pragma unroll
-    for (int j = 0; j < kSeg; j++) b_lane[j] = kOffB + (uint32_t)i16 * (kSeg * 64) + 16u * (uint32_t)((4 * j + g) ^ i16);
     typedef __attribute__((address_space(3))) uint8_t lds_u8;
     const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>((lds_u8 *)lds);
 
@@ -327,11 +322,23 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
     // so the workgroups finish together.
     int parity = 0;  // item parity (s_bias / s_ent / s_next buffer)
     for (int it = vb; it < total; parity ^= 1) {
+        // The lane's roles, from the lane index made opaque per item: the
+        // addresses derived from it are recomputed per item (a few VALU
+        // operations) rather than held across the item loop, where the K
+        // loop's registers leave no room for them.
+        int lane_it = lane;
+        asm volatile("" : "+v"(lane_it));
+        const int i16 = lane_it & 15, g = lane_it >> 4, tid_it = 64 * wave + lane_it;
+        // stage offsets of the B slot of quarter g of block j for this lane's entry
+        uint32_t b_lane[kSeg];
+#pragma unroll
+        for (int j = 0; j < kSeg; j++)
+            b_lane[j] = kOffB + (uint32_t)i16 * (kSeg * 64) + 16u * (uint32_t)((4 * j + g) ^ i16);
         // item -> slot: the number of slots i >= 1 whose first item is at or
         // below it (gm_tile_off is increasing), 64 slots per ballot
         int slot = 0;
         for (int c = 1; c < n_slots; c += 64) {
-            const int i = c + lane;
+            const int i = c + lane_it;
             const bool le = i < n_slots && a.gm_tile_off[i] * units <= it;
             slot += __popcll(__ballot(le));
         }
@@ -366,7 +373,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
         bool a_ok[kALoads];
 #pragma unroll
         for (int k = 0; k < kALoads; k++) {
-            const int q = 64 * (wave + kWaves * k) + lane, r = q / kASlots, pc = q - r * kASlots;
+            const int q = 64 * (wave + kWaves * k) + lane_it, r = q / kASlots, pc = q - r * kASlots;
             const int row = mrow(r);
             a_ok[k] = row < a.rows;
             a_pos[k] = ((MODE == kGateUp && r >= kBM / 2) ? le1 : le0) + (uint32_t)(a_ok[k] ? row : 0) * row_bytes +
@@ -375,7 +382,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
         uint32_t b_off[2];
 #pragma unroll
         for (int k = 0; k < 2; k++) {
-            const int q = tid + kThreads * k, t = q / (4 * kSeg), piece = (q % (4 * kSeg)) ^ (t & 15);
+            const int q = tid_it + kThreads * k, t = q / (4 * kSeg), piece = (q % (4 * kSeg)) ^ (t & 15);
             b_off[k] = kOOR;
             if (t < nt) {
                 const int ent = a.list[begin + t];
@@ -385,7 +392,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
         }
         uint32_t d_off = kOOR;
         {
-            const int idx = 64 * wave + lane, t = idx / kSeg, j = idx % kSeg;
+            const int idx = 64 * wave + lane_it, t = idx / kSeg, j = idx % kSeg;
             if (t < nt) {
                 const int ent = a.list[begin + t];
                 const int ar = MODE == kGateUp ? ent / a.topk : ent;
@@ -396,13 +403,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
         // item (staged in LDS once segment 0's loads have landed)
         float bias_v = 0.0f;
         int ent_v = -1, next_v = 0;
-        if (tid == 0) next_v = G + atomicAdd(a.claim, 1);
-        if (tid < kBM) {
-            const int m = MODE == kGateUp ? tid / (kBM / 2) : 0;
-            const int row = MODE == kGateUp ? u * (kBM / 2) + (tid & (kBM / 2 - 1)) : u * kBM + tid;
+        if (tid_it == 0) next_v = G + atomicAdd(a.claim, 1);
+        if (tid_it < kBM) {
+            const int m = MODE == kGateUp ? tid_it / (kBM / 2) : 0;
+            const int row = MODE == kGateUp ? u * (kBM / 2) + (tid_it & (kBM / 2 - 1)) : u * kBM + tid_it;
             if (row < a.rows) bias_v = bias_at(a.bias[m], a.bias_type[m], (uint64_t)e * a.rows + row);
-        } else if (tid < kBM + kBN) {
-            if (tid - kBM < nt) ent_v = a.list[begin + tid - kBM];
+        } else if (tid_it < kBM + kBN) {
+            if (tid_it - kBM < nt) ent_v = a.list[begin + tid_it - kBM];
         }
         // The DMA loads of segment s into the stage at LDS byte address st, in
         // two parts: the weights and d_x, then the B codes (a wave stalls at
@@ -478,11 +485,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
             issue_a(0, st_of(0), G::kOffD);
             issue_b(ntf_c, 0, st_of(0));
             asm volatile("" ::: "memory");
-            if (tid < kBM)
-                s_bias[parity][tid] = bias_v;
-            else if (tid < kBM + kBN)
-                s_ent[parity][tid - kBM] = ent_v;
-            if (tid == 0) s_next[parity] = next_v;
+            if (tid_it < kBM)
+                s_bias[parity][tid_it] = bias_v;
+            else if (tid_it < kBM + kBN)
+                s_ent[parity][tid_it - kBM] = ent_v;
+            if (tid_it == 0) s_next[parity] = next_v;
             asm volatile("" ::: "memory");
             for (int q = 1; q < G::kAhead && q < nseg; q++) {
                 issue_a(q, st_of(q), G::kOffD);
@@ -568,8 +575,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
             const uint32_t rows16 = (uint32_t)__ballot(sp) & 0xFFFFu;  // lanes 0..15 hold rows 0..15
             if (rows16) {
                 int ar = -1;
-                if (lane < nt) {
-                    const int en = a.list[begin + lane];
+                if (lane_it < nt) {
+                    const int en = a.list[begin + lane_it];
                     ar = MODE == kGateUp ? en / a.topk : en;
                 }
                 const int rbase = MODE == kGateUp ? 16 * wave + (kBM / 2) * rf : 32 * wave + 16 * rf;
