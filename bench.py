@@ -37,8 +37,8 @@ INT8_DENSE_TOPS = 5000.0     # MI355X dense int8 MFMA
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "k_mx_mfma_decode_b64_36layers.md")
 MFMA_PROFILE = os.path.join(ROOT, "profiles", "k_mx_gemm_prefill_b512_hot.md")
 # grouped-GEMM policy of the library's default (spt_abi.hip: kGemmMinGroup,
-# kGemmMinSelections; select: items must fill the device)
-GEMM_MIN_GROUP, GEMM_MIN_SELECTIONS = 9, 1024
+# kGemmMinSelections; select: items must fill half the device)
+GEMM_MIN_GROUP, GEMM_MIN_SELECTIONS = 9, 384
 # host threads for the CPU baseline: the box's CPU share per GPU
 CPU_SHARE = 16
 
@@ -346,7 +346,9 @@ def prefill(args, ctx, dl, shp, W, stream, reps=20):
     the library's stream), the weight bytes of the touched experts over the
     layer time, and for the grouped GEMM its algorithmic multiply-adds
     (selections of GEMM experts x 3 x hidden x expert dim) over its kernel
-    time against the dense bf16 MFMA peak it runs on and the int8 peak."""
+    time against the dense bf16 MFMA peak it runs on (it issues bf16 MFMAs
+    only); at 512 tokens, the Q4_0 projections' int8 MFMA rate (the int8
+    MFMA kernel of this path) against the dense int8 peak."""
     import numpy as np
     import torch
 
@@ -368,7 +370,7 @@ def prefill(args, ctx, dl, shp, W, stream, reps=20):
         distinct = int(np.count_nonzero(c))
         n = B * k
         big = c[c >= GEMM_MIN_GROUP]
-        gemm_on = n >= GEMM_MIN_SELECTIONS and int(np.sum((big + 63) // 64)) * ((D + 127) // 128) >= 256
+        gemm_on = n >= GEMM_MIN_SELECTIONS and int(np.sum((big + 63) // 64)) * ((D + 127) // 128) >= 128
         gemm_sel = int(big.sum()) if gemm_on else 0
         # warm for at least 60 ms of back-to-back layers: a few calls after
         # the host-side set-up above the 512-token layer still runs about
@@ -407,12 +409,19 @@ def prefill(args, ctx, dl, shp, W, stream, reps=20):
         if gemm_sel and gemm_us > 0:
             macs = gemm_sel * 3 * H * D
             tops = 2 * macs / (gemm_us * 1e-6) / 1e12
-            res["gemm"] = {"macs": macs, "us": round(gemm_us, 1), "tops": round(tops, 2),
-                           "frac_bf16_dense": round(tops / BF16_DENSE_TFLOPS, 4),
-                           "frac_int8_dense": round(tops / INT8_DENSE_TOPS, 4),
+            res["gemm"] = {"mfma": "bf16 (v_mfma_f32_16x16x32_bf16)", "macs": macs, "us": round(gemm_us, 1),
+                           "tflops_bf16": round(tops, 2), "frac_bf16_dense": round(tops / BF16_DENSE_TFLOPS, 4),
                            "mfma_util_measured": measured_mfma_util(name)}
         if name == "hot_b512":
-            res["q40_attention"] = q40_projections(ctx, B, W, stream, reps)
+            qa = q40_projections(ctx, B, W, stream, reps)
+            # the four projections' int8 multiply-adds (k_q40_gemm, int8 MFMA)
+            ops = 2 * B * sum(din * dout for _, din, dout in W.q40_projection_shapes())
+            q_us = qa["fused_qkv_o_us"]
+            qa["int8_mfma"] = {"mfma": "int8 (v_mfma_i32_16x16x32_i8)", "ops": ops,
+                               "tops": round(ops / (q_us * 1e-6) / 1e12, 2),
+                               "frac_int8_dense": round(ops / (q_us * 1e-6) / 1e12 / INT8_DENSE_TOPS, 4),
+                               "mfma_util_measured_pct": (measured_mfma_util(name) or {}).get("q40_gemm_pct")}
+            res["q40_attention"] = qa
         out[name] = res
         log(f"prefill {name}: {json.dumps(res)}")
     # the dense Q4_0 projections alone (GEMV at B=1, small GEMM at B=32)

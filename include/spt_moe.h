@@ -130,8 +130,8 @@ int spt_ctx_set_cancel_flag(struct spt_ctx *ctx, const volatile int32_t *flag);
 /* Expert groups of at least min_group selections run through the grouped
  * GEMM (bf16 MFMA, up to 64 selections per pass over the expert's weights);
  * smaller groups through the grouped GEMV (4 per pass).  0 restores the
- * default policy: groups of 9 or more when the batch holds at least 1024
- * selections and those groups' GEMM work fills the device.  Results are the
+ * default policy: groups of 9 or more when the batch holds at least 384
+ * selections and those groups' GEMM work fills half the device.  Results are the
  * same either way within the fp32 tolerance (the per-block sums are exact on
  * both).  No reference counterpart: the reference picks its CPU loop by tile
  * size (forward/mxfp4_batch.go:55-95). */

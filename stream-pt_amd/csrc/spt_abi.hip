@@ -398,11 +398,16 @@ int copy_tap(spt_ctx *ctx, void *dst, const void *src, size_t bytes) {
 // Default policy for the grouped GEMM (measured on MI355X with GPT-OSS
 // shapes): groups of at least kGemmMinGroup selections (three or more GEMV
 // passes over the expert's weights) go to the GEMM when the batch holds at
-// least kGemmMinSelections selections and their work items fill the device;
-// below that the GEMV's passes are faster (a GEMM item walks the whole input
-// dimension serially, so a few large groups leave most CUs idle).
+// least kGemmMinSelections selections and their work items fill at least
+// half the device; below that the GEMV's passes are faster (a GEMM item
+// walks the whole input dimension serially, and the persistent GEMV holds
+// every CU until it ends, so a few GEMM items run after it as a tail).
+// Measured per layer, Zipf(1.1) routing, default against GEMV only: 96
+// tokens 299 / 322 us, 128: 338 / 373, 160: 379 / 483, 192: 392 / 545;
+// uniform routing at 96 and 128 tokens (one or two groups of 9 or 10) stays
+// on the GEMV (328, 400 us; 386, 457 with those groups on the GEMM).
 constexpr int kGemmMinGroup = 9;
-constexpr int kGemmMinSelections = 1024;
+constexpr int kGemmMinSelections = 384;
 // Batches of up to this many selections (topk <= 4, no GEMM group) take the
 // decode path: top-k inside the gate/up launch, combine inside the down
 // launch, a workgroup per selection (spt_mx_decode.hip).
@@ -422,7 +427,7 @@ struct MoELayout {
 // An expert's group holds at most n selections: with fewer than the
 // threshold no expert can reach the GEMM, which is then not launched.  An
 // explicit threshold (spt_ctx_set_gemm_min_group) applies as given; the
-// default also needs kGemmMinSelections and a full device of items.  The
+// default also needs kGemmMinSelections and half a device of items.  The
 // fp32 act buffer exists only for the act tap.
 MoELayout moe_layout(const spt_ctx *ctx, const MoEDims &m, bool act_tap, size_t base) {
     const int64_t h = m.h, d = m.d, E = m.E, B = m.batch, n = m.batch * m.k;
@@ -476,7 +481,7 @@ int run_moe_at(spt_ctx *ctx, const spt_moe_layer *lw, const float *x, float *out
     so.n_active = (int32_t *)(S + L.o_na);
     so.gemm_min = use_gemm ? gemm_min : INT_MAX;
     so.gemm_units = (int32_t)((d + 127) / 128);
-    so.gemm_min_items = forced ? 0 : ctx->n_cu;
+    so.gemm_min_items = forced ? 0 : ctx->n_cu / 2;
     so.gv_active = (int32_t *)(S + L.o_gv);
     so.gv_n = (int32_t *)(S + L.o_gvn);
     so.gv_pass_off = (int32_t *)(S + L.o_gvp);
