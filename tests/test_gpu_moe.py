@@ -199,6 +199,39 @@ def test_moe_prefill_zipf(gpu_ctx, O, batch, path):
     check_stagewise(O, lay, x, batch, g, logits_in=logits)
 
 
+def test_moe_prefill_mid_batch_gemm(gpu_ctx, O):
+    """128 tokens (512 selections) with Zipf(1.1) popularity: under the
+    default policy the groups of 9 or more go to the grouped GEMM (at least
+    384 selections, and their items fill half the device); routing, packing,
+    the Q8_0 stages and the combine are checked on every selection, the
+    projections on a sample holding the largest group's first and last
+    entries and random others."""
+    from spt import synth
+    from spt import workloads as W
+
+    batch = 128
+    shp = W.MoEShape()
+    dl = W.device_layer(gpu_ctx, seed=6, layer=0, shp=shp)
+    x = W.x_tokens(6, 0, batch, shp.hidden)
+    logits = synth.zipf_logits(synth.stream_key(6, 99), batch, shp.experts, 1.1)
+    gpu_ctx.enable_timing(True)
+    gpu_ctx.read_timing()
+    g = _run(gpu_ctx, dl.config, dl.layer, x, batch, logits_in=logits)
+    kt = gpu_ctx.read_timing()
+    gpu_ctx.enable_timing(False)
+    counts, offsets, lst = g["counts"], g["offsets"], g["list"]
+    big = counts[counts >= 9]
+    assert int(np.sum((big + 63) // 64)) * ((shp.expert_dim + 127) // 128) >= 128
+    assert kt["gate_up_gemm"][1] == 1 and kt["down_gemm"][1] == 1, kt
+    top = int(np.argmax(counts))
+    grp = lst[offsets[top]:offsets[top + 1]]
+    rng = np.random.default_rng(6)
+    sample = set(grp[:3].tolist()) | set(grp[-3:].tolist())
+    sample |= set(rng.choice(batch * shp.topk, 24, replace=False).tolist())
+    lay = W.host_layer(6, 0, shp, experts=np.unique(g["ids"][sorted(sample)]))
+    check_stagewise(O, lay, x, batch, g, logits_in=logits, sample=sorted(sample))
+
+
 def test_moe_prefill_hot_expert(gpu_ctx, O):
     """512 tokens, 25% of them forced to one hot expert and the rest Zipf(1.1)
     (the long-prompt chunk): groups from 1 to hundreds of rows (by default
