@@ -992,7 +992,7 @@ int run_q40_at(spt_ctx *ctx, const Q40Proj *p, int np, const Q40Plan &L, char *S
         g.nmore = np - 1;
         g.xq34 = xq34;
         if ((rc = check_cancel(ctx))) return rc;
-        SPT_HIP(timed(ctx, SPT_KERNEL_Q40, [&] { return spt::launch_q40_tile(ctx->stream, g); }));
+        SPT_HIP(timed(ctx, SPT_KERNEL_Q40, [&] { return spt::launch_q40_tile(ctx->stream, g, ctx->n_cu); }));
         return SPT_OK;
     }
     int8_t *codes = L.views ? (int8_t *)(S + L.o_c) : nullptr;

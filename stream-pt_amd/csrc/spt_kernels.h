@@ -324,7 +324,8 @@ hipError_t launch_q8_unpack(hipStream_t s, const uint8_t *blocks34, int64_t nblo
                             float *scales, int32_t *sumq, uint8_t *mxtab);
 hipError_t launch_q40_gemm(hipStream_t s, const Q40Args &a);
 // 5 to 64 tokens of inputs up to 128 blocks (spt_q40_tile.hip): a
-// workgroup per 32 output rows and 32 tokens (16 when the input is too long
+// workgroup per 16 output rows (when those workgroups all fit on the n_cu
+// compute units at once) or 32, and 32 tokens (16 when the input is too long
 // for 32 tokens' blocks in LDS), the K blocks split over its waves and their
 // sums added in wave order; the activations as GGML Q8_0 blocks
 // (Q40Args::xq34), all the matrices of the call in one launch.  Used while a
@@ -334,7 +335,7 @@ constexpr int kQ40TileMinTokens = kQ40DecTokens + 1;
 constexpr int kQ40TileMaxTokens = 64;
 constexpr int kQ40TileMaxNb = 128;
 bool q40_tile_form(int64_t batch, int64_t nb);
-hipError_t launch_q40_tile(hipStream_t s, const Q40Args &a);
+hipError_t launch_q40_tile(hipStream_t s, const Q40Args &a, int n_cu);
 int q80_grid_waves(int rows, int nb, int n_cu);
 // RMSNorm of `batch` rows of n (spt_rmsnorm.hip): y = x * w * factor in the
 // lane order of RMSNormInto, or of normBatch with batch_order; with q8 set,

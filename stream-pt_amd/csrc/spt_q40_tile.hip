@@ -1,18 +1,23 @@
 // spt_q40_tile.hip -- Q4_0 x Q8_0 projections of 5 to 64 tokens, a
-// workgroup per 32 output rows and 16 or 32 tokens, on the gfx950 int8 MFMA.
+// workgroup per 16 or 32 output rows and 16 or 32 tokens, on the gfx950 int8
+// MFMA.
 //
 // forward.MulQ40BatchInto (forward/q40.go:40-103) at the batch sizes of
 // continuous-batching decode and short prefill chunks: y[t][row] =
 // sum_b float(isum) * (d_w * d_x) with isum = sum (n - 8) * q the exact int32
-// block sum.  At these sizes a projection is a few megabytes of weights, and
-// what bounds it is how many bytes each compute unit must bring in (a CU
-// sustains about 50 GB/s with its ~48 KB of loads in flight): every
-// workgroup needs its rows' weights (18 bytes per block) and all of its
-// tokens' Q8_0 blocks (34 bytes per block), so tiles of 32 rows x 16 or 32
-// tokens keep that near its minimum while the tiles still spread over the
-// CUs (32 tokens when both images fit in LDS: inputs up to 91 blocks).
+// block sum.  At these sizes a projection is a few megabytes of weights;
+// every workgroup needs its rows' weights (18 bytes per block) and all of
+// its tokens' Q8_0 blocks (34 bytes per block), and once they are in LDS its
+// multiply is bound by the compute unit's VALU: three ops per output and
+// block (the int32 sum to fp32, d_w * d_x, the fma) against one MFMA per
+// 256 outputs (32 rows x 32 tokens over 90 blocks: 3.7 us of a 9 us
+// workgroup, the loads 2 us).  So the launch takes 16-row tiles when their
+// workgroups all run at once, and 32-row tiles (half the workgroups, each
+// loading the tokens' blocks once for twice the rows) when they would not;
+// 32 tokens per workgroup when both images fit in LDS (inputs up to 91
+// blocks).
 // Everything is loaded at the start by LDS DMA, 1 KB per wave instruction:
-//   * the 32 rows of the tile (GGUF rows are contiguous) and the tokens'
+//   * the rows of the tile (GGUF rows are contiguous) and the tokens'
 //     GGML Q8_0 blocks ([ntok][nb] x 34 bytes: the caller's, or written by
 //     the quantizer just before -- no unpacking launch), each as one run of
 //     bytes; when the rows (tokens) start on 16-byte boundaries they are
@@ -22,7 +27,7 @@
 //   * the rows' fp16 d_w are then widened into a [block][row] table (one
 //     16-byte read gives the four rows of an MFMA lane's results).
 // The K blocks are split over the eight waves (wave w takes blocks w, w + 8,
-// ...), each multiplying its blocks for both 16-row halves and every token
+// ...), each multiplying its blocks for every 16-row half and token
 // fragment, the next
 // block's LDS reads issued before the current block's MFMAs; the waves'
 // partial sums are added in wave order through LDS, so there is no split-K
@@ -48,10 +53,14 @@ typedef float v4f_t __attribute__((ext_vector_type(4)));
 
 constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;
-constexpr int kRT = 2;  // 16-row halves per tile
-constexpr int kTileRows = 16 * kRT;
 constexpr size_t kMaxLds = 160 * 1024;
-__host__ __device__ constexpr uint32_t part_bytes(int ntf) { return (uint32_t)kWaves * kRT * ntf * 4 * 64 * 4; }
+// The waves' partial sums, [wave][register][lane] with registers kPartPitch
+// floats apart: the 32 outputs a half-wave adds (16 or 32 rows of one token)
+// then fall in distinct banks.
+constexpr int kPartPitch = 66;
+__host__ __device__ constexpr uint32_t part_bytes(int rt, int ntf) {
+    return (uint32_t)kWaves * rt * ntf * 4 * kPartPitch * 4;
+}
 
 // How `n` runs of `len` bytes, `len` apart from byte `first` of a buffer,
 // are copied to LDS: pitched (row by row, each run at pitch * i, when every
@@ -76,14 +85,14 @@ struct TileLayout {
     Runs w, x;
     uint32_t xo, dwo, total;  // LDS offsets of the tokens' image and of the d_w table
 };
-__host__ __device__ inline TileLayout tile_layout(uint32_t wfirst, uint32_t xfirst, int nb, int ntf) {
+__host__ __device__ inline TileLayout tile_layout(uint32_t wfirst, uint32_t xfirst, int nb, int rt, int ntf) {
     TileLayout L;
-    L.w = plan_runs(wfirst, (uint32_t)nb * kQ40Block, kTileRows);
+    L.w = plan_runs(wfirst, (uint32_t)nb * kQ40Block, 16 * rt);
     L.x = plan_runs(xfirst, (uint32_t)nb * kQ80Block, 16 * ntf);
-    const uint32_t w = L.w.bytes > part_bytes(ntf) ? L.w.bytes : part_bytes(ntf);  // partial sums reuse it
+    const uint32_t w = L.w.bytes > part_bytes(rt, ntf) ? L.w.bytes : part_bytes(rt, ntf);  // partial sums reuse it
     L.xo = (w + 15u) & ~15u;
     L.dwo = (L.xo + L.x.bytes + 15u) & ~15u;
-    L.total = L.dwo + (uint32_t)nb * kTileRows * 4u;
+    L.total = L.dwo + (uint32_t)nb * 16u * (uint32_t)rt * 4u;
     return L;
 }
 
@@ -150,10 +159,12 @@ __device__ inline TileJob tile_job(int id, int groups) {
     return TileJob{(rest / groups) * 8 + (id & 7), rest % groups};
 }
 
-template <int NTF>
+template <int RT, int NTF>
 __global__ __launch_bounds__(kThreads) void k_q40_tile(Q40Args args, int tiles, int groups) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    constexpr int kTokens = 16 * NTF;  // tokens per workgroup
+    constexpr int kRT = RT;             // 16-row halves per tile
+    constexpr int kTileRows = 16 * RT;  // rows per workgroup
+    constexpr int kTokens = 16 * NTF;   // tokens per workgroup
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int i16 = lane & 15, g = lane >> 4;
@@ -174,7 +185,7 @@ __global__ __launch_bounds__(kThreads) void k_q40_tile(Q40Args args, int tiles, 
     const u32x4v rsx =
         rsrc_words(reinterpret_cast<const void *>(xa - xle), (uint32_t)(((uint64_t)ntok * xb + xle + 15u) & ~15ull));
     const uint32_t wfirst = wle + (uint32_t)r0 * rb, xfirst = xle + (uint32_t)t0 * xb;
-    const TileLayout L = tile_layout(wfirst, xfirst, nb, NTF);
+    const TileLayout L = tile_layout(wfirst, xfirst, nb, RT, NTF);
     typedef __attribute__((address_space(3))) uint8_t lds_u8;
     const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>((lds_u8 *)lds);
     stage_runs(rsw, lds0, wfirst, rb, kTileRows, L.w, groups == 1, wave, lane);
@@ -272,45 +283,73 @@ __global__ __launch_bounds__(kThreads) void k_q40_tile(Q40Args args, int tiles, 
     }
 
     // 4. the waves' partial sums (over the weights image, every wave done
-    // with it) added in wave order; thread k takes row k % 32 of token k / 32
+    // with it) added in wave order; thread k takes row k % tile rows of
+    // token k / tile rows
+    constexpr int kRegs = kRT * NTF * 4;
     lds_barrier();
-    float *part = reinterpret_cast<float *>(lds);  // [wave][h][tf][r][lane]
+    float *part = reinterpret_cast<float *>(lds);  // [wave][h][tf][r] x kPartPitch + lane
 #pragma unroll
     for (int h = 0; h < kRT; h++)
 #pragma unroll
         for (int tf = 0; tf < NTF; tf++)
 #pragma unroll
-            for (int r = 0; r < 4; r++) part[(((wave * kRT + h) * NTF + tf) * 4 + r) * 64 + lane] = acc[h][tf][r];
+            for (int r = 0; r < 4; r++)
+                part[(wave * kRegs + (h * NTF + tf) * 4 + r) * kPartPitch + lane] = acc[h][tf][r];
     lds_barrier();
 #pragma unroll
     for (int k = tid; k < kTileRows * kTokens; k += kThreads) {
         const int rho = k & (kTileRows - 1), tl = k / kTileRows;
         const int h = rho >> 4, rr = rho & 15, tf = tl >> 4;
-        const int reg = ((h * NTF + tf) * 4 + (rr & 3)) * 64 + 16 * (rr >> 2) + (tl & 15);
+        const int reg = ((h * NTF + tf) * 4 + (rr & 3)) * kPartPitch + 16 * (rr >> 2) + (tl & 15);
         float v = part[reg];
 #pragma unroll
-        for (int w = 1; w < kWaves; w++) v = v + part[w * kRT * NTF * 4 * 64 + reg];
+        for (int w = 1; w < kWaves; w++) v = v + part[w * kRegs * kPartPitch + reg];
         const int row = r0 + rho, t = t0 + tl;
         if (row < a.rows && t < ntok) q40_store(a, (size_t)t * a.rows + row, row, v);
     }
 }
 
-// The LDS the tile launch needs for an input of nb blocks and 16 * ntf
-// tokens per workgroup: the largest of the plans for 16-byte-aligned runs
-// (pitched) and for runs at the largest even lead (14 bytes) of a
-// contiguous copy.
-size_t q40_tile_lds(int nb, int ntf) {
+// The LDS the tile launch needs for an input of nb blocks, 16 * rt rows and
+// 16 * ntf tokens per workgroup: the largest of the plans for
+// 16-byte-aligned runs (pitched) and for runs at the largest even lead
+// (14 bytes) of a contiguous copy.
+size_t q40_tile_lds(int nb, int rt, int ntf) {
     size_t worst = 0;
     for (uint32_t wle : {0u, 14u})
         for (uint32_t xle : {0u, 14u}) {
-            const size_t t = tile_layout(wle, xle, nb, ntf).total;
+            const size_t t = tile_layout(wle, xle, nb, rt, ntf).total;
             worst = t > worst ? t : worst;
         }
     return worst;
 }
 
-// Tokens per workgroup: 32 when they and the tile fit in LDS, else 16.
-int tile_tokens(int nb) { return q40_tile_lds(nb, 2) <= kMaxLds ? 32 : 16; }
+// Tokens per workgroup: 32 when they and a 32-row tile fit in LDS, else 16.
+int tile_tokens(int nb) { return q40_tile_lds(nb, 2, 2) <= kMaxLds ? 32 : 16; }
+
+// Workgroups of a launch over rt x 16-row tiles and 16 * ntf tokens.
+int tile_grid(const Q40Args &a, int rt, int ntf) {
+    const int tr = 16 * rt;
+    int tiles = (a.rows + tr - 1) / tr;
+    for (int i = 0; i < a.nmore; i++) tiles += (a.more[i].rows + tr - 1) / tr;
+    const int groups = (a.ntok + 16 * ntf - 1) / (16 * ntf);
+    return (tiles + 7) / 8 * 8 * groups;
+}
+
+template <int RT, int NTF>
+hipError_t launch_shape(hipStream_t s, const Q40Args &a) {
+    constexpr int kTileRows = 16 * RT;
+    const size_t lds = q40_tile_lds(a.nb, RT, NTF);
+    if (lds > kMaxLds) return hipErrorInvalidConfiguration;
+    // one-time opt-in to more than 64 KB of dynamic LDS
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_q40_tile<RT, NTF>),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxLds);
+    if (attr != hipSuccess) return attr;
+    int nt = (a.rows + kTileRows - 1) / kTileRows;
+    for (int i = 0; i < a.nmore; i++) nt += (a.more[i].rows + kTileRows - 1) / kTileRows;
+    const int groups = (a.ntok + 16 * NTF - 1) / (16 * NTF);
+    hipLaunchKernelGGL((k_q40_tile<RT, NTF>), dim3(tile_grid(a, RT, NTF)), dim3(kThreads), lds, s, a, nt, groups);
+    return hipGetLastError();
+}
 
 }  // namespace
 
@@ -319,35 +358,22 @@ bool q40_tile_form(int64_t batch, int64_t nb) {
     return batch <= 2 * tile_tokens((int)nb);
 }
 
-hipError_t launch_q40_tile(hipStream_t s, const Q40Args &a) {
+hipError_t launch_q40_tile(hipStream_t s, const Q40Args &a, int n_cu) {
     if (a.rows <= 0 || a.ntok <= 0 || a.nb <= 0) return hipSuccess;
-    if (a.nmore < 0 || a.nmore > 2 || !a.xq34 || a.nb > kQ40TileMaxNb || a.ntok > kQ40TileMaxTokens)
+    if (a.nmore < 0 || a.nmore > 2 || !a.xq34 || a.nb > kQ40TileMaxNb || a.ntok > kQ40TileMaxTokens || n_cu <= 0)
         return hipErrorInvalidValue;
-    const int ntf = a.ntok > 16 && tile_tokens(a.nb) == 32 ? 2 : 1;
-    const size_t lds = q40_tile_lds(a.nb, ntf);
-    if (lds > kMaxLds) return hipErrorInvalidConfiguration;
-    // one-time opt-in to more than 64 KB of dynamic LDS
-    static const hipError_t attr = [] {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_q40_tile<1>),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxLds);
-        if (e == hipSuccess)
-            e = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_q40_tile<2>),
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxLds);
-        return e;
-    }();
-    if (attr != hipSuccess) return attr;
-    int tiles = (a.rows + kTileRows - 1) / kTileRows;
-    for (int i = 0; i < a.nmore; i++) {
+    for (int i = 0; i < a.nmore; i++)
         if (a.more[i].rows <= 0) return hipErrorInvalidValue;
-        tiles += (a.more[i].rows + kTileRows - 1) / kTileRows;
-    }
-    const int groups = (a.ntok + 16 * ntf - 1) / (16 * ntf);
-    const int grid = (tiles + 7) / 8 * 8 * groups;
-    if (ntf == 2)
-        hipLaunchKernelGGL(k_q40_tile<2>, dim3(grid), dim3(kThreads), lds, s, a, tiles, groups);
-    else
-        hipLaunchKernelGGL(k_q40_tile<1>, dim3(grid), dim3(kThreads), lds, s, a, tiles, groups);
-    return hipGetLastError();
+    const int ntf = a.ntok > 16 && tile_tokens(a.nb) == 32 ? 2 : 1;
+    // 16-row tiles when their workgroups all run at once (as many as the LDS
+    // lets each compute unit hold), else 32-row tiles: the multiply is bound
+    // by the compute unit's VALU (three ops per output and block), so twice
+    // the workgroups on idle compute units halve it, while a second round
+    // of workgroups costs a whole workgroup's time again.
+    const int per_cu = (int)(kMaxLds / q40_tile_lds(a.nb, 1, ntf));
+    const bool rows16 = tile_grid(a, 1, ntf) <= n_cu * per_cu;
+    if (rows16) return ntf == 2 ? launch_shape<1, 2>(s, a) : launch_shape<1, 1>(s, a);
+    return ntf == 2 ? launch_shape<2, 2>(s, a) : launch_shape<2, 1>(s, a);
 }
 
 }  // namespace spt
