@@ -41,40 +41,28 @@ constexpr size_t kMaxMxLds = 120 * 1024;  // dynamic LDS; with the static part (
 constexpr int kStageUnits = 2;             // units per stage set (two sets: one fills while the other is flushed)
 
 
-// A wave's part of a tile image in flight: four loads of 1 KB per group.
-// The loads are issued and waited for with inline assembly, out of sight of
-// the compiler's wait-count analysis, which turns conservative (a full
-// drain) at the loop's control-flow joins: tile_issue writes the registers
-// asynchronously, tile_wait (s_waitcnt vmcnt(0)) names every one of them,
-// and only tile_store reads them, after the wait.  Each issue block opens
-// with five wait states: its descriptor and offset SGPRs may have just been
-// written by a VALU instruction, which a following VMEM read must not see
-// early, and the compiler cannot pad inside inline assembly.  Offsets past
-// the descriptor's range read zeros.  The loads are nontemporal (`nt`): each
-// weight byte is read once per pass and the stream is far larger than the
-// caches, and a plain streaming read reaches about 7.0 TB/s with the bit
-// against 6.1 TB/s without it on MI355X.
+// A wave's part of a tile image in flight: four loads of 1 KB per group,
+// ordinary buffer loads whose waits the compiler places (before the LDS
+// stores that read the registers).  Every step of the loop issues every
+// group, at an offset past the descriptor's range (read as zeros, no
+// memory traffic) when there is no next unit or the group is not the
+// wave's, so that all paths into the loop's joins carry the same loads in
+// the same order and the compiler's wait counts stay exact there (with the
+// issue conditional it drained every load at the joins).  The loads are
+// nontemporal (cache policy bit 1, `nt`): each weight byte is read once per
+// pass and the stream is far larger than the caches, and a plain streaming
+// read reaches about 7.0 TB/s with the bit against 6.1 TB/s without it on
+// MI355X.
+constexpr uint32_t kPastRange = 0x80000000u;
 struct TileRegs {
     u32x4v q[4 * kWaveGroups];
 };
 
 template <int G>
-__device__ inline void tile_issue(TileRegs &t, uint32_t vo, const u32x4v &rs, uint32_t so) {
-    asm volatile(
-        "s_nop 4\n\t"
-        "buffer_load_dwordx4 %0, %4, %5, %6 offen nt\n\t"
-        "buffer_load_dwordx4 %1, %4, %5, %6 offen offset:1024 nt\n\t"
-        "buffer_load_dwordx4 %2, %4, %5, %6 offen offset:2048 nt\n\t"
-        "buffer_load_dwordx4 %3, %4, %5, %6 offen offset:3072 nt"
-        : "=&v"(t.q[4 * G]), "=&v"(t.q[4 * G + 1]), "=&v"(t.q[4 * G + 2]), "=&v"(t.q[4 * G + 3])
-        : "v"(vo), "s"(rs), "s"(so));
-}
-
-__device__ inline void tile_wait(TileRegs &t) {
-    static_assert(kWaveGroups == 3, "operand list below");
-    asm volatile("s_waitcnt vmcnt(0) ; spt tile wait"
-                 : "+v"(t.q[0]), "+v"(t.q[1]), "+v"(t.q[2]), "+v"(t.q[3]), "+v"(t.q[4]), "+v"(t.q[5]),
-                   "+v"(t.q[6]), "+v"(t.q[7]), "+v"(t.q[8]), "+v"(t.q[9]), "+v"(t.q[10]), "+v"(t.q[11]));
+__device__ inline void tile_issue(TileRegs &t, uint32_t vo, rsrc_t r, uint32_t so) {
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+        t.q[4 * G + k] = __builtin_bit_cast(u32x4v, __builtin_amdgcn_raw_buffer_load_b128(r, vo + 1024u * k, so, 2));
 }
 
 // After the stores of a step: the LDS writes are complete, so their data
@@ -319,7 +307,7 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(2))) void k
     // Registers of the next unit: this wave's groups of its tile image, and
     // the bias words of this thread's row.
     TileRegs tr;
-    u32x4v nrs = {0u, 0u, 0u, 0u};
+    rsrc_t nrs = __builtin_amdgcn_make_buffer_rsrc(nullptr, (short)0, 0, kRsrcWord3);
     uint32_t na0 = 0u;
     bool nxt_ok = false;
     const uint32_t vo = 16u * (uint32_t)lane;
@@ -328,7 +316,7 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(2))) void k
     auto issue = [&](auto gc) {
         constexpr int G = decltype(gc)::value;
         static_assert(G < kWaveGroups, "group");
-        if (nxt_ok && G < gmine) tile_issue<G>(tr, vo, nrs, na0 + 4096u * G);
+        tile_issue<G>(tr, vo, nrs, nxt_ok && G < gmine ? na0 + 4096u * G : kPastRange);
     };
     uint32_t b0r = 0u, b1r = 0u;
     auto prefetch = [&](const Cursor &c) {
@@ -347,9 +335,8 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(2))) void k
             const uint32_t le = (uint32_t)(mb & 15u);
             const uint64_t base = mb - le;
             // descriptor words: base, base_hi (stride 0), num_records, format
-            const u32x4v rs = {(uint32_t)base, (uint32_t)(base >> 32) & 0xFFFFu,
-                               (uint32_t)((a.expert_bytes + le + 15u) & ~15ull), (uint32_t)kRsrcWord3};
-            nrs = rs;
+            nrs = __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void *>(base), (short)0,
+                                                    (int)(uint32_t)((a.expert_bytes + le + 15u) & ~15ull), kRsrcWord3);
             na0 = ((le + (uint32_t)row0 * row_bytes) & ~15u) + 4096u * (uint32_t)g0;
             nxt_ok = true;
         }
@@ -472,17 +459,18 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(2))) void k
         const Cursor u = cur;
         const PassTokens pt = npt;
         if (u.slot != staged_slot || u.p != staged_p) {
-            // A new token pass: its B operands and d_x, loaded before the
-            // wait below so that it covers them (pass changes are rare:
-            // each workgroup walks a contiguous range of work items).
+            // A new token pass: its B operands and d_x (pass changes are
+            // rare: each workgroup walks a contiguous range of work items).
             load_pass_b(pb, a.nb, a.mxtab, a.scales, pt.arow, pt.nt, L, wave);
             npair = (pt.nt + 1) >> 1;
             staged_slot = u.slot;
             staged_p = u.p;
         }
-        tile_wait(tr);
-        // Everything loaded before the wait has arrived; take it now so no
-        // later use waits on the next unit's loads.
+        // The pass's B operands and the bias words are taken here, before
+        // the next unit's loads are issued, so that no later use of them
+        // waits on those loads (a wait covers every older load); a new
+        // pass's B operands, loaded after this unit's tile loads, wait for
+        // those too, as the image stores below would.
 #pragma unroll
         for (int j = 0; j < kChunksPerWave; j++)
 #pragma unroll

@@ -81,8 +81,14 @@ struct PassB {
 
 // Loads a pass's B operands from the digit tables (zero past nb, for the
 // unused token slots and for the lane's empty half) and d_x from the scales.
+// Every lane loads (the table's first block where it has nothing to load,
+// then zeroes it), so the twelve loads go out back to back and are waited
+// for once, instead of one round trip each behind a branch.
 __device__ inline void load_pass_b(PassB &pb, int nb, const uint8_t *mxtab, const float *scales,
                                    const int (&arow)[kTokPerPass], int nt, const LaneRole &L, int wave) {
+    u32x4v v[kChunksPerWave][2];
+    float d[kChunksPerWave][2];
+    bool okb[kChunksPerWave][2], okd[kChunksPerWave][2];
 #pragma unroll
     for (int j = 0; j < kChunksPerWave; j++) {
         const int b = 4 * (wave + kWaves * j) + L.gc;
@@ -91,15 +97,23 @@ __device__ inline void load_pass_b(PassB &pb, int nb, const uint8_t *mxtab, cons
             const int t = 2 * tp + L.slot;
             const bool ok = t < nt && b < nb;
             const int ar = t == 0 ? arow[0] : t == 1 ? arow[1] : t == 2 ? arow[2] : arow[3];
-            const size_t blk = (size_t)ar * nb + b;
-            u32x4v v = {0u, 0u, 0u, 0u};
-            if (ok && (L.lo_on || L.hi_on)) v = *reinterpret_cast<const u32x4v *>(mxtab + blk * 64 + L.boff);
-            const u32x4v z = {0u, 0u, 0u, 0u};
-            pb.b[j][tp] = L.lo_on ? __builtin_bit_cast(v8i, __builtin_shufflevector(v, z, 0, 1, 2, 3, 4, 5, 6, 7))
-                                  : __builtin_bit_cast(v8i, __builtin_shufflevector(z, v, 0, 1, 2, 3, 4, 5, 6, 7));
-            pb.dx[j][tp] = ok ? scales[blk] : 0.0f;
+            const size_t blk = ok ? (size_t)ar * nb + b : 0;
+            okd[j][tp] = ok;
+            okb[j][tp] = ok && (L.lo_on || L.hi_on);
+            v[j][tp] = *reinterpret_cast<const u32x4v *>(mxtab + blk * 64 + (okb[j][tp] ? L.boff : 0));
+            d[j][tp] = scales[blk];
         }
     }
+#pragma unroll
+    for (int j = 0; j < kChunksPerWave; j++)
+#pragma unroll
+        for (int tp = 0; tp < 2; tp++) {
+            const u32x4v z = {0u, 0u, 0u, 0u};
+            const u32x4v w = okb[j][tp] ? v[j][tp] : z;
+            pb.b[j][tp] = L.lo_on ? __builtin_bit_cast(v8i, __builtin_shufflevector(w, z, 0, 1, 2, 3, 4, 5, 6, 7))
+                                  : __builtin_bit_cast(v8i, __builtin_shufflevector(z, w, 0, 1, 2, 3, 4, 5, 6, 7));
+            pb.dx[j][tp] = okd[j][tp] ? d[j][tp] : 0.0f;
+        }
 }
 
 // Per-lane view of a tile image.  Chunk c covers blocks 4c..4c+3 of the 16
