@@ -292,16 +292,16 @@ static size_t select_lds(int n, int E) {
 // accumulator per (expert, token) of its wavefront, each the FMA chain of
 // k_route below (element 64c + L over chunks c in order, the same bits), and
 // loads a chunk's element of each of its router rows and token rows once for
-// all of those chains, every load of a row in flight at once.  With q set,
+// all of those chains, the loads of U chunks of every row in flight at once
+// (one pass over a 2880-wide row at U = 45).  With q set,
 // the workgroups of a token group also quantize its rows of x to Q8_0 (a
 // half-wave per block).
-template <int EW, int TT>
+template <int EW, int TT, int U>
 __global__ __launch_bounds__(kWG) void k_route_tile(const float *__restrict__ router, const void *bias,
                                                     int bias_type, const float *__restrict__ x, int B, int H, int E,
                                                     float *__restrict__ logits, QuantOut q) {
-    static_assert(EW == 1 || EW == 2, "wavefronts of one or two experts");
-    constexpr int TW = EW * TT;  // tokens per workgroup
-    constexpr int U = 45;        // chunks per pass of loads
+    static_assert(EW == 1 || EW == 2 || EW == 4, "wavefronts of one, two or four experts");
+    constexpr int TW = EW * TT;  // tokens per workgroup (U: chunks per pass of loads)
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int tg0 = blockIdx.y * TW;
     if (q.codes || q.blocks34) {
@@ -335,9 +335,8 @@ __global__ __launch_bounds__(kWG) void k_route_tile(const float *__restrict__ ro
     for (int i = 0; i < EW; i++)
 #pragma unroll
         for (int j = 0; j < TT; j++) acc[i][j] = 0.0f;
-    // passes of U chunks with every load of a pass in flight at once (one
-    // pass over a 2880-wide row); chunks past the row load its last chunk
-    // and are not multiplied
+    // passes of U chunks with every load of a pass in flight at once;
+    // chunks past the row load its last chunk and are not multiplied
     const int nfull = H / 64;
     for (int c0 = 0; c0 < nfull; c0 += U) {
         float wv[U][EW], xv[U][TT];
@@ -522,17 +521,33 @@ hipError_t launch_route(hipStream_t s, const float *router, const void *bias, in
                         const float *x, int batch, int hidden, int experts, float *logits,
                         const QuantOut &q) {
     if (batch > kRouteLdsMaxBatch) {
-        // from 32 tokens, wavefronts of (2 experts, 2 tokens): 512 workgroups
-        // at 64 tokens and 128 experts, two waves per SIMD, one round;
-        // below, of (1 expert, 1 token), so few tokens still fill the CUs
-        if (batch >= 32) {
+        // Every wavefront loads its router rows and token rows whole, so a
+        // wider (experts x tokens) tile reads fewer bytes per logit from the
+        // caches (rows per logit: 1 at 2 x 2, 0.75 at 2 x 4, 0.5 at 4 x 4)
+        // but makes fewer workgroups.  Measured per router launch at 128
+        // experts (us, 2 x 2 / 2 x 4 / 4 x 4): 64 tokens 11.2 / 13.2 / 18.6,
+        // 96: 16.4 / 15.0 / 19.2, 192: 24.9 / 18.5 / 22.6, 256: 33.3 / 27.0
+        // / 24.9, 512: 58.8 / 42.0 / 42.1, 1024: 108 / 74 / 68.  So from 256
+        // tokens 4 x 4 in passes of 15 chunks, from 80 tokens 2 x 4 in passes
+        // of 23, from 32 tokens 2 x 2 (512 workgroups at 64 tokens, one
+        // round); below, (1 expert, 1 token), so few tokens still fill the
+        // CUs.
+        if (batch >= 256) {
+            dim3 grid((experts + 3) / 4, (batch + 15) / 16);
+            hipLaunchKernelGGL((k_route_tile<4, 4, 15>), grid, dim3(kWG), 0, s, router, bias, bias_type, x, batch,
+                               hidden, experts, logits, q);
+        } else if (batch >= 80) {
+            dim3 grid((experts + 3) / 4, (batch + 7) / 8);
+            hipLaunchKernelGGL((k_route_tile<2, 4, 23>), grid, dim3(kWG), 0, s, router, bias, bias_type, x, batch,
+                               hidden, experts, logits, q);
+        } else if (batch >= 32) {
             dim3 grid((experts + 3) / 4, (batch + 3) / 4);
-            hipLaunchKernelGGL((k_route_tile<2, 2>), grid, dim3(kWG), 0, s, router, bias, bias_type, x, batch, hidden,
-                               experts, logits, q);
+            hipLaunchKernelGGL((k_route_tile<2, 2, 45>), grid, dim3(kWG), 0, s, router, bias, bias_type, x, batch,
+                               hidden, experts, logits, q);
         } else {
             dim3 grid((experts + 3) / 4, batch);
-            hipLaunchKernelGGL((k_route_tile<1, 1>), grid, dim3(kWG), 0, s, router, bias, bias_type, x, batch, hidden,
-                               experts, logits, q);
+            hipLaunchKernelGGL((k_route_tile<1, 1, 45>), grid, dim3(kWG), 0, s, router, bias, bias_type, x, batch,
+                               hidden, experts, logits, q);
         }
         return hipGetLastError();
     }
