@@ -269,8 +269,9 @@ def test_q40_bias_residual(gpu_ctx, O, input_dim, output_dim, batch, btype):
     assert_close(got, ref.reshape(-1), what="q40+bias")
 
 
-@pytest.mark.parametrize("hidden,batch", [(2880, 1), (2880, 19), (2880, 40), (2880, 64), (2880, 200), (96, 3),
-                                          (32, 2), (96, 17), (32, 70), (160, 37)])
+@pytest.mark.parametrize("hidden,batch", [(2880, 1), (2880, 19), (2880, 40), (2880, 64), (2880, 80), (2880, 200),
+                                          (2880, 300), (96, 3), (32, 2), (96, 17), (32, 70), (160, 37), (96, 255),
+                                          (160, 513)])
 def test_router_logits_bit_exact(gpu_ctx, O, hidden, batch):
     import torch
 
