@@ -531,7 +531,8 @@ hipError_t launch_route(hipStream_t s, const float *router, const void *bias, in
         // tokens 4 x 4 in passes of 15 chunks, from 80 tokens 2 x 4 in passes
         // of 23, from 32 tokens 2 x 2 (512 workgroups at 64 tokens, one
         // round); below, (1 expert, 1 token), so few tokens still fill the
-        // CUs.
+        // CUs, in passes of 23 chunks (76 VGPRs: 7.1-7.5 against 7.9 us at
+        // 8 tokens, 9.6-9.9 against 10.7-12.6 at 31, with one pass of 45).
         if (batch >= 256) {
             dim3 grid((experts + 3) / 4, (batch + 15) / 16);
             hipLaunchKernelGGL((k_route_tile<4, 4, 15>), grid, dim3(kWG), 0, s, router, bias, bias_type, x, batch,
@@ -546,7 +547,7 @@ hipError_t launch_route(hipStream_t s, const float *router, const void *bias, in
                                hidden, experts, logits, q);
         } else {
             dim3 grid((experts + 3) / 4, batch);
-            hipLaunchKernelGGL((k_route_tile<1, 1, 45>), grid, dim3(kWG), 0, s, router, bias, bias_type, x, batch,
+            hipLaunchKernelGGL((k_route_tile<1, 1, 23>), grid, dim3(kWG), 0, s, router, bias, bias_type, x, batch,
                                hidden, experts, logits, q);
         }
         return hipGetLastError();
