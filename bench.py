@@ -39,6 +39,8 @@ MFMA_PROFILE = os.path.join(ROOT, "profiles", "k_mx_gemm_prefill_b512_hot.md")
 # grouped-GEMM policy of the library's default (spt_abi.hip: kGemmMinGroup,
 # kGemmMinSelections; select: items must fill half the device)
 GEMM_MIN_GROUP, GEMM_MIN_SELECTIONS = 9, 384
+# selections per grouped-GEMV weight pass (spt_kernels.h: kGemvTokens)
+GEMV_TOKENS = 4
 # host threads for the CPU baseline: the box's CPU share per GPU
 CPU_SHARE = 16
 
@@ -91,6 +93,8 @@ def parse():
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill workloads")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the prefill workloads (one layer resident; for counter passes)")
+    ap.add_argument("--prefill-workloads", default="zipf_b32,hot_b512",
+                    help="which prefill workloads run (comma-separated; for counter passes)")
     ap.add_argument("--no-lm-head", action="store_true", help="skip the Q8_0 LM head")
     ap.add_argument("--q40-only", action="store_true", help="only the Q4_0 attention projections (for profiles)")
     ap.add_argument("--no-graph", action="store_true",
@@ -357,7 +361,10 @@ def prefill(args, ctx, dl, shp, W, stream, reps=20):
 
     H, D, E, k = shp.hidden, shp.expert_dim, shp.experts, shp.topk
     out = {}
+    wanted = set(args.prefill_workloads.split(","))
     for name, B, hot, seed in (("zipf_b32", 32, 0.0, 2), ("hot_b512", 512, 0.25, 4)):
+        if name not in wanted:
+            continue
         logits = torch.from_numpy(synth.zipf_logits(synth.stream_key(seed, 99), B, E, 1.1,
                                                     hot_fraction=hot, hot_expert=17)).cuda()
         x = torch.from_numpy(W.x_tokens(seed, 0, B, H)).cuda()
@@ -399,10 +406,17 @@ def prefill(args, ctx, dl, shp, W, stream, reps=20):
         ctx.enable_timing(False)
         kus = {kk: round(v[0] / reps * 1e3, 1) for kk, v in kt.items() if v[1]}
         wbytes = distinct * (2 * shp.gate_bytes + shp.down_bytes)
+        # the grouped GEMV streams each of its experts once per pass of
+        # GEMV_TOKENS selections: its weight bytes once, and as streamed
+        gv = c[(c > 0) & ~((c >= GEMM_MIN_GROUP) & gemm_on)]
+        gv_passes = int(np.sum((gv + GEMV_TOKENS - 1) // GEMV_TOKENS))
         res = {
             "batch": B, "ms_per_layer": round(ms, 4), "tokens_per_s": round(B / (ms / 1e3), 1),
             "distinct_experts": distinct, "largest_group": int(c.max()),
             "weight_gb": round(wbytes / 1e9, 4), "weight_gbps": round(wbytes / (ms / 1e3) / 1e9, 1),
+            "gemv_experts": int(gv.size), "gemv_passes": gv_passes,
+            "gemv_gate_up_bytes_once": int(gv.size * 2 * shp.gate_bytes),
+            "gemv_gate_up_bytes_streamed": int(gv_passes * 2 * shp.gate_bytes),
             "kernel_us": kus, "gemm_experts": int(len(big)) if gemm_on else 0, "gemm_selections": gemm_sel,
         }
         gemm_us = kus.get("gate_up_gemm", 0.0) + kus.get("down_gemm", 0.0)
