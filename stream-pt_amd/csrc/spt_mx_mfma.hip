@@ -58,10 +58,10 @@ struct TileRegs {
     u32x4v q[4 * kWaveGroups];
 };
 
-template <int G>
+template <int G, int K0, int K1>
 __device__ inline void tile_issue(TileRegs &t, uint32_t vo, rsrc_t r, uint32_t so) {
 #pragma unroll
-    for (int k = 0; k < 4; k++)
+    for (int k = K0; k < K1; k++)
         t.q[4 * G + k] = __builtin_bit_cast(u32x4v, __builtin_amdgcn_raw_buffer_load_b128(r, vo + 1024u * k, so, 2));
 }
 
@@ -172,9 +172,10 @@ __device__ inline int pick4(const int (&v)[kTokPerPass], int t) {
 // Each step: wait for this wave's prefetched groups; advance the cursor to
 // the next unit; barrier (every wave is past the previous unit's multiply);
 // write the groups to LDS, issuing the next unit's first load group after
-// the first; barrier; multiply (tiles 0-1, then 2-3), issuing the second
-// and third groups before each tile pair and flushing a full stage set
-// after the second; write the partial sums.  Measured alternatives, all
+// the first; barrier; multiply (tiles 0-1, then 2-3), issuing half of the
+// second group before tiles 0-1 and half after them, the third likewise
+// around tiles 2-3, and flushing a full stage set after the second group's
+// first half; write the partial sums.  Measured alternatives, all
 // slower for gate/up at 64 tokens: one wave role loading and another
 // multiplying (208 us against 190 us at the time: one multiplying wave per
 // SIMD leaves the LDS and MFMA latencies exposed), and tile pairs streamed
@@ -311,13 +312,17 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(2))) void k
     uint32_t na0 = 0u;
     bool nxt_ok = false;
     const uint32_t vo = 16u * (uint32_t)lane;
-    // local group G of the next tile's loads (G a compile-time constant, so
-    // every issue block writes fixed registers)
-    auto issue = [&](auto gc) {
-        constexpr int G = decltype(gc)::value;
-        static_assert(G < kWaveGroups, "group");
-        tile_issue<G>(tr, vo, nrs, nxt_ok && G < gmine ? na0 + 4096u * G : kPastRange);
+    // loads K0 .. K1-1 of local group G of the next tile's loads (compile-
+    // time constants, so every issue block writes fixed registers)
+    auto issue = [&](auto gc, auto k0, auto k1) {
+        constexpr int G = decltype(gc)::value, K0 = decltype(k0)::value, K1 = decltype(k1)::value;
+        static_assert(G < kWaveGroups && 0 <= K0 && K0 < K1 && K1 <= 4, "group");
+        tile_issue<G, K0, K1>(tr, vo, nrs, nxt_ok && G < gmine ? na0 + 4096u * G : kPastRange);
     };
+    using C0 = std::integral_constant<int, 0>;
+    using C1 = std::integral_constant<int, 1>;
+    using C2 = std::integral_constant<int, 2>;
+    using C4 = std::integral_constant<int, 4>;
     uint32_t b0r = 0u, b1r = 0u;
     auto prefetch = [&](const Cursor &c) {
         const uint32_t brow = (uint32_t)c.e * (uint32_t)a.rows + (uint32_t)(c.tile * tile_rows + brow_l);
@@ -448,9 +453,9 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(2))) void k
     int n_staged = 0, cur_set = 0, pending = -1;
     prefetch(cur);
     static_assert(kWaveGroups == 3, "issue list below");
-    issue(std::integral_constant<int, 0>{});
-    issue(std::integral_constant<int, 1>{});
-    issue(std::integral_constant<int, 2>{});
+    issue(C0{}, C0{}, C4{});
+    issue(C1{}, C0{}, C4{});
+    issue(C2{}, C0{}, C4{});
     cur.p = MODE == kRows ? q0 : table ? p0 : q0 - rt.pass_off[slot0];
     slot_info<MODE>(a, rt, cur);
     PassTokens npt = pass_tokens<MODE>(a, rt, cur);  // tokens of the unit in the registers
@@ -494,7 +499,7 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(2))) void k
         }
         // the first group's registers are free once its stores are done
         tile_stored(tr);
-        issue(std::integral_constant<int, 0>{});
+        issue(C0{}, C0{}, C4{});
         if (row0_load < a.rows) {
             if (gmine > 1) tile_store<1>(img_lds + 4096u, tr);
             if (gmine > 2) tile_store<2>(img_lds + 8192u, tr);
@@ -545,24 +550,32 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(2))) void k
                 for (int p = 0; p < 2; p++)
 #pragma unroll
                     for (int i = 0; i < 4; i++) acc[h][p][i] = 0.0f;
-            // the next unit's second load group before the first tile
-            // pair's multiplies, the third before the second's (a wave
-            // stalls at a load's issue while its CU's memory queue is full;
-            // measured for gate/up at 64 tokens: both here 184 us, against
-            // 172 us)
+            // the next unit's second load group around the first tile
+            // pair's multiplies, the third around the second's: half of the
+            // group before, half after (a wave stalls at a load's issue
+            // while its CU's memory queue is full, so each stall holds up
+            // half as much of the multiply; measured for gate/up at 64
+            // tokens: 168.6 against 169.8 us with whole groups before, 169.7
+            // with whole groups after, 180 with the first group and half the
+            // second before the first pair; both whole groups before the
+            // first pair: 184 against 172 us)
             if (r0 == 0) {
-                issue(std::integral_constant<int, 1>{});
+                issue(C1{}, C0{}, C2{});
                 if (pending >= 0) {
                     flush(kStage * pending, kStage);
                     pending = -1;
                 }
             } else {
-                issue(std::integral_constant<int, 2>{});
+                issue(C2{}, C0{}, C2{});
             }
             if (npair == 2)
                 tile_pair<2>(tv, r0, wave, nc, mask_last, nb, L, pb, acc);
             else
                 tile_pair<1>(tv, r0, wave, nc, mask_last, nb, L, pb, acc);
+            if (r0 == 0)
+                issue(C1{}, C2{}, C4{});
+            else
+                issue(C2{}, C2{}, C4{});
 #pragma unroll
             for (int h = 0; h < 2; h++) {
                 const int r = r0 + h;
