@@ -41,7 +41,7 @@ MFMA_PROFILE = os.path.join(ROOT, "profiles", "k_mx_gemm_prefill_b512_hot.md")
 GEMM_MIN_GROUP, GEMM_MIN_SELECTIONS = 9, 384
 # selections per grouped-GEMV weight pass (spt_kernels.h: kGemvTokens)
 GEMV_TOKENS = 4
-# host threads for the CPU baseline: the box's CPU share per GPU
+# host threads for the CPU baseline: the host's CPU share per GPU
 CPU_SHARE = 16
 
 
@@ -626,7 +626,7 @@ def cpu_baseline(args, shp, W):
     reference's AVX2/FMA order, rows split over threads like the Go worker
     pool (forward/workers_quant.go:42-52), weights pre-faulted in RAM (1.4 GB
     for layer 0's ~108 experts, far beyond the last-level cache).  Timed with
-    the box's CPU share of threads (16 per GPU, capped by the affinity mask)
+    the host's CPU share of threads (16 per GPU, capped by the affinity mask)
     and with one thread."""
     import numpy as np
 

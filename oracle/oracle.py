@@ -1,8 +1,8 @@
 """ctypes wrapper of the CPU oracle (oracle/liboracle.so).
 
 TEST INFRASTRUCTURE ONLY: the CPU restatement of Stream-PT's quantized MoE
-path, used as the checker by tests/, by ``__graft_entry__.smoke()`` and as the
-timed CPU baseline by bench.py.  The product library never imports it.
+path: the results tests/ and ``__graft_entry__.smoke()`` compare the HIP
+library against, and the timed CPU baseline of bench.py.  The product library never imports it.
 
 Every function here wraps one C function of spt_oracle.c; the C file cites the
 reference Go source line each one follows.

@@ -3,10 +3,11 @@
  *
  * TEST INFRASTRUCTURE ONLY.  This library restates, on the CPU, the
  * algorithms of Stream-PT's forward package (pure Go, GOEXPERIMENT=simd) and
- * the build-defined Q8_0-activation variant that the HIP kernels implement.
- * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
- * load it, and only as the checker or as the timed CPU baseline; the product
- * library never links or calls it.
+ * the Q8_0-activation variant that the HIP kernels implement (activations
+ * quantized to Q8_0 before the integer block dots).  Only tests/,
+ * __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it, and
+ * only as the results to compare against or as the timed CPU baseline; the
+ * product library never links or calls it.
  *
  * Two families of functions:
  *   so_*_f32 : fp32-activation reference restatement.  Each one follows the
