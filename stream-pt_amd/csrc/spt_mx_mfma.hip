@@ -178,9 +178,12 @@ __device__ inline int pick4(const int (&v)[kTokPerPass], int t) {
 // first half; write the partial sums.  Measured alternatives, all
 // slower for gate/up at 64 tokens: one wave role loading and another
 // multiplying (208 us against 190 us at the time: one multiplying wave per
-// SIMD leaves the LDS and MFMA latencies exposed), and tile pairs streamed
-// by LDS DMA into a two-deep ring (370 us: in-flight bytes drop to zero at
-// every pair).
+// SIMD leaves the LDS and MFMA latencies exposed), tile pairs streamed by
+// LDS DMA into a two-deep ring (370 us: in-flight bytes drop to zero at
+// every pair), and tile pairs as the step with two pair images in LDS and
+// two pairs of loads in these registers (181 us against 168.5 us: with two
+// pairs in flight every issue finds the CU's memory queue full, and the
+// issuing wave stalls before its multiply).
 template <int MODE>
 __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(2))) void k_mx_mfma(MxMfmaArgs a, const int32_t *__restrict__ r_active,
                                                                       const int32_t *__restrict__ r_offsets,
