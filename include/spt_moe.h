@@ -141,8 +141,8 @@ int spt_ctx_set_gemm_min_group(struct spt_ctx *ctx, int32_t min_group);
  * used <= 4, and no group on the grouped GEMM) take the decode path: the
  * top-k inside the gate/up launch (a workgroup per selection) and the
  * weighted combine inside the down launch, two launches after the router.
- * 0 restores the default (16 selections: the measured crossover with the
- * grouped GEMV is between 4 and 8 tokens at top-4); a negative value turns the path
+ * 0 restores the default (8 selections: the measured crossover with the
+ * grouped GEMV is between 2 and 3 tokens at top-4); a negative value turns the path
  * off (every batch through select, the grouped GEMV and combine).  Results
  * are the same within the fp32 tolerance either way; ids, weights, lists
  * and the Q8_0 stages are identical.  No reference counterpart (a launch

@@ -410,8 +410,12 @@ constexpr int kGemmMinGroup = 9;
 constexpr int kGemmMinSelections = 384;
 // Batches of up to this many selections (topk <= 4, no GEMM group) take the
 // decode path: top-k inside the gate/up launch, combine inside the down
-// launch, a workgroup per selection (spt_mx_decode.hip).
-constexpr int kDecodeMaxSelections = 16;
+// launch, a workgroup per selection (spt_mx_decode.hip).  Measured on the
+// 36-layer step at GPT-OSS-120B shape (top-4, HIP graph replay, decode path
+// against the grouped GEMV): 1 token 0.925 / 1.317 ms, 2 tokens 1.403 /
+// 1.619, 3 tokens 2.000 / 1.975, 4 tokens 2.245 / 2.179, 6 tokens 3.220 /
+// 2.771.
+constexpr int kDecodeMaxSelections = 8;
 
 // Scratch layout of one forwardMoEBatch call (offsets into the arena).
 struct MoELayout {

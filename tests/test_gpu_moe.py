@@ -77,8 +77,9 @@ def _bias_vec(lay, name, e, dim, O):
 # (grouped-GEMM threshold, decode-path limit) of each path: the library's
 # default (small batches on the two-launch decode path), every group through
 # the grouped GEMM, every group through GEMVs (the decode path where it
-# applies), and the grouped GEMV with the decode path off.
-PATHS = {"default": (0, 0), "gemm": (1, 0), "gemv": (1 << 30, 0), "grouped": (1 << 30, -1)}
+# applies), the grouped GEMV with the decode path off, and the decode path
+# up to 16 selections (beyond the default limit, as a caller may set it).
+PATHS = {"default": (0, 0), "gemm": (1, 0), "gemv": (1 << 30, 0), "grouped": (1 << 30, -1), "decode": (1 << 30, 16)}
 
 
 class gemm_path:
@@ -259,7 +260,7 @@ def test_moe_prefill_hot_expert(gpu_ctx, O):
     check_stagewise(O, lay, x, batch, g, logits_in=logits, sample=sorted(sample))
 
 
-@pytest.mark.parametrize("path", ["default", "gemm", "gemv", "grouped"])
+@pytest.mark.parametrize("path", ["default", "gemm", "gemv", "grouped", "decode"])
 @pytest.mark.parametrize("experts,topk", [(1, 1), (4, 2), (7, 7), (8, 2)])
 @pytest.mark.parametrize("bias_type", [-1, 0, 1, 30])
 @pytest.mark.parametrize("mode", ROUTER_MODES)
@@ -304,12 +305,13 @@ def test_moe_special_scales(gpu_ctx, O, scale, path):
             assert_close(g["out"], want, what=f"scale {scale} batch {batch}")
 
 
-@pytest.mark.parametrize("batch,path", [(8, "default"), (8, "grouped"), (16, "default"), (64, "default")])
+@pytest.mark.parametrize("batch,path", [(2, "default"), (4, "default"), (4, "decode"), (8, "default"), (8, "grouped"),
+                                        (16, "default"), (64, "default")])
 def test_moe_decode_continuous_batching(gpu_ctx, O, batch, path):
     """The continuous-batching decode step at GPT-OSS-120B shape: two MoE
     layers resident at once, `batch` tokens (one per sequence) each routed
     by the layer's own router (N(0,0.02) weights over RMS-normalised N(0,1)
-    tokens, so logits are about N(0,1)), through the default path, the two
+    tokens, so logits are about N(0,1)), through the given path, the two
     layers' calls enqueued back to back as in a decode step.  Every stage
     of every selection is checked against the oracle."""
     import torch
