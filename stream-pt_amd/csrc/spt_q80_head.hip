@@ -13,12 +13,22 @@
 // v_fma_mix_f32(q, d, -0.0) forms it from the fp16 bits in one instruction
 // (adding -0.0 leaves every product, -0.0 included, unchanged).
 //
-// Memory: the matrix is read once.  A wave takes tiles of 8 consecutive
+// Memory: the matrix is read once.  A wave takes tiles of 16 consecutive
 // rows (tiles w, w + W, ... of the grid's W waves) and walks each tile's K
-// in segments of kSeg blocks; a segment's 8 row windows are loaded into the
+// in segments of kSeg blocks; a segment's 16 row windows are loaded into the
 // wave's own LDS stage by LDS DMA, kBufs - 1 segments in flight while one is
 // multiplied.  x is staged once per workgroup in LDS.  The argmax form keeps
 // each wave's best (logit, row) and a one-workgroup pass merges them.
+//
+// Ten waves per workgroup, one segment in flight each: a compute unit's
+// memory queue holds about 48 KB of loads, and a wave whose load finds it
+// full stalls at the issue instead of multiplying, so 10 x 6 KB in flight
+// keeps the queue full with few stalls (eight waves with two segments in
+// flight each: 126.9 us for the 201,088 x 2,880 head; one each: 124.5 us).
+// Ten waves also split that head's 12,568 tiles almost evenly (at most 5
+// per wave against 4.91 on average; with 8, 9, 11 or 12 waves the slowest
+// waves take 7, 6, 5 or 5 against 6.14, 5.45, 4.46 or 4.09): 121.5 us, and
+// 133.6, 128.3 and 132.3 us with 9, 11 and 12 waves.
 #include "spt_device.h"
 #include "spt_kernels.h"
 
@@ -26,7 +36,7 @@ namespace spt {
 
 namespace {
 
-constexpr int kWaves = 8;
+constexpr int kWaves = 10;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kRowsPerLane = 2;                                       // rows rg and rg + 8 share x reads
 constexpr int kTileRows = 8 * kRowsPerLane;                           // 8 lanes per row
@@ -35,7 +45,7 @@ constexpr int kPieces = (15 + kSeg * kQ80Block + 15) / 16;            // 16-byte
 constexpr int kSlot = 16 * kPieces;                                   // LDS bytes per row in a stage
 constexpr int kSegInstr = (kTileRows * kPieces + 63) / 64;            // LDS DMA loads per segment
 constexpr int kStageBytes = 1024 * kSegInstr;
-constexpr int kBufs = 3;
+constexpr int kBufs = 2;
 constexpr int kGroup = 3;                                             // blocks per LDS read group
 constexpr uint32_t kOOR = 0xFFFFFFF0u;                                // past every descriptor's range
 static_assert(kSeg % kGroup == 0, "segment of whole groups");
