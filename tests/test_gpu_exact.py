@@ -130,11 +130,11 @@ def exact_layer():
     del keep
 
 
-@pytest.mark.parametrize("path,batch", [("default", 1), ("default", 3), ("grouped", 1), ("grouped", 5),
-                                        ("gemm", 5), ("gemm", 37), ("default", 64)])
+@pytest.mark.parametrize("path,batch", [("default", 1), ("default", 2), ("decode", 3), ("default", 3), ("grouped", 1),
+                                        ("grouped", 5), ("gemm", 5), ("gemm", 37), ("default", 64)])
 def test_moe_kernels_exact(gpu_ctx, O, exact_layer, path, batch):
-    """Decode kernels (k_dec_gate_up / k_dec_down: up to 16 selections on the
-    default path), the grouped GEMV (k_mx_mfma kGateUp / kDown) and the
+    """Decode kernels (k_dec_gate_up / k_dec_down: up to 8 selections on the
+    default path, 12 when forced), the grouped GEMV (k_mx_mfma kGateUp / kDown) and the
     grouped GEMM (k_mx_gemm, every group forced onto it): the gate and up
     taps equal the integer form over the full 2,880-input rows, every
     selection's down result the single rounding of its one block, and the
