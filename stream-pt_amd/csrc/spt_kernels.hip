@@ -384,7 +384,10 @@ __global__ __launch_bounds__(kWG) void k_route_tile(const float *__restrict__ ro
 constexpr int kRouteSeg = 4096;
 // Up to this many tokens the router spreads over one workgroup per (expert,
 // token) with LDS staging (latency); beyond, k_route_tile (throughput).
-constexpr int kRouteLdsMaxBatch = 4;
+// Measured on the 36-layer step (ms, this form against the tiled one): 2
+// tokens 1.401 / 1.433, 4: 2.176 / 2.212, 6: 2.764 / 2.780, 8: 3.230 /
+// 3.235, 12: 4.167 / 4.082, 16: 4.873 / 4.780.
+constexpr int kRouteLdsMaxBatch = 8;
 template <bool MULTI>  // MULTI: H > kRouteSeg, segments in a loop; else one segment, straight-line
 __global__ __launch_bounds__(64) void k_route(const float *__restrict__ router, const void *bias, int bias_type,
                                               const float *__restrict__ x, int H, int E,
@@ -531,8 +534,9 @@ hipError_t launch_route(hipStream_t s, const float *router, const void *bias, in
         // tokens 4 x 4 in passes of 15 chunks, from 80 tokens 2 x 4 in passes
         // of 23, from 32 tokens 2 x 2 (512 workgroups at 64 tokens, one
         // round); below, (1 expert, 1 token), so few tokens still fill the
-        // CUs, in passes of 23 chunks (76 VGPRs: 7.1-7.5 against 7.9 us at
-        // 8 tokens, 9.6-9.9 against 10.7-12.6 at 31, with one pass of 45).
+        // CUs, in passes of 23 chunks (76 VGPRs; measured while this form
+        // also took 8 tokens: 7.1-7.5 against 7.9 us there, and 9.6-9.9
+        // against 10.7-12.6 at 31, with one pass of 45).
         if (batch >= 256) {
             dim3 grid((experts + 3) / 4, (batch + 15) / 16);
             hipLaunchKernelGGL((k_route_tile<4, 4, 15>), grid, dim3(kWG), 0, s, router, bias, bias_type, x, batch,
