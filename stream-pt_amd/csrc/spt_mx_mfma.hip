@@ -316,11 +316,17 @@ __global__ __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(2))) void k
     bool nxt_ok = false;
     const uint32_t vo = 16u * (uint32_t)lane;
     // loads K0 .. K1-1 of local group G of the next tile's loads (compile-
-    // time constants, so every issue block writes fixed registers)
+    // time constants, so every issue block writes fixed registers).  The
+    // wave issues them at the highest wave priority, so they go out ahead of
+    // the other waves' MFMA and LDS work (gate/up at 64 tokens, four runs
+    // each, alternating builds: 167.6-168.0 against 168.3-168.6 us; priority
+    // 2: 168.0-168.5; priority 3 also over the image stores: 167.3-168.7).
     auto issue = [&](auto gc, auto k0, auto k1) {
         constexpr int G = decltype(gc)::value, K0 = decltype(k0)::value, K1 = decltype(k1)::value;
         static_assert(G < kWaveGroups && 0 <= K0 && K0 < K1 && K1 <= 4, "group");
+        __builtin_amdgcn_s_setprio(3);
         tile_issue<G, K0, K1>(tr, vo, nrs, nxt_ok && G < gmine ? na0 + 4096u * G : kPastRange);
+        __builtin_amdgcn_s_setprio(0);
     };
     using C0 = std::integral_constant<int, 0>;
     using C1 = std::integral_constant<int, 1>;
