@@ -392,3 +392,45 @@ def spt_split(rows, ntok):
     narrow projections below 1024 rows always)."""
     tiles = ((rows + 63) // 64) * ((ntok + 63) // 64)
     return ntok >= 32 and (rows < 1024 or tiles < 256)
+
+
+def _at_offset(raw, off):
+    """raw's bytes on the device starting `off` bytes past a 256-byte
+    aligned allocation (with room past the end): the tensor base the C ABI
+    accepts for Q4_0 and Q8_0 data (2-byte aligned) without being 16-byte
+    aligned."""
+    import torch
+
+    buf = torch.zeros(raw.size + 64, dtype=torch.uint8, device="cuda")
+    buf[off:off + raw.size].copy_(torch.from_numpy(np.ascontiguousarray(raw)))
+    return buf, buf.data_ptr() + off
+
+
+@pytest.mark.parametrize("off", [2, 6, 14])
+@pytest.mark.parametrize("batch", [1, 8, 70, 300])
+def test_q40_unaligned_base(gpu_ctx, O, off, batch):
+    """Every Q4_0 launch form (1 token: the few-token launch, 8: the tiled
+    MFMA form, 70 and 300: the GEMM) on a weight base 2, 6 or 14 bytes past
+    a 16-byte boundary gives the same bits as on an aligned base, and stays
+    within tolerance of the oracle."""
+    import torch
+
+    import spt
+    from spt import synth
+
+    din, dout = 2880, 512
+    print(f"q40 base +{off} batch {batch}", flush=True)
+    w = synth.q40_bytes(synth.stream_key(8, dout + off), dout, din)
+    x = synth.normal(synth.stream_key(9, batch + off), batch * din)
+    xd = _dev(x)
+    outs = []
+    for o in (0, off):
+        buf, ptr = _at_offset(w, o)
+        t = spt.Tensor.make("attn", spt.TYPE_Q4_0, [din, dout], ptr, w.size)
+        y = torch.full((batch * dout,), 12345.0, dtype=torch.float32, device="cuda")
+        gpu_ctx.mul_q40_batch_into(t, xd, y, batch)
+        torch.cuda.synchronize()
+        outs.append(y.cpu().numpy())
+        del buf
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    assert_close(outs[1], O.mul_q40_q8(w, x, din, dout, batch), what="q40 unaligned base")

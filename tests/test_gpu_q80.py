@@ -160,3 +160,29 @@ def test_q80_lm_head_full(gpu_ctx, O):
     y, tok, logit = _run(gpu_ctx, w, x, input_dim, rows)
     _same_bits(y, O.mul_q80_f32(w, x, input_dim, rows, threads=16))
     _same_argmax((tok, logit), O.mul_q80_argmax(w, x, input_dim, rows))
+
+
+@pytest.mark.parametrize("off", [2, 6, 14])
+@pytest.mark.parametrize("input_dim,output_dim", [(2880, 4099), (96, 17)])
+def test_q80_unaligned_base(gpu_ctx, O, off, input_dim, output_dim):
+    """A Q8_0 matrix whose base is 2, 6 or 14 bytes past a 16-byte boundary
+    (the C ABI requires only 2-byte alignment): logits and argmax bits equal
+    to the oracle's, as on an aligned base."""
+    import torch
+
+    import spt
+    from spt import synth
+
+    print(f"q80 base +{off} {input_dim}x{output_dim}", flush=True)
+    w = synth.q80_bytes(synth.stream_key(42, input_dim + off), output_dim, input_dim)
+    x = synth.normal(synth.stream_key(43, output_dim + off), input_dim)
+    buf = torch.zeros(w.size + 64, dtype=torch.uint8, device="cuda")
+    buf[off:off + w.size].copy_(torch.from_numpy(np.ascontiguousarray(w)))
+    t = spt.Tensor.make("output.weight", spt.TYPE_Q8_0, [input_dim, output_dim], buf.data_ptr() + off, w.size)
+    xd = _dev(x)
+    y = torch.full((output_dim,), 12345.0, dtype=torch.float32, device="cuda")
+    gpu_ctx.mul_q80_into(t, xd, y)
+    tok, logit = gpu_ctx.mul_q80_argmax(t, xd)
+    torch.cuda.synchronize()
+    _same_bits(y.cpu().numpy(), O.mul_q80_f32(w, x, input_dim, output_dim, threads=8))
+    _same_argmax((tok, np.float32(logit)), O.mul_q80_argmax(w, x, input_dim, output_dim))
