@@ -317,7 +317,8 @@ int spt_mul_mxfp4_expert(struct spt_ctx *ctx, const spt_tensor *w, const spt_ten
 
 /* forward.routeMoEBatch (forward/moe_batch.go:221-303, vector_amd64.go:11-56):
  * logits[t*E + e] = router_e . x_t + bias[e], in the reference's fp32
- * accumulation order. */
+ * accumulation order.  The router's F32 data must be 4-byte aligned (as
+ * in spt_forward_moe_batch); SPT_ERR_INVALID otherwise. */
 int spt_route_moe_batch(struct spt_ctx *ctx, const spt_tensor *router, const spt_tensor *bias,
                         const float *x_dev, int64_t batch, float *logits_dev);
 

@@ -366,6 +366,8 @@ int validate_moe(spt_ctx *ctx, const spt_moe_config *cfg, const spt_moe_layer *l
         router.shape[0] != (uint64_t)h || router.shape[1] != (uint64_t)E || router.nbytes != (uint64_t)rb)
         return fail(SPT_ERR_INVALID, "\"%s\": invalid F32 router shape or range", tname(&router));
     if (!router.data) return fail(SPT_ERR_INVALID, "\"%s\": tensor is not resident (nil data)", tname(&router));
+    if ((uintptr_t)router.data & 3u)
+        return fail(SPT_ERR_INVALID, "\"%s\": router data must be 4-byte aligned", tname(&router));
     int rc;
     if ((rc = validate_expert(&lw->ffn_gate_exps, h, d, E))) return rc;
     if ((rc = validate_expert(&lw->ffn_up_exps, h, d, E))) return rc;
@@ -1695,6 +1697,8 @@ int spt_route_moe_batch(spt_ctx *ctx, const spt_tensor *router, const spt_tensor
     if (router->type != SPT_TYPE_F32 || router->n_dims != 2 || !product(&rb, {h, E, 4}) ||
         router->nbytes != (uint64_t)rb || !router->data)
         return fail(SPT_ERR_INVALID, "\"%s\": invalid F32 router shape or range", tname(router));
+    if ((uintptr_t)router->data & 3u)
+        return fail(SPT_ERR_INVALID, "\"%s\": router data must be 4-byte aligned", tname(router));
     spt_tensor none{};
     if ((rc = validate_bias(bias ? bias : &none, E, 1))) return rc;
     if (h % 32 != 0) return fail(SPT_ERR_INVALID, "hidden dimension %lld is not a multiple of 32", (long long)h);

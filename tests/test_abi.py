@@ -79,6 +79,7 @@ CASES = {
     "router type": lambda c, w: setattr(w.ffn_gate_inp, "type", 1),
     "router shape": lambda c, w: setattr(w.ffn_gate_inp, "n_dims", 0),
     "router range": lambda c, w: setattr(w.ffn_gate_inp, "nbytes", w.ffn_gate_inp.nbytes - 1),
+    "router alignment": lambda c, w: setattr(w.ffn_gate_inp, "data", w.ffn_gate_inp.data + 2),
     "expert type": lambda c, w: setattr(w.ffn_up_exps, "type", 0),
     "expert shape": lambda c, w: w.ffn_gate_exps.shape.__setitem__(2, 5),
     "expert range": lambda c, w: setattr(w.ffn_down_exps, "nbytes", 0),
@@ -364,3 +365,15 @@ def test_moe_large_batches_run_as_slices(vctx):
         cfg, lw = _moe_descriptors(H=H, E=E, k=kk)
         assert _call_moe(vctx, cfg, lw, X, 2 * H, OUT, 2 * H, 2) == spt.ERR_INVALID
         assert b"experts used <= 16, experts <= 256" in spt.lib().spt_last_error()
+
+
+def test_route_router_alignment(vctx):
+    """spt_route_moe_batch rejects a router whose F32 data is not 4-byte
+    aligned before any launch; an aligned one reaches the device."""
+    rt = spt.Tensor.make("router", spt.TYPE_F32, [32, 4], 0x10000000, 32 * 4 * 4)
+    none = spt.Tensor.absent()
+    lib = spt.lib()
+    assert lib.spt_route_moe_batch(vctx.handle, C.byref(rt), C.byref(none), X, 1, OUT) == spt.ERR_DEVICE
+    rt = spt.Tensor.make("router", spt.TYPE_F32, [32, 4], 0x10000002, 32 * 4 * 4)
+    assert lib.spt_route_moe_batch(vctx.handle, C.byref(rt), C.byref(none), X, 1, OUT) == spt.ERR_INVALID
+    assert b"4-byte aligned" in lib.spt_last_error()
