@@ -434,3 +434,31 @@ def test_q40_unaligned_base(gpu_ctx, O, off, batch):
         del buf
     assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
     assert_close(outs[1], O.mul_q40_q8(w, x, din, dout, batch), what="q40 unaligned base")
+
+
+@pytest.mark.parametrize("off", [1, 3, 10])
+@pytest.mark.parametrize("batch", [1, 5])
+def test_mxfp4_expert_unaligned_base(gpu_ctx, O, off, batch):
+    """MXFP4 expert weights (17-byte blocks, accepted at any byte address)
+    whose base is 1, 3 or 10 bytes past a 16-byte boundary give the same
+    bits as on an aligned base."""
+    import torch
+
+    import spt
+    from spt import synth
+
+    din, dout, E, expert = 2880, 2880, 2, 1
+    print(f"mxfp4 base +{off} batch {batch}", flush=True)
+    w = synth.mxfp4_expert_bytes(synth.stream_key(5, din + off), 0, E * dout * (din // 32))
+    x = synth.normal(synth.stream_key(7, batch + off), batch * din)
+    xd = _dev(x)
+    outs = []
+    for o in (0, off):
+        buf, ptr = _at_offset(w, o)
+        t = spt.Tensor.make("w", spt.TYPE_MXFP4, [din, dout, E], ptr, w.size)
+        y = torch.full((batch * dout,), 12345.0, dtype=torch.float32, device="cuda")
+        gpu_ctx.mul_mxfp4_expert(t, None, expert, xd, y, batch)
+        torch.cuda.synchronize()
+        outs.append(y.cpu().numpy())
+        del buf
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
